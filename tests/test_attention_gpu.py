@@ -1,0 +1,201 @@
+"""GPU parity and invariance tests of the trie-verification attention kernel.
+
+Parity: every output element lies within the deterministic error bound of the
+reference's rounding points around the float64 answer
+(oracle.attention.attn_error_bound: 2^-9 relative error of the bf16 prompt
+probabilities + fp32 slack + 1 bf16 ulp), exactly the bound the oracle
+restatement of the reference kernel itself satisfies.  In bf16 ulps (at
+max(|exact|, rms/8)) the kernel must be at least as close to fp64 as the
+reference's own arithmetic: the fraction within 2 ulp and the mean ulp error
+may not be worse than the oracle's.
+
+Invariance (bitwise, torch.equal): trie rows vs 1-token calls along each
+root path, slot layouts, committed-token offsets, rows-per-wave settings.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as A
+from oracle import bf16, gen
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(x, dtype=torch.bfloat16):
+    t = torch.from_numpy(np.ascontiguousarray(x))
+    return t.to(dtype).cuda() if dtype is not None else t.cuda()
+
+
+def _run(case, **kw):
+    from respect_amd.kernels.attention import trie_attn
+    print(f"[attn] H={case.q.shape[0]} M={case.q.shape[1]} D={case.q.shape[2]} "
+          f"HK={case.kp.shape[0]} P={case.kp.shape[1]} NN={case.kn.shape[1]} {kw}", flush=True)
+    out = trie_attn(_dev(case.q), _dev(case.kp), _dev(case.vp), _dev(case.kn), _dev(case.vn),
+                    _dev(case.msk, None), case.sm_scale, **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+def _check_parity(case, out):
+    a = (case.q, case.kp, case.vp, case.kn, case.vn, case.msk, case.sm_scale)
+    o = _np(out)
+    assert np.isfinite(o).all()
+    e = A.attn_exact(*a)
+    bound = A.attn_error_bound(*a)
+    ratio = np.abs(o - e) / bound
+    assert ratio.max() <= 1.0, f"max err/bound {ratio.max():.3f}"
+    # ulp distances, measured at max(|exact|, rms/8) so near-zero outputs are not
+    # judged by a vanishing ulp.  The reference's own arithmetic (the oracle) is
+    # not within 2 ulp of fp64 everywhere (bf16 probabilities); the kernel must be
+    # at least as close to fp64 as the oracle is.
+    ref = A.attn_hyb(*a)
+    rms = np.sqrt((e ** 2).mean())
+    ud_k = bf16.ulp_diff(o, e, rms / 8)
+    ud_r = bf16.ulp_diff(ref, e, rms / 8)
+    ud_kr = bf16.ulp_diff(o, ref, rms / 8)
+    print(f"  err/bound max {ratio.max():.3f} (oracle {(np.abs(ref - e) / bound).max():.3f}); "
+          f"ulp vs fp64: <=2 {(ud_k <= 2).mean():.4f} (oracle {(ud_r <= 2).mean():.4f}) "
+          f"mean {ud_k.mean():.3f} (oracle {ud_r.mean():.3f}); vs oracle: <=2 {(ud_kr <= 2).mean():.4f} "
+          f"max {ud_kr.max():.2f} equal {(o == ref).mean():.4f}", flush=True)
+    assert (ud_k <= 2).mean() >= (ud_r <= 2).mean() - 0.01
+    assert ud_k.mean() <= 1.25 * ud_r.mean() + 0.05
+    return o
+
+
+def test_cfg1_parity():
+    c = gen.cfg1()
+    _check_parity(c, _run(c))
+
+
+def test_cfg2_parity():
+    c = gen.cfg2()
+    _check_parity(c, _run(c))
+
+
+def test_repeat_calls_are_bitwise_identical():
+    c = gen.cfg2(seed=5)
+    a = _run(c)
+    for _ in range(3):
+        assert torch.equal(_run(c), a)
+
+
+def test_rows_per_wave_does_not_change_bits():
+    """64 or 128 rows per prompt workgroup: a different work split, the same bits."""
+    c = gen.cfg2(seed=3)
+    assert torch.equal(_run(c, rows_per_wave=1), _run(c, rows_per_wave=2))
+
+
+@pytest.mark.parametrize("cfg", ["cfg1", "cfg2"])
+def test_trie_rows_equal_one_token_paths(cfg):
+    """Output preservation at kernel level: row i of the trie call equals the 1-row call
+    whose node segment is node i's root path laid out contiguously."""
+    c = getattr(gen, cfg)()
+    full = _run(c)
+    for i in range(len(c.tree.nodes)):
+        one = _run(gen.path_case(c, i))
+        assert torch.equal(one[:, 0], full[:, i]), f"node {i}"
+
+
+@pytest.mark.parametrize("base", [1, 7, 37, 100])
+def test_committed_offset_rows_equal_paths(base):
+    """Trie placed after `base` committed slots (all rows see them); tile edges of the
+    node segment fall mid-trie.  Each row equals its 1-token path call."""
+    c = gen.cfg2(seed=4, base=base)
+    _check_parity(c, full := _run(c))
+    rng = np.random.default_rng(base)
+    for i in rng.choice(len(c.tree.nodes), 12, replace=False):
+        one = _run(gen.path_case(c, int(i)))
+        assert torch.equal(one[:, 0], full[:, int(i)]), f"node {i}"
+
+
+def test_slot_layout_invariance_reference_shapes():
+    """tests/test_kernel_invariance.py:30-54 of the reference: 26 node values in slots
+    0-25 vs 0-17 + 200-207, H=32, HK=8, D=128, NP=300, NN=224, 64 query rows."""
+    rng = np.random.default_rng(0)
+    H, HK, D, NP, n, NN = 32, 8, 128, 300, 26, 224
+    q = gen.bf16_normal(rng, (H, 64, D))
+    kp = gen.bf16_normal(rng, (HK, NP, D))
+    vp = gen.bf16_normal(rng, (HK, NP, D))
+    kk = gen.bf16_normal(rng, (HK, n, D))
+    vv = gen.bf16_normal(rng, (HK, n, D))
+    outs = []
+    for slots in (list(range(n)), list(range(18)) + list(range(200, 208))):
+        kn = np.zeros((HK, NN, D), np.float32)
+        vn = np.zeros_like(kn)
+        msk = np.zeros((64, NN), bool)
+        kn[:, slots] = kk
+        vn[:, slots] = vv
+        msk[:, slots] = True
+        case = gen.AttnCase(q, kp, vp, kn, vn, msk, None, 0, D ** -0.5)
+        outs.append(_run(case))
+        _check_parity(case, outs[-1])
+    assert torch.equal(outs[0], outs[1])
+    # random layouts as well (run_kernel_order.py checks 5)
+    for seed in range(5):
+        slots = sorted(np.random.default_rng(seed).choice(NN, n, replace=False).tolist())
+        kn = np.zeros((HK, NN, D), np.float32)
+        vn = np.zeros_like(kn)
+        msk = np.zeros((64, NN), bool)
+        kn[:, slots] = kk
+        vn[:, slots] = vv
+        msk[:, slots] = True
+        assert torch.equal(_run(gen.AttnCase(q, kp, vp, kn, vn, msk, None, 0, D ** -0.5)), outs[0])
+
+
+@pytest.mark.parametrize("P", [1, 31, 33, 3086, 5000])
+def test_prompt_lengths(P):
+    c = gen.attn_case(6, 32, 8, 128, P, 3, 10, 0, 5, None, kv_scale=128 ** -0.5)
+    full = _run(c)
+    _check_parity(c, full)
+    for i in (0, len(c.tree.nodes) - 1):
+        assert torch.equal(_run(gen.path_case(c, i))[:, 0], full[:, i])
+
+
+@pytest.mark.parametrize("H,HK,D", [(8, 8, 64), (16, 8, 128), (32, 4, 128), (16, 2, 64), (32, 2, 128)])
+def test_gqa_and_head_dims(H, HK, D):
+    c = gen.attn_case(7, H, HK, D, 700, 3, 9, 0, 6, None)
+    full = _run(c)
+    _check_parity(c, full)
+    i = len(c.tree.nodes) - 1
+    assert torch.equal(_run(gen.path_case(c, i))[:, 0], full[:, i])
+
+
+def test_no_node_slots_and_no_prompt():
+    c = gen.cfg1()
+    # NN = 0: prompt only
+    c0 = gen.AttnCase(c.q, c.kp, c.vp, c.kn[:, :0], c.vn[:, :0], c.msk[:, :0], None, 0, c.sm_scale)
+    _check_parity(c0, _run(c0))
+    # P = 0: node segment only; every row allows its own slot
+    cp = gen.AttnCase(c.q, c.kp[:, :0], c.vp[:, :0], c.kn, c.vn, c.msk, c.tree, 0, c.sm_scale)
+    o = _np(_run(cp))
+    e = A.attn_exact(cp.q, cp.kp, cp.vp, cp.kn, cp.vn, cp.msk, cp.sm_scale)
+    assert np.abs(o - e).max() <= 2 * bf16.ulp(np.abs(e).max())
+
+
+def test_large_trie_128_nodes_long_prompt():
+    c = gen.attn_case(8, 32, 8, 128, 16384, 8, 32, 0, 32, 128, kv_scale=128 ** -0.5)
+    full = _run(c)
+    _check_parity(c, full)
+    for i in np.random.default_rng(0).choice(128, 8, replace=False):
+        assert torch.equal(_run(gen.path_case(c, int(i)))[:, 0], full[:, int(i)])
+
+
+def test_drop_in_signature_and_errors():
+    from respect_amd.kernels.attention import fused_attn_hyb
+    c = gen.cfg1()
+    args = [_dev(c.q), _dev(c.kp), _dev(c.vp), _dev(c.kn), _dev(c.vn), _dev(c.msk, None)]
+    out = fused_attn_hyb(*args, BM=64, BN=128, BNB=16, num_warps=4, num_stages=1)
+    assert out.shape == args[0].shape and out.dtype == torch.bfloat16
+    assert torch.equal(out, _run(c))
+    with pytest.raises(AssertionError):
+        fused_attn_hyb(*args, BNB=24)
+    with pytest.raises(TypeError):
+        fused_attn_hyb(args[0].float(), *args[1:])
+    # non-contiguous views are accepted (copied where the layout needs it)
+    qt = args[0].transpose(0, 1).contiguous().transpose(0, 1)
+    assert torch.equal(fused_attn_hyb(qt, *args[1:]), out)

@@ -1,0 +1,203 @@
+"""CPU checks that pin the oracle (no GPU).
+
+Known answers restated from the reference's tests/test_trie.py:11-49, closed
+forms for attention, and float64 brute force on tiny inputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as A
+from oracle import bf16, gen
+from oracle.trie import ancestry_from_parents, build_trie, greedy_token, root_paths, trie_ancestry, walk
+
+EOS = 99
+
+
+# ---------------------------------------------------------------- bf16 helpers
+
+def test_bf16_round_matches_torch():
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 2 ** 32, 200000, dtype=np.uint64).astype(np.uint32)
+    # every tie case: low 16 bits exactly 0x8000, both parities of bit 16
+    ties = (rng.integers(0, 2 ** 16, 4096, dtype=np.uint64).astype(np.uint32) << 16) | 0x8000
+    x = np.concatenate([bits, ties]).view(np.float32)
+    x = x[np.isfinite(x)]
+    ours = bf16.round_bf16(x)
+    ref = torch.from_numpy(x.copy()).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(ours.view(np.uint32), ref.view(np.uint32))
+
+
+def test_bf16_bits_roundtrip():
+    x = bf16.round_bf16(np.linspace(-5, 5, 1001, dtype=np.float32))
+    assert np.array_equal(bf16.from_bits(bf16.to_bits(x)), x)
+
+
+# ---------------------------------------------------------------- trie (test_trie.py:11-49)
+
+def test_shared_prefix_is_merged():
+    t = build_trie([(1, 2, 3, EOS), (1, 2, 4, EOS), (1, 2, 3, EOS)])
+    assert [n.token for n in t.nodes] == [1, 2, 3, EOS, 4, EOS]
+    assert len(t.seqs) == 2
+
+
+def test_parent_precedes_child_and_ancestry():
+    t = build_trie([(1, 2, 3), (1, 5)])
+    for i, n in enumerate(t.nodes):
+        assert n.parent is None or n.parent < i
+    a = trie_ancestry(t)
+    assert np.flatnonzero(a[3]).tolist() == [0, 3]
+
+
+def test_walk_accepts_until_mismatch():
+    t = build_trie([(1, 2, 3, EOS)])
+    target = {0: 2, 1: 9}
+    path, acc, rec = walk(t, 1, 128, EOS, lambda a, ch: target[ch])
+    assert acc == [1, 2] and rec == 9 and path == [0, 1]
+
+
+def test_walk_stops_at_eos():
+    t = build_trie([(1, EOS)])
+    path, acc, rec = walk(t, 1, 128, EOS, lambda a, ch: EOS)
+    assert acc == [1, EOS]
+
+
+def test_walk_cap_and_unknown_root():
+    t = build_trie([(1, 2, 3, 4)])
+    path, acc, rec = walk(t, 1, 2, EOS, lambda a, ch: t.nodes[ch].token + 1)
+    assert acc == [1, 2] and path == [0, 1]
+    path, acc, rec = walk(t, 7, 128, EOS, lambda a, ch: 0)
+    assert path == [] and acc == [] and rec == 7
+
+
+def test_ancestry_bruteforce_and_parent_array():
+    rng = np.random.default_rng(3)
+    for _ in range(20):
+        tree = gen.merged_trie(rng, 5, 7, 0, 6, vocab=4)
+        anc = trie_ancestry(tree)
+        assert np.array_equal(anc, ancestry_from_parents(tree.parents))
+        for i in range(len(tree.nodes)):
+            expect, cur = set(), i
+            while cur is not None:
+                expect.add(cur)
+                cur = tree.nodes[cur].parent
+            assert set(np.flatnonzero(anc[i]).tolist()) == expect
+        for p in root_paths(tree):
+            assert [tree.nodes[j].depth for j in p] == list(range(len(p)))
+
+
+def test_greedy_masks_action_vocab_and_breaks_ties_low():
+    logits = np.array([[0.0, 5.0, 5.0, 1.0], [9.0, 1.0, 2.0, 2.0]], np.float32)
+    assert greedy_token(logits, 0, 0).tolist() == [1, 0]
+    assert greedy_token(logits, 0, 1).tolist() == [1, 2]
+    assert greedy_token(logits, 1, 2).tolist() == [3, 0]
+
+
+def test_generated_tries_have_requested_size():
+    assert len(gen.cfg1().tree.nodes) == 16
+    c2 = gen.cfg2()
+    assert len(c2.tree.nodes) == 64
+    assert max(n.depth for n in c2.tree.nodes) <= 23
+
+
+# ---------------------------------------------------------------- attention oracle
+
+def _small(seed=0, H=4, HK=2, D=16, P=40, M=6, NN=32, p_allow=0.4):
+    rng = np.random.default_rng(seed)
+    q = gen.bf16_normal(rng, (H, M, D))
+    kp = gen.bf16_normal(rng, (HK, P, D))
+    vp = gen.bf16_normal(rng, (HK, P, D))
+    kn = gen.bf16_normal(rng, (HK, NN, D))
+    vn = gen.bf16_normal(rng, (HK, NN, D))
+    msk = rng.random((M, NN)) < p_allow
+    return q, kp, vp, kn, vn, msk
+
+
+def test_exact_matches_rowwise_bruteforce():
+    args = _small()
+    assert np.allclose(A.attn_exact(*args), A.attn_rows_bruteforce(*args), rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_hyb_close_to_exact(seed):
+    args = _small(seed, P=300)
+    o = A.attn_hyb(*args)
+    e = A.attn_exact(*args)
+    bound = A.attn_error_bound(*args)
+    assert (np.abs(o - e) <= bound).all()
+    # A plausible slip -- dropping the node segment, a wrong scale, or p not
+    # rounded where the reference rounds it -- breaks the bound somewhere.
+    q, kp, vp, kn, vn, msk = args
+    bad = A.attn_hyb(q, kp, vp, kn, vn, np.zeros_like(msk))
+    assert (np.abs(bad - e) > bound).mean() > 0.2
+    bad = A.attn_hyb(q, kp, vp, kn, vn, msk, sm_scale=0.97 * q.shape[-1] ** -0.5)
+    assert (np.abs(bad - e) > bound).mean() > 0.05
+
+
+def test_single_key_returns_value_exactly():
+    rng = np.random.default_rng(5)
+    H, HK, D = 4, 2, 64
+    q = gen.bf16_normal(rng, (H, 3, D))
+    kp = gen.bf16_normal(rng, (HK, 1, D))
+    vp = gen.bf16_normal(rng, (HK, 1, D))
+    kn = gen.bf16_normal(rng, (HK, 16, D))
+    vn = gen.bf16_normal(rng, (HK, 16, D))
+    o = A.attn_hyb(q, kp, vp, kn, vn, np.zeros((3, 16), bool))
+    assert np.array_equal(o, np.repeat(vp, 2, axis=0)[:, [0, 0, 0]])
+    # P = 0 and one allowed node slot (slot 0, so the fold never starts on a masked slot)
+    msk = np.zeros((3, 16), bool)
+    msk[:, 0] = True
+    o = A.attn_hyb(q, kp[:, :0], vp[:, :0], kn, vn, msk)
+    assert np.array_equal(o, np.repeat(vn, 2, axis=0)[:, [0, 0, 0]])
+
+
+def test_equal_scores_give_the_mean():
+    args = list(_small(7, P=64, NN=16, p_allow=0.5))
+    args[0] = np.zeros_like(args[0])          # q = 0: every score 0
+    q, kp, vp, kn, vn, msk = args
+    o = A.attn_hyb(*args)
+    H = q.shape[0]
+    VP = np.repeat(vp, H // kp.shape[0], 0).astype(np.float64)
+    VN = np.repeat(vn, H // kp.shape[0], 0).astype(np.float64)
+    for m in range(q.shape[1]):
+        vals = np.concatenate([VP, VN[:, msk[m]]], axis=1)
+        mean = vals.mean(axis=1)
+        assert bf16.ulp_diff(o[:, m], mean, np.abs(mean).max() / 8).max() <= 1.0
+
+
+def _layout_case():
+    """The reference's slot-layout test (test_kernel_invariance.py:30-54) at CPU size."""
+    rng = np.random.default_rng(11)
+    H, HK, D, NP, n, NN = 8, 2, 32, 50, 26, 224
+    q = gen.bf16_normal(rng, (H, 4, D))
+    kp = gen.bf16_normal(rng, (HK, NP, D))
+    vp = gen.bf16_normal(rng, (HK, NP, D))
+    kk = gen.bf16_normal(rng, (HK, n, D))
+    vv = gen.bf16_normal(rng, (HK, n, D))
+    outs = []
+    for slots in (list(range(n)), list(range(18)) + list(range(200, 208))):
+        kn = np.zeros((HK, NN, D), np.float32)
+        vn = np.zeros_like(kn)
+        msk = np.zeros((4, NN), bool)
+        kn[:, slots] = kk
+        vn[:, slots] = vv
+        msk[:, slots] = True
+        outs.append((q, kp, vp, kn, vn, msk))
+    return outs
+
+
+def test_hyb_is_slot_layout_invariant_and_blocked_is_not():
+    a, b = _layout_case()
+    assert np.array_equal(A.attn_hyb(*a), A.attn_hyb(*b))
+    # negative control: the tile-wise node reduction depends on where slots sit
+    assert not np.array_equal(A.attn_blocked(*a), A.attn_blocked(*b))
+
+
+def test_hyb_matches_one_token_paths_bitwise():
+    """Oracle analogue of output preservation: each trie row equals its 1-token path call."""
+    c = gen.cfg1()
+    full = A.attn_hyb(c.q, c.kp, c.vp, c.kn, c.vn, c.msk, c.sm_scale)
+    for i in range(len(c.tree.nodes)):
+        pc = gen.path_case(c, i)
+        one = A.attn_hyb(pc.q, pc.kp, pc.vp, pc.kn, pc.vn, pc.msk, pc.sm_scale)
+        assert np.array_equal(one[:, 0], full[:, i])
