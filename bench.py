@@ -9,9 +9,9 @@ set; 32 input sets (445 MB) rotate so the KV stream comes from HBM, not from
 the 256 MB last-level cache.
 
 Timing: W untimed warm-up calls, then K calls enqueued behind a GPU sleep so the
-host never starves the queue; HIP events on the launch stream bracket every
-call.  ms_per_step = GPU time of the K calls / K.  roofline.achieved uses the
-median per-launch event duration.  cpu_baseline times the CPU oracle (a numpy
+host never starves the queue; two HIP events on the launch stream bracket the K
+back-to-back calls.  ms_per_step = GPU time of the K calls / K, and
+roofline.achieved = algorithmic bytes per call / that time.  cpu_baseline times the CPU oracle (a numpy
 restatement of the reference kernel's arithmetic) on one input set.
 
 Prints ONE JSON line.  Only one GPU is used: --gpus N with N > 1 exits.
@@ -38,25 +38,27 @@ def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def time_launches(launchers, steps: int, warmup: int):
-    """Run launchers round-robin; return (ms_per_step, per-launch event ms list)."""
+def time_launches(launchers, steps: int, warmup: int) -> float:
+    """Run launchers round-robin; return the average GPU time per launch in ms.
+
+    Two HIP events on the launch stream bracket the K timed launches; a GPU
+    sleep queued first keeps the device busy while the host enqueues them, so
+    the region holds back-to-back kernels and no host gaps.
+    """
     import torch
     n = len(launchers)
     for i in range(warmup):
         launchers[i % n]()
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    # Keep the GPU busy while the host enqueues the timed calls (about 30 us each).
-    torch.cuda._sleep(int(max(steps, 1) * 30e-6 * 2.4e9) + 10_000_000)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(max(steps, 1) * 20e-6 * 2.4e9) + 10_000_000)
+    start.record()
     for i in range(steps):
-        starts[i].record()
         launchers[i % n]()
-        ends[i].record()
+    end.record()
     torch.cuda.synchronize()
-    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    total = starts[0].elapsed_time(ends[-1])
-    return total / steps, per
+    return start.elapsed_time(end) / steps
 
 
 def cpu_baseline_attn(wl, budget_s: float = 20.0) -> dict:
@@ -95,8 +97,8 @@ def bench_attn(args) -> dict:
         launchers.append(launch)
         keep.append(out)
     _log(f"N={wl.N} nodes, NN={wl.NN}, P={wl.P}; timing {args.steps} steps after {args.warmup} warm-up")
-    ms_step, per = time_launches(launchers, args.steps, args.warmup)
-    kern_ms = statistics.median(per)
+    ms_step = time_launches(launchers, args.steps, args.warmup)
+    kern_ms = ms_step
     nbytes = wl.algorithmic_bytes()
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
     tflops = wl.flops() / (kern_ms * 1e-3) / 1e12
@@ -106,8 +108,6 @@ def bench_attn(args) -> dict:
         "unit": "us per trie-verify attention call",
         "higher_is_better": False,
         "ms_per_step": ms_step,
-        "kernel_us_median": round(kern_ms * 1e3, 3),
-        "kernel_us_mean": round(statistics.mean(per) * 1e3, 3),
         "hbm_frac_of_peak": round(achieved / HBM_PEAK_GBS, 4),
         "mfma_frac_of_peak": round(tflops / BF16_PEAK_TFLOPS, 4),
         "dtype": "bf16",
@@ -117,12 +117,92 @@ def bench_attn(args) -> dict:
                    "algorithmic_bytes_per_call": nbytes, "flops_per_call": wl.flops()},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "rspx::trie_attn_kernel<128,4>"},
+                     "kernel": "rspx::prompt_kernel<128,2> + rspx::node_merge_kernel<128> (one call)"},
     }
     if not args.no_cpu:
         _log("timing CPU baseline (oracle)")
         res["cpu_baseline"] = cpu_baseline_attn(wl, args.cpu_budget)
     return res
+
+
+def _launcher(fn, *args):
+    """Bind a C entry point and its arguments into a zero-argument launch."""
+    from respect_amd import _lib
+
+    def launch():
+        rc = fn(*args)
+        if rc != 0:
+            _lib.check(fn.__name__, rc)
+    return launch
+
+
+def bench_norm_rope(args) -> dict:
+    """RMSNorm [64, 4096] + q/k RMSNorm-and-RoPE (q [64,32,128], k [64,8,128]),
+    positions = 3072 + trie depth; bf16.  Two launches per step."""
+    import torch
+
+    from respect_amd import _lib
+    from respect_amd.system.fused import rope_tables
+    L = _lib.lib()
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    T, HID, HQ, HK, D = 64, 4096, 32, 8, 128
+    sets = 256
+    w = (1 + 0.02 * torch.randn(HID, generator=g, device=dev)).to(torch.bfloat16)
+    wq = (1 + 0.02 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    wk = (1 + 0.02 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    depth = torch.randint(0, 24, (T,), generator=g, device=dev)
+    cos, sin = rope_tables(3072 + depth, D, 1.0e6, device=dev)
+    s = _lib.stream_ptr(dev)
+    norm_l, qk_l, keep = [], [], []
+    for _ in range(sets):
+        x = torch.randn(T, HID, generator=g, device=dev).to(torch.bfloat16)
+        q = torch.randn(T, HQ, D, generator=g, device=dev).to(torch.bfloat16)
+        k = torch.randn(T, HK, D, generator=g, device=dev).to(torch.bfloat16)
+        y = torch.empty_like(x)
+        qo, ko = torch.empty_like(q), torch.empty_like(k)
+        keep += [x, q, k, y, qo, ko]
+        norm_l.append(_launcher(L.rspx_rmsnorm, x.data_ptr(), HID, w.data_ptr(), y.data_ptr(), HID, T, HID, 1e-6, s))
+        qk_l.append(_launcher(L.rspx_qk_norm_rope, q.data_ptr(), HQ * D, D, k.data_ptr(), HK * D, D, wq.data_ptr(),
+                              wk.data_ptr(), cos.data_ptr(), sin.data_ptr(), D, qo.data_ptr(), ko.data_ptr(),
+                              T, HQ, HK, D, 1e-6, s))
+    tn = time_launches(norm_l, args.steps, args.warmup) * 1e-3
+    tq = time_launches(qk_l, args.steps, args.warmup) * 1e-3
+    bytes_norm = 2 * T * HID * 2 + HID * 2
+    bytes_rope = (T * HQ * D + T * HK * D) * 2 * 2 + 2 * T * D * 2
+    return {"workload": "RMSNorm [64,4096] + q/k RMSNorm+RoPE q[64,32,128] k[64,8,128], theta 1e6, bf16",
+            "us_per_step": round((tn + tq) * 1e6, 3),
+            "rmsnorm_us": round(tn * 1e6, 3), "rmsnorm_GBps": round(bytes_norm / tn / 1e9, 1),
+            "qk_norm_rope_us": round(tq * 1e6, 3), "qk_norm_rope_GBps": round(bytes_rope / tq / 1e9, 1),
+            "algorithmic_bytes": bytes_norm + bytes_rope,
+            "hbm_frac_of_peak": round((bytes_norm + bytes_rope) / (tn + tq) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def bench_swiglu(args) -> dict:
+    """SwiGLU on a packed gate/up [64, 2 x 12288] -> [64, 12288], bf16."""
+    import torch
+
+    from respect_amd import _lib
+    L = _lib.lib()
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    T, F = 64, 12288
+    sets = 64
+    s = _lib.stream_ptr(dev)
+    ls, keep = [], []
+    for _ in range(sets):
+        gu = torch.randn(T, 2 * F, generator=g, device=dev).to(torch.bfloat16)
+        y = torch.empty(T, F, device=dev, dtype=torch.bfloat16)
+        keep += [gu, y]
+        ls.append(_launcher(L.rspx_silu_mul, gu.data_ptr(), 2 * F, gu.data_ptr() + 2 * F, 2 * F, y.data_ptr(), F,
+                            T, F, s))
+    t = time_launches(ls, args.steps, args.warmup) * 1e-3
+    nbytes = T * F * 2 * 3
+    return {"workload": "SwiGLU gate/up [64, 2x12288] -> [64, 12288], bf16", "us_per_step": round(t * 1e6, 3),
+            "algorithmic_bytes": nbytes, "GBps": round(nbytes / t / 1e9, 1),
+            "hbm_frac_of_peak": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def main() -> int:
@@ -132,6 +212,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sets", type=int, default=32, help="rotating input sets")
     ap.add_argument("--workload", default="attn", choices=["attn"])
+    ap.add_argument("--no-extra", action="store_true", help="skip the norm/RoPE and SwiGLU lines")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     args = ap.parse_args()
@@ -146,6 +227,9 @@ def main() -> int:
         return 2
     t0 = time.time()
     res = bench_attn(args)
+    if not args.no_extra:
+        _log("timing RMSNorm + q/k norm+RoPE and SwiGLU")
+        res["extra"] = {"norm_rope": bench_norm_rope(args), "swiglu": bench_swiglu(args)}
     res.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "scaling": "weak",
                 "vs_baseline": None, "data": "synthetic (seeded torch.randn / numpy tries)"})
     res["wall_s"] = round(time.time() - t0, 2)

@@ -84,6 +84,47 @@ int rspx_trie_attn(const void* q, int64_t sqh, int64_t sqm,
                    void* workspace, int64_t workspace_bytes, int rows_per_wave,
                    void* stream);
 
+/* ---------------------------------------------------------------- RMSNorm
+ * y[r] = bf16(w * bf16(x[r] * rsqrt(mean(x[r]^2) + eps))), fp32 statistics
+ * (replaces respect/kernels/rmsnorm.py:25 rmsnorm(x, w, eps)).
+ * x, y: [rows, n] with row strides sx, sy (elements); w: [n].  n % 8 == 0,
+ * n <= 16384.  The sum of squares of a row is taken in an order fixed by n,
+ * so a row's output does not depend on `rows`.
+ */
+int rspx_rmsnorm(const void* x, int64_t sx, const void* w, void* y, int64_t sy, int rows, int n, float eps,
+                 void* stream);
+
+/* ---------------------------------------------------------------- RoPE
+ * y = bf16(bf16(x * cos) + bf16(rotate_half(x) * sin))   (replaces
+ * respect/system/fused.py:67 rope(x, cos, sin) for bf16 inputs).
+ * x: [B, H, L, D] with strides sxb, sxh, sxl; cos/sin: [B, L, D] with strides
+ * scb, scl; y: [B, H, L, D] contiguous.  D == 128.  Bitwise equal to PyTorch's
+ * bf16 elementwise ops.
+ */
+int rspx_rope(const void* x, int64_t sxb, int64_t sxh, int64_t sxl, const void* cos, const void* sin,
+              int64_t scb, int64_t scl, void* y, int B, int H, int L, int D, void* stream);
+
+/* ---------------------------------------------------------------- q/k norm + RoPE
+ * The q_norm / k_norm RMSNorm over head_dim followed by RoPE, for all query
+ * and key heads of T tokens in one launch (replaces rmsnorm
+ * respect/kernels/rmsnorm.py:25 on q/k heads followed by HF
+ * apply_rotary_pos_emb).  q: [T, HQ, D] (strides sqt, sqh), k: [T, HK, D]
+ * (skt, skh), wq/wk: [D], cos/sin: [T, D] (row stride scs), qo: [T, HQ, D],
+ * ko: [T, HK, D] contiguous.  D == 128.  Bitwise equal to rspx_rmsnorm
+ * followed by rspx_rope.
+ */
+int rspx_qk_norm_rope(const void* q, int64_t sqt, int64_t sqh, const void* k, int64_t skt, int64_t skh,
+                      const void* wq, const void* wk, const void* cos, const void* sin, int64_t scs, void* qo,
+                      void* ko, int T, int HQ, int HK, int D, float eps, void* stream);
+
+/* ---------------------------------------------------------------- SwiGLU
+ * y = bf16(bf16(g / (1 + exp(-g))) * u)  (replaces respect/system/fused.py:116
+ * silu_mul(g, u)).  g, u, y: [rows, cols] with row strides sg, su, sy; views
+ * into one packed gate/up tensor are fine.  cols % 8 == 0.
+ */
+int rspx_silu_mul(const void* g, int64_t sg, const void* u, int64_t su, void* y, int64_t sy, int rows, int cols,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

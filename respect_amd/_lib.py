@@ -36,6 +36,11 @@ SIGNATURES: dict[str, tuple] = {
         _c_p, _i64, _i32,          # workspace, bytes, rows_per_wave
         _c_p,                      # stream
     ]),
+    "rspx_rmsnorm": (_i32, [_c_p, _i64, _c_p, _c_p, _i64, _i32, _i32, _f32, _c_p]),
+    "rspx_rope": (_i32, [_c_p, _i64, _i64, _i64, _c_p, _c_p, _i64, _i64, _c_p, _i32, _i32, _i32, _i32, _c_p]),
+    "rspx_qk_norm_rope": (_i32, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _c_p,
+                                 _i32, _i32, _i32, _i32, _f32, _c_p]),
+    "rspx_silu_mul": (_i32, [_c_p, _i64, _c_p, _i64, _c_p, _i64, _i32, _i32, _c_p]),
 }
 
 _lib = None

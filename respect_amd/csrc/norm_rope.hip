@@ -1,0 +1,312 @@
+// Row-invariant RMSNorm, RoPE, and the fused q/k RMSNorm + RoPE of a decoder
+// layer, for gfx950.
+//
+// RMSNorm (respect/kernels/rmsnorm.py:12-32, HF Qwen3VLTextRMSNorm):
+//   x32 = float(x); var = sum(x32^2) / N; xh = bf16(x32 * rsqrt(var + eps));
+//   y = bf16(float(w) * float(xh)).
+// The sum of squares of a row is always taken in the same order -- each lane
+// folds its 8-element vectors sequentially, lanes are combined by a fixed DPP /
+// permlane butterfly, waves in wave order -- and the work split depends on N
+// only, so a row's bits never depend on how many rows a call carries.
+//
+// RoPE (respect/system/fused.py:45-75, HF apply_rotary_pos_emb):
+//   y = bf16(bf16(x * cos) + bf16(rotate_half(x) * sin)),
+//   rotate_half(x)[d] = -x[d + D/2] (d < D/2) or x[d - D/2].
+// Every multiply and add is an IEEE fp32 operation rounded once to bf16, the
+// rounding points of PyTorch bf16 arithmetic (no FMA contraction), so results
+// match PyTorch's elementwise ops bit for bit.
+//
+// Vectors of 8 bf16 (16-byte loads/stores) throughout; N and D must be
+// multiples of 8.
+
+#include "common.h"
+#include "respect_amd.h"
+
+namespace rspx {
+
+namespace {
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of L lanes (L a power of two <= 64); every lane of a
+// group gets bitwise the same value.
+template <int L>
+__device__ __forceinline__ float lane_group_sum(float x) {
+  if constexpr (L >= 2) x = x + dpp_f<0xB1>(x);    // lane ^ 1
+  if constexpr (L >= 4) x = x + dpp_f<0x4E>(x);    // lane ^ 2
+  if constexpr (L >= 8) x = x + dpp_f<0x141>(x);   // half-row mirror
+  if constexpr (L >= 16) x = x + dpp_f<0x140>(x);  // row mirror
+  if constexpr (L >= 32) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
+    x = __int_as_float(r[0]) + __int_as_float(r[1]);
+  }
+  if constexpr (L >= 64) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+    x = __int_as_float(r[0]) + __int_as_float(r[1]);
+  }
+  return x;
+}
+
+__device__ __forceinline__ void unpack8(const u32x4& w, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { f[2 * i] = bf16_lo(w[i]); f[2 * i + 1] = bf16_hi(w[i]); }
+}
+__device__ __forceinline__ u32x4 pack8(const float* f) {
+  u32x4 w;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
+  return w;
+}
+
+// 1 / sqrt(v): correctly rounded square root, then a correctly rounded divide.
+__device__ __forceinline__ float rsqrt_rn(float v) { return 1.0f / __builtin_sqrtf(v); }
+
+// Normalise one 8-element vector per iteration for a row held by TPR lanes
+// (TPR <= 64, all in one wave), VPL vectors per lane.  Returns nothing; writes y.
+template <int TPR, int VPL>
+__device__ __forceinline__ void rms_row_wave(const uint16_t* x, const uint16_t* w, uint16_t* y, int sub,
+                                             int n, float eps) {
+  float xv[VPL][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int c = (v * TPR + sub) * 8;
+    if (c < n) {
+      unpack8(*reinterpret_cast<const u32x4*>(x + c), xv[v]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xv[v][i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(xv[v][i], xv[v][i], ss);
+  }
+  ss = lane_group_sum<TPR>(ss);
+  const float r = rsqrt_rn(ss / (float)n + eps);
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int c = (v * TPR + sub) * 8;
+    if (c < n) {
+      float wv[8], o[8];
+      unpack8(*reinterpret_cast<const u32x4*>(w + c), wv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = wv[i] * round_bf16(xv[v][i] * r);
+      *reinterpret_cast<u32x4*>(y + c) = pack8(o);
+    }
+  }
+}
+
+}  // namespace
+
+// Rows of up to 64*8*VPL elements: one row per TPR lanes of a wave.
+template <int TPR, int VPL>
+__global__ __launch_bounds__(256) void rmsnorm_small_kernel(const uint16_t* x, int64_t sx, const uint16_t* w,
+                                                            uint16_t* y, int64_t sy, int rows, int n, float eps) {
+  const int lane = __lane_id();
+  const int row = (blockIdx.x * 256 + threadIdx.x) / TPR;
+  const int sub = lane % TPR;
+  if (row >= rows) return;   // whole lane groups leave together (TPR divides 64)
+  rms_row_wave<TPR, VPL>(x + row * sx, w, y + row * sy, sub, n, eps);
+}
+
+// Long rows: one 256-thread workgroup per row, VPL 8-element vectors per
+// thread.  Wave sums are combined in wave order through LDS.
+template <int VPL>
+__global__ __launch_bounds__(256) void rmsnorm_row_kernel(const uint16_t* x, int64_t sx, const uint16_t* w,
+                                                          uint16_t* y, int64_t sy, int n, float eps) {
+  __shared__ float part[4];
+  const int row = blockIdx.x;
+  const int t = threadIdx.x, lane = __lane_id(), wv = t >> 6;
+  const uint16_t* xr = x + row * sx;
+  float xv[VPL][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int c = (v * 256 + t) * 8;
+    if (c < n) {
+      unpack8(*reinterpret_cast<const u32x4*>(xr + c), xv[v]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xv[v][i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(xv[v][i], xv[v][i], ss);
+  }
+  ss = lane_group_sum<64>(ss);
+  if (lane == 0) part[wv] = ss;
+  __syncthreads();
+  const float tot = ((part[0] + part[1]) + part[2]) + part[3];
+  const float r = rsqrt_rn(tot / (float)n + eps);
+  uint16_t* yr = y + row * sy;
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int c = (v * 256 + t) * 8;
+    if (c < n) {
+      float wvv[8], o[8];
+      unpack8(*reinterpret_cast<const u32x4*>(w + c), wvv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = wvv[i] * round_bf16(xv[v][i] * r);
+      *reinterpret_cast<u32x4*>(yr + c) = pack8(o);
+    }
+  }
+  (void)lane;
+}
+
+namespace {
+
+// RoPE on one row of D = 16 * 8 elements held by 16 lanes (8 each).  The
+// partner half comes from the lane 8 positions away (DPP row rotate by 8).
+__device__ __forceinline__ void rope_vec(const float* xv, const float* cs, const float* sn, int sub, float* o) {
+  float part[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    part[i] = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(xv[i]), 0x128, 0xF, 0xF, false));  // row_ror:8
+  const bool first_half = sub < 8;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float rh = first_half ? -part[i] : part[i];
+    const float a = round_bf16(xv[i] * cs[i]);
+    const float b = round_bf16(rh * sn[i]);
+    o[i] = a + b;   // rounded to bf16 by the store
+  }
+}
+
+}  // namespace
+
+// RoPE for D = 128: x [B, H, L, D] (any strides, D contiguous), cos/sin
+// [B, L, D] with row stride scl and batch stride scb; y [B, H, L, D] contiguous.
+__global__ __launch_bounds__(256) void rope_kernel(const uint16_t* x, int64_t sxb, int64_t sxh, int64_t sxl,
+                                                   const uint16_t* cosb, const uint16_t* sinb, int64_t scb,
+                                                   int64_t scl, uint16_t* y, int B, int H, int L) {
+  constexpr int D = 128;
+  const int gid = blockIdx.x * 256 + threadIdx.x;
+  const int rowid = gid >> 4;      // (b, h, l) row
+  const int sub = gid & 15;
+  const int nrows = B * H * L;
+  if (rowid >= nrows) return;      // 16-lane groups leave together
+  const int l = rowid % L;
+  const int h = (rowid / L) % H;
+  const int b = rowid / (L * H);
+  float xv[8], cs[8], sn[8], o[8];
+  unpack8(*reinterpret_cast<const u32x4*>(x + b * sxb + h * sxh + (int64_t)l * sxl + sub * 8), xv);
+  unpack8(*reinterpret_cast<const u32x4*>(cosb + b * scb + (int64_t)l * scl + sub * 8), cs);
+  unpack8(*reinterpret_cast<const u32x4*>(sinb + b * scb + (int64_t)l * scl + sub * 8), sn);
+  rope_vec(xv, cs, sn, sub, o);
+  *reinterpret_cast<u32x4*>(y + (int64_t)rowid * D + sub * 8) = pack8(o);
+}
+
+// q/k RMSNorm over head_dim followed by RoPE, D = 128, one launch for q and k.
+// q [T, HQ, D] (token stride sqt, head stride sqh), k [T, HK, D]; wq, wk [D];
+// cos/sin rows per token (stride scs); outputs qo [T, HQ, D], ko [T, HK, D]
+// contiguous.  Equal, bit for bit, to rmsnorm followed by rope.
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* q, int64_t sqt, int64_t sqh,
+                                                           const uint16_t* k, int64_t skt, int64_t skh,
+                                                           const uint16_t* wq, const uint16_t* wk,
+                                                           const uint16_t* cosb, const uint16_t* sinb,
+                                                           int64_t scs, uint16_t* qo, uint16_t* ko, int T,
+                                                           int HQ, int HK, float eps) {
+  constexpr int D = 128;
+  const int gid = blockIdx.x * 256 + threadIdx.x;
+  const int rowid = gid >> 4;
+  const int sub = gid & 15;
+  const int nq = T * HQ;
+  if (rowid >= nq + T * HK) return;
+  const bool isq = rowid < nq;
+  const int r = isq ? rowid : rowid - nq;
+  const int HH = isq ? HQ : HK;
+  const int t = r / HH, hh = r - t * HH;
+  const uint16_t* src = isq ? q + (int64_t)t * sqt + hh * sqh : k + (int64_t)t * skt + hh * skh;
+  const uint16_t* w = isq ? wq : wk;
+  float xv[8];
+  unpack8(*reinterpret_cast<const u32x4*>(src + sub * 8), xv);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(xv[i], xv[i], ss);
+  ss = lane_group_sum<16>(ss);
+  const float rr = rsqrt_rn(ss / (float)D + eps);
+  float wv[8], nv[8], cs[8], sn[8], o[8];
+  unpack8(*reinterpret_cast<const u32x4*>(w + sub * 8), wv);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) nv[i] = round_bf16(wv[i] * round_bf16(xv[i] * rr));
+  unpack8(*reinterpret_cast<const u32x4*>(cosb + (int64_t)t * scs + sub * 8), cs);
+  unpack8(*reinterpret_cast<const u32x4*>(sinb + (int64_t)t * scs + sub * 8), sn);
+  rope_vec(nv, cs, sn, sub, o);
+  uint16_t* dst = isq ? qo + (int64_t)r * D : ko + (int64_t)r * D;
+  *reinterpret_cast<u32x4*>(dst + sub * 8) = pack8(o);
+}
+
+}  // namespace rspx
+
+using namespace rspx;
+
+static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+extern "C" int rspx_rmsnorm(const void* x, int64_t sx, const void* w, void* y, int64_t sy, int rows, int n,
+                            float eps, void* stream) {
+  if (rows < 0 || n <= 0 || n % 8 != 0 || n > 16384) return n % 8 ? RSPX_EUNSUPPORTED : RSPX_EINVAL;
+  if (rows == 0) return RSPX_OK;
+  if (!x || !w || !y) return RSPX_EINVAL;
+  if (!al16(x) || !al16(w) || !al16(y) || sx % 8 || sy % 8) return RSPX_EALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  auto X = static_cast<const uint16_t*>(x);
+  auto W = static_cast<const uint16_t*>(w);
+  auto Y = static_cast<uint16_t*>(y);
+  const int vec = n / 8;
+  // The split depends on n only.
+  if (vec <= 16) {
+    hipLaunchKernelGGL((rmsnorm_small_kernel<16, 1>), dim3((rows * 16 + 255) / 256), dim3(256), 0, s, X, sx, W, Y, sy, rows, n, eps);
+  } else if (vec <= 64) {
+    hipLaunchKernelGGL((rmsnorm_small_kernel<64, 1>), dim3((rows * 64 + 255) / 256), dim3(256), 0, s, X, sx, W, Y, sy, rows, n, eps);
+  } else if (vec <= 256) {
+    hipLaunchKernelGGL((rmsnorm_row_kernel<1>), dim3(rows), dim3(256), 0, s, X, sx, W, Y, sy, n, eps);
+  } else if (vec <= 512) {
+    hipLaunchKernelGGL((rmsnorm_row_kernel<2>), dim3(rows), dim3(256), 0, s, X, sx, W, Y, sy, n, eps);
+  } else if (vec <= 1024) {
+    hipLaunchKernelGGL((rmsnorm_row_kernel<4>), dim3(rows), dim3(256), 0, s, X, sx, W, Y, sy, n, eps);
+  } else {
+    hipLaunchKernelGGL((rmsnorm_row_kernel<8>), dim3(rows), dim3(256), 0, s, X, sx, W, Y, sy, n, eps);
+  }
+  return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
+}
+
+extern "C" int rspx_rope(const void* x, int64_t sxb, int64_t sxh, int64_t sxl, const void* cosb, const void* sinb,
+                         int64_t scb, int64_t scl, void* y, int B, int H, int L, int D, void* stream) {
+  if (B < 0 || H < 0 || L < 0) return RSPX_EINVAL;
+  if (D != 128) return RSPX_EUNSUPPORTED;
+  const int64_t rows = (int64_t)B * H * L;
+  if (rows == 0) return RSPX_OK;
+  if (!x || !cosb || !sinb || !y) return RSPX_EINVAL;
+  if (!al16(x) || !al16(cosb) || !al16(sinb) || !al16(y) || sxb % 8 || sxh % 8 || sxl % 8 || scb % 8 || scl % 8)
+    return RSPX_EALIGN;
+  const int64_t threads = rows * 16;
+  hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), sxb, sxh, sxl,
+                     static_cast<const uint16_t*>(cosb), static_cast<const uint16_t*>(sinb), scb, scl,
+                     static_cast<uint16_t*>(y), B, H, L);
+  return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
+}
+
+extern "C" int rspx_qk_norm_rope(const void* q, int64_t sqt, int64_t sqh, const void* k, int64_t skt,
+                                 int64_t skh, const void* wq, const void* wk, const void* cosb,
+                                 const void* sinb, int64_t scs, void* qo, void* ko, int T, int HQ, int HK,
+                                 int D, float eps, void* stream) {
+  if (T < 0 || HQ < 0 || HK < 0) return RSPX_EINVAL;
+  if (D != 128) return RSPX_EUNSUPPORTED;
+  const int64_t rows = (int64_t)T * (HQ + HK);
+  if (rows == 0) return RSPX_OK;
+  if (!q || !k || !wq || !wk || !cosb || !sinb || !qo || !ko) return RSPX_EINVAL;
+  const void* ps[] = {q, k, wq, wk, cosb, sinb, qo, ko};
+  for (const void* p : ps)
+    if (!al16(p)) return RSPX_EALIGN;
+  if (sqt % 8 || sqh % 8 || skt % 8 || skh % 8 || scs % 8) return RSPX_EALIGN;
+  const int64_t threads = rows * 16;
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(q), sqt, sqh,
+                     static_cast<const uint16_t*>(k), skt, skh, static_cast<const uint16_t*>(wq),
+                     static_cast<const uint16_t*>(wk), static_cast<const uint16_t*>(cosb),
+                     static_cast<const uint16_t*>(sinb), scs, static_cast<uint16_t*>(qo),
+                     static_cast<uint16_t*>(ko), T, HQ, HK, eps);
+  return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
+}

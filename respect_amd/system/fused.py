@@ -1,0 +1,99 @@
+"""RoPE and SwiGLU at PyTorch's bf16 rounding points, plus the fused q/k norm + RoPE.
+
+Signatures follow respect/system/fused.py: ``rope(x, cos, sin)`` (:67) and
+``silu_mul(g, u)`` (:116).  Every multiply/add is an fp32 operation rounded once
+to bf16 (no FMA contraction), so ``rope`` matches PyTorch's bf16 elementwise ops
+bit for bit; ``silu_mul`` rounds silu(g) to bf16 before the product with u.
+Only bf16 is built: other dtypes raise TypeError (the reference computes them
+with PyTorch ops instead).
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ..kernels._tensor import as_kernel_input
+
+
+def rope(x, cos, sin):
+    """q*cos + rotate_half(q)*sin.  x [B,H,L,D], cos/sin [B,L,D] -> [B,H,L,D] bf16."""
+    if x.dtype != torch.bfloat16 or cos.dtype != torch.bfloat16 or sin.dtype != torch.bfloat16:
+        raise TypeError("rope: respect_amd builds the bf16 path only")
+    B, H, L, D = x.shape
+    if tuple(cos.shape) != (B, L, D) or tuple(sin.shape) != (B, L, D):
+        raise ValueError(f"rope: cos/sin must be [{B}, {L}, {D}]")
+    x = as_kernel_input(x, "x")
+    cos = as_kernel_input(cos.contiguous(), "cos")
+    sin = as_kernel_input(sin.contiguous(), "sin")
+    y = torch.empty((B, H, L, D), dtype=torch.bfloat16, device=x.device)
+    rc = _lib.lib().rspx_rope(x.data_ptr(), x.stride(0), x.stride(1), x.stride(2), cos.data_ptr(),
+                              sin.data_ptr(), cos.stride(0), cos.stride(1), y.data_ptr(), B, H, L, D,
+                              _lib.stream_ptr(x.device))
+    _lib.check("rspx_rope", rc)
+    return y
+
+
+def silu_mul(g, u):
+    """silu(g) * u for bf16 tensors of the same shape (views into a packed gate/up are fine)."""
+    if g.dtype != torch.bfloat16 or u.dtype != torch.bfloat16:
+        raise TypeError("silu_mul: respect_amd builds the bf16 path only")
+    if g.shape != u.shape:
+        raise ValueError("silu_mul: g and u must have the same shape")
+    F = g.shape[-1]
+    g2 = as_kernel_input(g.reshape(-1, F) if g.is_contiguous() else _rows(g), "g")
+    u2 = as_kernel_input(u.reshape(-1, F) if u.is_contiguous() else _rows(u), "u")
+    M = g2.shape[0]
+    y = torch.empty((M, F), dtype=torch.bfloat16, device=g.device)
+    rc = _lib.lib().rspx_silu_mul(g2.data_ptr(), g2.stride(0), u2.data_ptr(), u2.stride(0), y.data_ptr(),
+                                  y.stride(0), M, F, _lib.stream_ptr(g.device))
+    _lib.check("rspx_silu_mul", rc)
+    return y.reshape(g.shape)
+
+
+def _rows(t):
+    """A 2-D row view of t without copying when only the leading dims are strided."""
+    F = t.shape[-1]
+    if t.dim() == 2 and t.stride(-1) == 1:
+        return t
+    try:
+        return t.view(-1, F)
+    except RuntimeError:
+        return t.reshape(-1, F)
+
+
+def qk_norm_rope(q, k, wq, wk, eps, cos, sin):
+    """q_norm / k_norm (RMSNorm over head_dim) followed by RoPE, one launch.
+
+    q [T, HQ, D], k [T, HK, D], wq/wk [D], cos/sin [T, D] (the rotary rows of
+    each token's position) -> (q_out [T, HQ, D], k_out [T, HK, D]).  Bitwise
+    equal to ``rope(rmsnorm(q, wq, eps), ...)`` and the same for k.
+    """
+    T, HQ, D = q.shape
+    HK = k.shape[1]
+    q = as_kernel_input(q, "q")
+    k = as_kernel_input(k, "k")
+    wq = as_kernel_input(wq.contiguous(), "wq")
+    wk = as_kernel_input(wk.contiguous(), "wk")
+    cos = as_kernel_input(cos.reshape(T, D), "cos")
+    sin = as_kernel_input(sin.reshape(T, D), "sin")
+    if cos.stride(0) != sin.stride(0):
+        cos, sin = cos.contiguous(), sin.contiguous()
+    qo = torch.empty((T, HQ, D), dtype=torch.bfloat16, device=q.device)
+    ko = torch.empty((T, HK, D), dtype=torch.bfloat16, device=q.device)
+    rc = _lib.lib().rspx_qk_norm_rope(q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0),
+                                      k.stride(1), wq.data_ptr(), wk.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                      cos.stride(0), qo.data_ptr(), ko.data_ptr(), T, HQ, HK, D, float(eps),
+                                      _lib.stream_ptr(q.device))
+    _lib.check("rspx_qk_norm_rope", rc)
+    return qo, ko
+
+
+def rope_tables(positions, head_dim: int = 128, theta: float = 1.0e6, device=None):
+    """cos/sin rows [T, head_dim] (bf16) for integer positions, computed like HF's
+    Qwen3VLTextRotaryEmbedding: fp32 inv_freq, fp32 angles, bf16 cos/sin."""
+    pos = torch.as_tensor(positions, device=device).to(torch.float32)
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64, device=pos.device).float()
+                                / head_dim))
+    freqs = pos[:, None] * inv_freq[None, :]
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)

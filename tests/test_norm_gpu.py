@@ -1,0 +1,122 @@
+"""GPU parity and row-invariance tests of RMSNorm, RoPE, q/k-norm+RoPE and SwiGLU.
+
+Parity bars: RoPE bitwise against the oracle (= PyTorch's bf16 elementwise
+ops); RMSNorm and SwiGLU within 1 bf16 ulp of the oracle (the reduction order,
+the rsqrt and the exp differ from PyTorch's CPU implementation); q/k norm +
+RoPE bitwise equal to RMSNorm followed by RoPE.  Row invariance is bitwise.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import bf16, gen
+from oracle import norm as N
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(torch.bfloat16).cuda()
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("rows,n", [(64, 4096), (64, 128), (5, 512), (3, 1024), (2, 12288), (2, 16384), (9, 2048)])
+def test_rmsnorm_parity(rows, n):
+    from respect_amd.kernels.rmsnorm import rmsnorm
+    print(f"[rmsnorm] rows={rows} n={n}", flush=True)
+    rng = np.random.default_rng(n)
+    x = gen.bf16_normal(rng, (rows, n))
+    w = bf16.round_bf16(1 + 0.02 * rng.standard_normal(n).astype(np.float32))
+    out = _np(rmsnorm(_dev(x), _dev(w), 1e-6))
+    ref = N.rmsnorm(x, w, 1e-6)
+    d = bf16.ulp_diff(out, ref)
+    print(f"  max ulp {d.max():.2f}, equal {(out == ref).mean():.5f}", flush=True)
+    assert d.max() <= 1.0
+
+
+def test_rmsnorm_row_count_invariant():
+    """tests/test_kernel_invariance.py:20-27 of the reference, plus more row counts."""
+    from respect_amd.kernels.rmsnorm import rmsnorm
+    torch.manual_seed(0)
+    x = torch.randn(64, 4096, device="cuda", dtype=torch.bfloat16)
+    w = torch.randn(4096, device="cuda", dtype=torch.bfloat16)
+    full = rmsnorm(x, w, 1e-6)
+    for m in (1, 7, 33):
+        assert torch.equal(rmsnorm(x[:m], w, 1e-6), full[:m])
+    # rows taken from the middle, and a 3-D input
+    assert torch.equal(rmsnorm(x[20:21], w, 1e-6), full[20:21])
+    assert torch.equal(rmsnorm(x.view(4, 16, 4096), w, 1e-6).view(64, 4096), full)
+
+
+def test_rope_bitwise():
+    from respect_amd.system.fused import rope
+    rng = np.random.default_rng(3)
+    B, H, L, D = 1, 32, 64, 128
+    x = gen.bf16_normal(rng, (B, H, L, D))
+    pos = 3072 + rng.integers(0, 24, L)          # KV offset + trie depth
+    cos, sin = N.rope_tables(pos)
+    out = _np(rope(_dev(x), _dev(cos[None]), _dev(sin[None])))
+    assert np.array_equal(out, N.rope(x, cos[None, None], sin[None, None]))
+    # strided x (heads and tokens swapped in memory) gives the same bits
+    xs = _dev(x).transpose(1, 2).contiguous().transpose(1, 2)
+    assert np.array_equal(_np(rope(xs, _dev(cos[None]), _dev(sin[None]))), out)
+
+
+def test_qk_norm_rope_equals_norm_then_rope():
+    from respect_amd.kernels.rmsnorm import rmsnorm
+    from respect_amd.system.fused import qk_norm_rope, rope
+    rng = np.random.default_rng(4)
+    T, HQ, HK, D = 64, 32, 8, 128
+    q = gen.bf16_normal(rng, (T, HQ, D))
+    k = gen.bf16_normal(rng, (T, HK, D))
+    wq = bf16.round_bf16(1 + 0.02 * rng.standard_normal(D).astype(np.float32))
+    wk = bf16.round_bf16(1 + 0.02 * rng.standard_normal(D).astype(np.float32))
+    cos, sin = N.rope_tables(3072 + rng.integers(0, 24, T))
+    qo, ko = qk_norm_rope(_dev(q), _dev(k), _dev(wq), _dev(wk), 1e-6, _dev(cos), _dev(sin))
+    # composition of the two kernels, in the [B, H, L, D] layout rope expects
+    qn = rmsnorm(_dev(q), _dev(wq), 1e-6).transpose(0, 1)[None]
+    kn = rmsnorm(_dev(k), _dev(wk), 1e-6).transpose(0, 1)[None]
+    q2 = rope(qn, _dev(cos)[None], _dev(sin)[None])[0].transpose(0, 1)
+    k2 = rope(kn, _dev(cos)[None], _dev(sin)[None])[0].transpose(0, 1)
+    assert torch.equal(qo, q2) and torch.equal(ko, k2)
+    # oracle composition (RMSNorm within 1 ulp, so compare through the oracle's own norm)
+    ref_q = N.rope(N.rmsnorm(q, wq, 1e-6), cos[:, None], sin[:, None])
+    assert bf16.ulp_diff(_np(qo), ref_q).max() <= 2.0
+    # token-count invariance
+    q1, k1 = qk_norm_rope(_dev(q[5:6]), _dev(k[5:6]), _dev(wq), _dev(wk), 1e-6, _dev(cos[5:6]), _dev(sin[5:6]))
+    assert torch.equal(q1[0], qo[5]) and torch.equal(k1[0], ko[5])
+
+
+def test_silu_mul_parity_packed_gate_up():
+    """Config shape: gate/up packed as [64, 2 x 12288] -> [64, 12288]."""
+    from respect_amd.system.fused import silu_mul
+    rng = np.random.default_rng(5)
+    F = 12288
+    gu = gen.bf16_normal(rng, (64, 2 * F))
+    gud = _dev(gu)
+    out = silu_mul(gud[:, :F], gud[:, F:])
+    ref = N.silu_mul(gu[:, :F], gu[:, F:])
+    o = _np(out)
+    d = bf16.ulp_diff(o, ref, 1e-30)
+    print(f"  silu_mul max ulp {d.max():.2f}, equal {(o == ref).mean():.5f}", flush=True)
+    assert d.max() <= 1.0
+    assert torch.equal(silu_mul(gud[7:8, :F], gud[7:8, F:]), out[7:8])
+    # contiguous separate tensors give the same bits
+    assert torch.equal(silu_mul(gud[:, :F].contiguous(), gud[:, F:].contiguous()), out)
+
+
+def test_kernel_errors():
+    from respect_amd._lib import RspxError
+    from respect_amd.kernels.rmsnorm import rmsnorm
+    from respect_amd.system.fused import rope, silu_mul
+    x = torch.randn(4, 100, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(RspxError):
+        rmsnorm(x, torch.ones(100, device="cuda", dtype=torch.bfloat16), 1e-6)
+    with pytest.raises(TypeError):
+        silu_mul(x.float(), x.float())
+    with pytest.raises(RspxError):
+        c = torch.ones(1, 2, 64, device="cuda", dtype=torch.bfloat16)
+        rope(torch.ones(1, 1, 2, 64, device="cuda", dtype=torch.bfloat16), c, c)
