@@ -62,25 +62,27 @@ def time_launches(launchers, steps: int, warmup: int) -> float:
 
 
 def cpu_baseline_attn(wl, budget_s: float = 20.0) -> dict:
-    """Time the CPU oracle (reference arithmetic in numpy) on input set 0."""
+    """Time the CPU oracle (reference arithmetic in numpy) on input set 0, one thread."""
     import numpy as np
+    from threadpoolctl import threadpool_limits
 
     from oracle import attention as A
     q, kp, vp, kn, vn = (t.float().cpu().numpy() for t in wl.sets[0])
     msk = wl.msk.cpu().numpy()
-    A.attn_hyb(q[:, :1], kp, vp, kn, vn, msk[:1], wl.sm_scale)  # warm numpy paths
     times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 2:
-        t0 = time.perf_counter()
-        A.attn_hyb(q, kp, vp, kn, vn, msk, wl.sm_scale)
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 20:
-            break
+    with threadpool_limits(limits=1):
+        A.attn_hyb(q[:, :1], kp, vp, kn, vn, msk[:1], wl.sm_scale)  # warm numpy paths
+        t_end = time.perf_counter() + budget_s
+        while time.perf_counter() < t_end or len(times) < 2:
+            t0 = time.perf_counter()
+            A.attn_hyb(q, kp, vp, kn, vn, msk, wl.sm_scale)
+            times.append(time.perf_counter() - t0)
+            if len(times) >= 20:
+                break
     med = statistics.median(times)
-    return {"value": med * 1e6, "unit": "us per call", "cores": os.cpu_count(), "kind": "port",
+    return {"value": round(med * 1e6, 1), "unit": "us per call", "cores": 1, "kind": "port",
             "sample": f"{len(times)} full calls of the 8B-shape 64-node attention on input set 0 "
-                      f"(numpy oracle restating respect/kernels/attention.py; median)"}
+                      f"(numpy oracle restating respect/kernels/attention.py, one thread; median)"}
 
 
 def bench_attn(args) -> dict:
@@ -123,6 +125,81 @@ def bench_attn(args) -> dict:
         _log("timing CPU baseline (oracle)")
         res["cpu_baseline"] = cpu_baseline_attn(wl, args.cpu_budget)
     return res
+
+
+ATTN_KERNELS = ("rspx::prompt_kernel", "rspx::node_merge_kernel")
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+PROBE_COPY_BYTES = 1 << 28   # the probe's device copy: 256 MiB read + 256 MiB written
+
+
+def traffic_probe(args) -> int:
+    """Child run under rocprofv3 --pmc: 6 attention calls and one 256 MiB device copy."""
+    import torch
+
+    from respect_amd.kernels.attention import make_launcher
+    from respect_amd.workloads import AttnWorkload
+    wl = AttnWorkload(sets=2, seed=0)
+    launchers = [make_launcher(*st, wl.msk, wl.sm_scale)[0] for st in wl.sets]
+    for i in range(6):
+        launchers[i % 2]()
+    src = torch.ones(PROBE_COPY_BYTES // 2, device="cuda", dtype=torch.bfloat16)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    return 0
+
+
+def measure_traffic(timeout_s: float = 180.0):
+    """Memory traffic per attention call from two rocprofv3 PMC passes over a child
+    run of this script (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), each scaled
+    by what the counter reads for the child's 256 MiB device copy.  Runs before this
+    process touches the GPU.  Returns None if rocprofv3 is missing or a pass fails."""
+    import csv
+    import shutil
+    import signal
+    import subprocess
+    import tempfile
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None
+    per_kernel: dict = {}
+    scale: dict = {}
+    with tempfile.TemporaryDirectory() as td:
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", td, "-o", counter,
+                   "--", sys.executable, str(ROOT / "bench.py"), "--traffic-probe"]
+            _log(f"traffic pass {counter}")
+            proc = subprocess.Popen(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                                    start_new_session=True)
+            try:
+                rc = proc.wait(timeout=timeout_s)
+            except subprocess.TimeoutExpired:
+                os.killpg(proc.pid, signal.SIGKILL)
+                proc.wait()
+                _log(f"traffic pass {counter} timed out")
+                return None
+            path = Path(td) / f"{counter}_counter_collection.csv"
+            if rc != 0 or not path.exists():
+                _log(f"traffic pass {counter} failed (rc={rc})")
+                return None
+            vals: dict = {}
+            with open(path) as f:
+                for row in csv.DictReader(f):
+                    vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+            copy_kib = max(vals.get(COPY_KERNEL, [0.0]))
+            if copy_kib <= 0:
+                return None
+            scale[counter] = PROBE_COPY_BYTES / 1024 / copy_kib
+            for name, v in vals.items():
+                for k in ATTN_KERNELS:
+                    if k in name:
+                        per_kernel.setdefault(k, {})[counter] = statistics.median(v) * 1024 * scale[counter]
+    if any(len(per_kernel.get(k, {})) != 2 for k in ATTN_KERNELS):
+        return None
+    total = sum(v["FETCH_SIZE"] + v["WRITE_SIZE"] for v in per_kernel.values())
+    return {"bytes": total, "scale": scale,
+            "by_kernel": {k: {"fetch": round(v["FETCH_SIZE"]), "write": round(v["WRITE_SIZE"])}
+                          for k, v in per_kernel.items()}}
 
 
 def _launcher(fn, *args):
@@ -205,6 +282,20 @@ def bench_swiglu(args) -> dict:
             "hbm_frac_of_peak": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def bench_copy(args) -> dict:
+    """Device-to-device copy of a 1 GiB bf16 buffer (torch's copy kernel): the
+    measured HBM ceiling the kernels above are compared with, and the known-size
+    kernel that scales rocprofv3's FETCH_SIZE/WRITE_SIZE counters."""
+    import torch
+    n = 1 << 29
+    src = torch.ones(n, device="cuda", dtype=torch.bfloat16)
+    dst = torch.empty_like(src)
+    t = time_launches([lambda: dst.copy_(src)], max(args.steps // 10, 10), 3) * 1e-3
+    nbytes = 2 * n * 2
+    return {"workload": "device copy of 1 GiB (read 1 GiB + write 1 GiB)", "us_per_step": round(t * 1e6, 1),
+            "GBps": round(nbytes / t / 1e9, 1), "hbm_frac_of_peak": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -215,21 +306,32 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="skip the norm/RoPE and SwiGLU lines")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 PMC passes")
+    ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.traffic_probe:
+        return traffic_probe(args)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: the verification kernels run on a single MI355X "
               "(multi-GPU sharding is a design note, not part of this build)", file=sys.stderr)
         return 2
+    t0 = time.time()
+    traffic = None if args.no_traffic else measure_traffic()
     import torch
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
-    t0 = time.time()
     res = bench_attn(args)
+    if traffic is not None:
+        res["roofline"]["traffic"] = round(traffic["bytes"])
+        res["roofline"]["traffic_detail"] = {
+            "source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per dispatch, scaled by a 256 MiB device copy",
+            "scale": {k: round(v, 4) for k, v in traffic["scale"].items()}, "by_kernel": traffic["by_kernel"]}
     if not args.no_extra:
         _log("timing RMSNorm + q/k norm+RoPE and SwiGLU")
-        res["extra"] = {"norm_rope": bench_norm_rope(args), "swiglu": bench_swiglu(args)}
+        res["extra"] = {"norm_rope": bench_norm_rope(args), "swiglu": bench_swiglu(args),
+                        "copy": bench_copy(args)}
     res.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "scaling": "weak",
                 "vs_baseline": None, "data": "synthetic (seeded torch.randn / numpy tries)"})
     res["wall_s"] = round(time.time() - t0, 2)
