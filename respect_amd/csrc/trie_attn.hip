@@ -7,53 +7,61 @@
 //
 // Reduction tree, fixed by P and by the row's allowed node slots only:
 //
-//   step   32 prompt keys.  Scores from bf16 MFMA 16x16x32 (fp32 accumulate,
-//          head_dim reduced by a fixed chain of MFMAs), base-2 exponent with
-//          the scale folded into log2(e).  Probabilities are rounded to bf16
-//          before the PV MFMA, as the reference rounds p before tl.dot
-//          (attention.py:48).
-//   group  RL consecutive prompt keys (a whole number of steps; NG <= 16
-//          groups), online softmax over its steps in key order.  The running
-//          reference maximum of a row is moved only when a step's maximum
-//          exceeds it by more than 2^8 (then the accumulator is rescaled);
-//          otherwise probabilities are taken against the old reference and may
-//          reach 2^8.  The rule looks at the row's own scores only.
-//   final  the NG groups left to right, then the node partial.
-//   node   the row's allowed node slots, one at a time in slot order, fp32
-//          probabilities (the reference's node loop, attention.py:52-67).
-//          Masked slots are skipped; in the reference they are exact no-ops,
-//          so only the sequence of allowed slots matters.
+//   step     32 prompt keys.  Scores from bf16 MFMA 16x16x32 (fp32
+//            accumulate, head_dim reduced by a fixed chain of MFMAs),
+//            base-2 exponent with the scale folded into log2(e).
+//            Probabilities are rounded to bf16 before the PV MFMA, as the
+//            reference rounds p before tl.dot (attention.py:48).
+//   quarter  steps 4i + k (i = 0, 1, ...) of a group, online softmax in step
+//            order.  The running reference maximum of a row moves only when
+//            a step's maximum exceeds it by more than 2^8 (then the
+//            accumulator is rescaled); otherwise probabilities are taken
+//            against the old reference and may reach 2^8.
+//   group    S = 4 NR consecutive steps (NG <= 8 groups): its quarters
+//            k = 0, 1, 2, 3 combined in order.
+//   node     the row's allowed node slots, one at a time in slot order,
+//            fp32 probabilities (the reference's node loop,
+//            attention.py:52-67).  Masked slots are skipped; in the
+//            reference they are exact no-ops, so only the sequence of
+//            allowed slots matters.
+//   final    the NG groups left to right, then the node partial.
 //
-// RL and NG depend on P only.  Which wavefront computes what changes with the
-// number of rows, never the arithmetic of a row, so a row's bits are the same
-// whether it is verified alone (1-token decoding) or inside a 128-node trie,
-// and wherever its allowed slots sit in the node segment.
+// S and NG depend on P only.  Which wave computes what changes with the number
+// of rows, never the arithmetic of a row, so a row's bits are the same whether
+// it is verified alone (1-token decoding) or inside a 128-node trie, and
+// wherever its allowed slots sit in the node segment.
 //
 // Two launches on the caller's stream, no host synchronisation:
-//   A  prompt_kernel: workgroup = (kv head g, 64 or 128 GQA rows, group).
-//      The four waves issue the group's K/V straight from HBM into an LDS ring
-//      (global_load_lds, up to 8 steps in flight, no registers held), laid
-//      out so that each lane's MFMA fragment is one conflict-free ds_read;
-//      then each wave consumes the steps for its 16 or 32 rows (V transposed
-//      in registers for the PV B operand) and stores its group partials.
-//   B  node_merge_kernel: one wave per (query row, head).  It lists the
-//      allowed node slots (ballot + mbcnt), folds them in order (dot products
-//      reduced with DPP / permlane butterflies), combines the group partials
-//      of kernel A in group order and the node partial last, writes bf16.
+//   A  prompt_kernel: workgroup = (kv head g, block of 32 RT GQA rows, key
+//      group), 8 waves = 2 row halves x 4 key quarters.  The waves issue the
+//      group's K/V straight from HBM into an LDS ring (buffer_load ... lds, a
+//      round of 4 steps per ring slot, nothing held in registers), laid out so
+//      that K fragments are one conflict-free ds_read_b128 and V fragments
+//      one ds_read_b64_tr_b16 (the transposing LDS read of gfx950) per MFMA
+//      operand half.  Wave (h, k) computes step 4i + k of round i for its 16 RT
+//      rows; at the end the four quarters of each row are combined through
+//      LDS and the group partial (m, l, acc) is stored.
+//   B  node_merge_kernel: one wave per 4 consecutive rows (16 lanes per row).
+//      It lists each row's allowed node slots (ballots), folds them in order
+//      (dot products reduced with a fixed DPP butterfly), combines the group
+//      partials in group order and the node partial last, writes bf16.
 //   Rows are packed GQA-wise (row = query * GQA + head-in-group), so a kv
-//   head's K/V is read once for all query heads that share it.  With 8 kv
-//   heads, workgroup g of either kernel lands on XCD g (round-robin dispatch),
-//   so a head's K/V and partials stay in one XCD's L2.
+//   head's K/V is read once from HBM for all query heads that share it.  With
+//   8 kv heads, workgroup g of kernel A lands on XCD g (round-robin dispatch),
+//   so the row blocks that share a head's K/V meet in one XCD's L2.
 
 #include "common.h"
 #include "respect_amd.h"
 
 namespace rspx {
 
-constexpr int kNGTarget = 16;   // maximum number of key groups per kv head
-constexpr int kStep = 32;       // keys per online-softmax step
-constexpr float kLazyTau = 8.f; // log2 headroom before the reference max moves
+constexpr int kStep = 32;        // keys per online-softmax step
+constexpr int kQuarters = 4;     // key quarters (waves) per row half
+constexpr int kGroupTarget = 8;  // maximum number of key groups per kv head
+constexpr float kLazyTau = 8.f;  // log2 headroom before the reference max moves
 constexpr int kMaxNodeSlots = 4096;
+constexpr int kWavesA = 8;       // waves per prompt workgroup
+constexpr int kWavesB = 2;       // waves per merge workgroup
 
 struct TrieAttnArgs {
   const uint16_t* q;  int64_t sqh, sqm;
@@ -64,15 +72,15 @@ struct TrieAttnArgs {
   const uint8_t* msk; int64_t smm, smn;
   uint16_t* out;      int64_t soh, som;
   int HK, GQA, M, P, NN;
-  int R, NT, NG, RL;
-  float c;        // sm_scale * log2(e)
-  float* gp_ml;   // [HK][R][NG][2]  group partial (m, l)
-  float* gp_acc;  // [HK][R][NG][D]
+  int R, NRB, NG, S;  // rows per kv head, row blocks, groups, steps per group
+  float c;            // sm_scale * log2(e)
+  float* gp_ml;       // [HK][R][NG][2]  group partial (m, l)
+  float* gp_acc;      // [HK][R][NG][D]
 };
 
-template <int D> struct VRow;
-template <> struct VRow<128> { typedef u32x4 T; };
-template <> struct VRow<64> { typedef u32x2 T; };
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) char lds_char;
 
 // state (m, l, acc) <- state (+) incoming.  An incoming partial with m = -inf
 // is empty and left out (it would be an exact no-op).  From the empty state
@@ -111,67 +119,44 @@ __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
-// Sum over aligned groups of L consecutive lanes; every lane of a group gets
-// bitwise the same value (each butterfly level adds the same two operands).
-template <int L>
-__device__ __forceinline__ float group_sum(float x) {
-  if constexpr (L >= 2) x = x + dpp<0xB1>(x);    // quad_perm [1,0,3,2]: lane ^ 1
-  if constexpr (L >= 4) x = x + dpp<0x4E>(x);    // quad_perm [2,3,0,1]: lane ^ 2
-  if constexpr (L >= 8) x = x + dpp<0x141>(x);   // row_half_mirror: quads of an 8-lane half
-  if constexpr (L >= 16) x = x + dpp<0x140>(x);  // row_mirror: halves of a 16-lane row
-  if constexpr (L >= 32) {
-    auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
-    x = __int_as_float(r[0]) + __int_as_float(r[1]);
-  }
-  if constexpr (L >= 64) {
-    auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
-    x = __int_as_float(r[0]) + __int_as_float(r[1]);
-  }
+// Sum over aligned groups of 16 lanes; every lane of a group gets bitwise the
+// same value (each butterfly level adds the same two operands in every lane).
+__device__ __forceinline__ float sum16(float x) {
+  x = x + dpp<0xB1>(x);    // quad_perm [1,0,3,2]: lane ^ 1
+  x = x + dpp<0x4E>(x);    // quad_perm [2,3,0,1]: lane ^ 2
+  x = x + dpp<0x141>(x);   // row_half_mirror: quads of an 8-lane half
+  x = x + dpp<0x140>(x);   // row_mirror: halves of a 16-lane row
   return x;
 }
 
-// Load n bf16 values (n in {1,2,4,8,16,32}) starting at p and widen to fp32.
-template <int N>
-__device__ __forceinline__ void load_row_f32(const uint16_t* p, float* dst) {
-  if constexpr (N == 1) {
-    dst[0] = bf16_to_f32(*p);
-  } else if constexpr (N == 2) {
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
-    dst[0] = bf16_lo(w); dst[1] = bf16_hi(w);
-  } else if constexpr (N == 4) {
-    const u32x2 w = *reinterpret_cast<const u32x2*>(p);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) { dst[2 * i] = bf16_lo(w[i]); dst[2 * i + 1] = bf16_hi(w[i]); }
-  } else {
-#pragma unroll
-    for (int c = 0; c < N / 8; ++c) {
-      const u32x4 w = reinterpret_cast<const u32x4*>(p)[c];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) { dst[8 * c + 2 * i] = bf16_lo(w[i]); dst[8 * c + 2 * i + 1] = bf16_hi(w[i]); }
-    }
-  }
-}
-
-// Geometry of one 32-key step of K/V in LDS.  A step is cut into 1 KB (or
-// 256 B) chunks, one per wave-wide direct-to-LDS load: lane l's bytes land at
-// chunk base + l * lane_bytes, which is exactly the MFMA fragment lane l reads
-// back with one conflict-free ds_read.
+// Geometry of one 32-key step of K/V in LDS.  A step is cut into 1 KB chunks,
+// one per wave-wide direct-to-LDS load (lane l's 16 bytes land at chunk base
+// + 16 l).  K chunk (kb, i): lane (n16, g4) <- K[16 kb + n16][32 i + 8 g4, +8),
+// exactly the A fragment lane l reads back with one ds_read_b128.  V: key rows
+// of U = D / 8 16-byte units; unit b of key t sits at position b ^ f(t) of the
+// row (f even), so the 16 lanes of one transposing read (4 keys x 32 bytes)
+// hit distinct banks.
 template <int D>
 struct StepGeom {
-  static constexpr int DQ = D / 32;              // QK k-steps over head_dim
-  static constexpr int DPL = D / 16;             // PV MFMAs per step
-  static constexpr int KCH = 2 * DQ;             // K chunks: (key block, k-step), 16 B per lane
-  static constexpr int VB = 2 * DPL;             // V bytes per lane per PV k-slot (16 or 8)
-  static constexpr int VS = VB == 16 ? 16 : 4;   // bytes per lane of one V load (DMA sizes: 4, 12, 16)
-  static constexpr int VPER = VB / VS;           // V loads per PV k-slot
-  static constexpr int VCH = 8 * VPER;           // V chunks
+  static constexpr int DQ = D / 32;          // QK MFMAs per 16x16 tile (k = 32 each)
+  static constexpr int DT = D / 16;          // PV MFMAs per tile (16 head_dim columns each)
+  static constexpr int U = D / 8;            // 16-byte units per key row
+  static constexpr int KCH = 2 * DQ;         // K chunks per step
+  static constexpr int VCH = D / 16;         // V chunks per step (32 keys x 2D bytes / 1 KB)
+  static constexpr int CH = KCH + VCH;       // chunks per step
+  static constexpr int KPV = 1024 / (16 * U);  // keys per V chunk
   static constexpr int KBYTES = KCH * 1024;
-  static constexpr int SLOT = KBYTES + VCH * 64 * VS;
-  static constexpr int CH = KCH + VCH;           // chunks (= loads) per step
+  static constexpr int SLOT = CH * 1024;     // bytes per step
+  static constexpr int ROUND = kQuarters * SLOT;
+  static constexpr int RING = D == 128 ? 2 : 4;  // rounds in flight
+  static constexpr int OWN = kQuarters * CH / kWavesA;  // chunks one wave issues per round
 };
 
-constexpr int kWaves = 4;     // waves per prompt workgroup
-constexpr int kRing = 7;      // LDS ring slots (steps in flight)
+template <int D>
+__device__ __forceinline__ int vswz(int key) {
+  constexpr int U = D / 8;
+  return 2 * ((key / (16 / U)) % (U / 2));
+}
 
 __device__ __forceinline__ void wait_vm(int n) {
   // s_waitcnt vmcnt(n); the count must be an immediate, hence the switch.
@@ -246,176 +231,182 @@ __device__ __forceinline__ void wait_vm(int n) {
 #undef RSPX_VM
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(3))) char lds_char;
-
-// Direct-to-LDS loads: lane l's bytes land at dst + l * size.  Non-template
+// Direct-to-LDS loads: lane l's bytes land at dst + 16 l.  Non-template
 // wrappers: the host compilation pass rejects these builtins inside templates.
 __device__ __forceinline__ void dma16(const void* src, lds_char* dst) {
   __builtin_amdgcn_global_load_lds(src, (lds_void*)dst, 16, 0, 0);
 }
 // Raw buffer variant: byte offset `voff` from the descriptor base; reads past
-// the descriptor's size return zeros.
+// the descriptor's size return zeros and touch no memory.
 __device__ __forceinline__ void bdma16(__amdgpu_buffer_rsrc_t r, int voff, lds_char* dst) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 16, voff, 0, 0, 0);
 }
-__device__ __forceinline__ void bdma4(__amdgpu_buffer_rsrc_t r, int voff, lds_char* dst) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 4, voff, 0, 0, 0);
-}
 constexpr int kBufWord3 = 0x00020000;  // gfx9 raw-buffer descriptor dword 3
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int64_t nbytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)nbytes, kBufWord3);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           (int)(nbytes > 0 ? nbytes : 0), kBufWord3);
 }
 
-// This wave's share of the chunks of one step into the ring slot at `dst`.
-// The descriptors start at the step's first key and end at key P, so keys past
-// P read zeros.  Chunk j of wave w is c = w + 4 j: K chunk (kb, i) gives lane
-// (n16, g4) K[key 16 kb + n16][32 i + 8 g4, +8); V chunk ii (VPER parts) gives
-// V[key(ii)][DPL n16, +DPL), key(ii) = 4 g4 + ii (ii < 4) or 12 + 4 g4 + ii.
-// voff[j] holds the lane's byte offset of chunk j within a step.
-template <int D>
-__device__ __forceinline__ void issue_step(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
-                                           const int* voff, lds_char* dst, int w) {
+// The transposing LDS read: within each 16-lane row, lane i receives
+// element (i % 4) of the 8 bytes addressed by lane 4 e + i / 4, for e = 0..3.
+__device__ __forceinline__ s16x4 lds_read_tr(const lds_char* p) {
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
+}
+
+__device__ __forceinline__ void lds_barrier() {
+  // Every wave's LDS reads issued so far are complete, then a raw s_barrier:
+  // __syncthreads() would also wait for every direct-to-LDS load in flight.
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// This wave's chunks of one round (4 steps from step `sfirst`) into the ring
+// slot at `dst`: chunk c = w + 8 j is chunk c % CH of step-in-round c / CH.
+// voff[t] is the lane's byte offset of chunk (w + 8 t) % CH relative to the
+// step's first key.  The descriptors cover keys [ks, P) of the kv head, so
+// keys past P (and whole steps past P) read zeros without touching memory.
+template <int D, int NV>
+__device__ __forceinline__ void issue_round(const uint16_t* kpg, const uint16_t* vpg, int64_t skpn, int64_t svpn,
+                                            int P, int sfirst, const int (&voff)[NV], lds_char* dst, int w) {
   using G = StepGeom<D>;
-  constexpr int L = G::CH / kWaves;
 #pragma unroll
-  for (int j = 0; j < L; ++j) {
-    const int c = w + j * kWaves;
-    if (c < G::KCH) {
-      bdma16(rk, voff[j], dst + c * 1024);
-    } else {
-      const int vc = c - G::KCH;
-      if constexpr (G::VS == 16) bdma16(rv, voff[j], dst + G::KBYTES + vc * 1024);
-      else bdma4(rv, voff[j], dst + G::KBYTES + vc * 256);
-    }
+  for (int j = 0; j < G::OWN; ++j) {
+    const int c = w + kWavesA * j;
+    const int sr = c / G::CH, cc = c % G::CH;
+    const int ks = (sfirst + sr) * kStep;
+    if (cc < G::KCH)
+      bdma16(buffer_rsrc(kpg + (int64_t)ks * skpn, 2 * ((int64_t)(P - ks - 1) * skpn + D)), voff[j % NV],
+             dst + sr * G::SLOT + cc * 1024);
+    else
+      bdma16(buffer_rsrc(vpg + (int64_t)ks * svpn, 2 * ((int64_t)(P - ks - 1) * svpn + D)), voff[j % NV],
+             dst + sr * G::SLOT + cc * 1024);
   }
 }
 
 // ------------------------------------------------------------------ kernel A
-// Workgroup (g, rb, q): kv head g, rows [64 kRT rb, +64 kRT) (4 waves x kRT
-// 16-row tiles), key group q = steps [q NS, q NS + NS).  Every wave issues its share
-// of the group's K/V chunks straight into an LDS ring (up to 8 steps in
-// flight, no registers held), then all waves consume the steps in order.
+// Workgroup (g, rb, q): kv head g, rows [32 kRT rb, +32 kRT), key group q =
+// steps [q S, q S + S).  Wave w: row half h = w / 4 (kRT tiles of 16 rows),
+// key quarter k = w % 4 (steps 4 i + k of the group).
 template <int D, int kRT>
-__global__ __launch_bounds__(256) void prompt_kernel(TrieAttnArgs A) {
+__global__ __launch_bounds__(512) void prompt_kernel(TrieAttnArgs A) {
   using G = StepGeom<D>;
-  constexpr int DQ = G::DQ, DPL = G::DPL;
-  static_assert(G::CH % kWaves == 0, "chunks must split evenly over the waves");
-  __shared__ __attribute__((aligned(16))) char ring[kRing * G::SLOT + kWaves * kRT * DQ * 1024];
+  constexpr int DQ = G::DQ, DT = G::DT;
+  constexpr int QBYTES = 2 * kRT * DQ * 1024;
+  constexpr int RINGBYTES = G::RING * G::ROUND;
+  static_assert(kWavesA * kRT * DT * 1024 <= RINGBYTES, "quarter accumulators reuse the ring");
+  static_assert(kWavesA * kRT * 16 * 8 <= QBYTES, "quarter (m, l) reuse the Q area");
+  static_assert(RINGBYTES + QBYTES <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(16))) char lds[RINGBYTES + QBYTES];
 
   const int lane = __lane_id();
-  const int w = threadIdx.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+  const int h = w >> 2, k = w & 3;
   const int n16 = lane & 15, g4 = lane >> 4;
   const int g = blockIdx.x % A.HK;
   const int rest = blockIdx.x / A.HK;
-  const int q = rest % A.NG;
-  const int t0 = (rest / A.NG) * (kWaves * kRT) + w * kRT;   // this wave's first tile
+  const int rb = rest % A.NRB;
+  const int q = rest / A.NRB;
   const int P = A.P;
-  const int kbeg = q * A.RL;
-  const int ns = min(A.RL, P - kbeg + kStep - 1) / kStep;      // steps with >= 1 valid key
-  const bool has_rows = 16 * t0 < A.R;
+  const int steps = (P + kStep - 1) / kStep;
+  const int s0 = q * A.S;                       // first step of the group
+  const int ns = min(A.S, steps - s0);          // steps of the group (>= 1)
+  const int nr = (ns + kQuarters - 1) / kQuarters;
+  const int row0 = rb * 32 * kRT;               // first row of the block
+  const int trow = row0 + 16 * kRT * h;         // first row of this wave's tiles
+  const bool has_rows = trow < A.R;
 
-  // Q^T fragments (B operand of S^T = K Q^T): row n16 of each tile, head_dim
-  // [32 i + 8 g4, +8).  They travel through LDS like K/V (issued before the
-  // K/V ring, so the step-0 wait covers them).  Rows past R read row 0 and
-  // are never stored.
-  lds_char* qreg = (lds_char*)ring + kRing * G::SLOT + w * (kRT * DQ * 1024);
-#pragma unroll
-  for (int t = 0; t < kRT; ++t) {
-    const int r = 16 * (t0 + t) + n16;
+  lds_char* ring = (lds_char*)lds;
+  lds_char* qreg = ring + RINGBYTES;
+
+  // Q^T fragments (B operand of S^T = K Q^T): chunk (tile T, i) holds, for
+  // lane (n16, g4), row 16 T + n16 of the block, head_dim [32 i + 8 g4, +8).
+  // Rows past R read row 0 and are never stored.
+  for (int c = w; c < 2 * kRT * DQ; c += kWavesA) {
+    const int T = c / DQ, i = c - T * DQ;
+    const int r = row0 + 16 * T + n16;
     const int rc = r < A.R ? r : 0;
     const int mq = rc / A.GQA, jh = rc - mq * A.GQA;
-    const uint16_t* base = A.q + (g * A.GQA + jh) * A.sqh + (int64_t)mq * A.sqm + 8 * g4;
-#pragma unroll
-    for (int i = 0; i < DQ; ++i)
-      dma16(base + 32 * i, qreg + (t * DQ + i) * 1024);
+    dma16(A.q + (int64_t)(g * A.GQA + jh) * A.sqh + (int64_t)mq * A.sqm + 32 * i + 8 * g4, qreg + c * 1024);
   }
-  bf16x8 qop[kRT][DQ];
 
-  const uint16_t* kpg = A.kp + g * A.skph;
-  const uint16_t* vpg = A.vp + g * A.svph;
-  lds_char* ringp = (lds_char*)ring;
-  constexpr int L = G::CH / kWaves;
-  int voff[L];
+  // This wave's chunks of a round: c = w + 8 j, step-in-round c / CH, chunk
+  // c % CH.  voff[t] is the lane's byte offset of chunk w + 8 t (mod CH)
+  // relative to the step's first key.
+  constexpr int NV = G::CH >= kWavesA ? G::CH / kWavesA : 1;
+  int voff[NV];
 #pragma unroll
-  for (int j = 0; j < L; ++j) {
-    const int c = w + j * kWaves;
-    if (c < G::KCH) {
-      const int kb = c / DQ, i = c - kb * DQ;
-      voff[j] = 2 * ((16 * kb + n16) * (int)A.skpn + 32 * i + 8 * g4);
+  for (int t = 0; t < NV; ++t) {
+    const int cc = (w + kWavesA * t) % G::CH;
+    if (cc < G::KCH) {
+      const int kb = cc / DQ, i = cc - kb * DQ;
+      voff[t] = 2 * ((16 * kb + n16) * (int)A.skpn + 32 * i + 8 * g4);
     } else {
-      const int vc = c - G::KCH;
-      const int ii = vc / G::VPER, part = vc - ii * G::VPER;
-      const int key = ii < 4 ? 4 * g4 + ii : 12 + 4 * g4 + ii;
-      voff[j] = 2 * (key * (int)A.svpn + DPL * n16) + part * G::VS;
+      const int key = G::KPV * (cc - G::KCH) + lane / G::U;
+      const int b = (lane % G::U) ^ vswz<D>(key);
+      voff[t] = 2 * key * (int)A.svpn + 16 * b;
     }
   }
-  // Descriptors covering keys [ks, P) of this kv head.
-#define RSPX_RK(ks) buffer_rsrc(kpg + (int64_t)(ks) * A.skpn, 2 * ((int64_t)(P - (ks) - 1) * A.skpn + D))
-#define RSPX_RV(ks) buffer_rsrc(vpg + (int64_t)(ks) * A.svpn, 2 * ((int64_t)(P - (ks) - 1) * A.svpn + D))
+  const uint16_t* kpg = A.kp + g * A.skph;
+  const uint16_t* vpg = A.vp + g * A.svph;
+
+  // Transposing-read addresses of the V operand halves (keys 4 g4 + e and
+  // 16 + 4 g4 + e) for head_dim tile j, relative to a step slot.
+  int trv[2][DT];
+  {
+    const int e = n16 >> 2, c4 = n16 & 3;
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      const int key = 16 * kh + 4 * g4 + e;
+#pragma unroll
+      for (int j = 0; j < DT; ++j) {
+        const int b = 2 * j + (c4 >> 1);
+        trv[kh][j] = G::KBYTES + 16 * (key * G::U + (b ^ vswz<D>(key))) + 8 * (c4 & 1);
+      }
+    }
+  }
 
   float mref[kRT], lrow[kRT];
-  f32x4 acc[kRT][DPL];
+  f32x4 acc[kRT][DT];
 #pragma unroll
   for (int t = 0; t < kRT; ++t) {
     mref[t] = kNegInf;
     lrow[t] = 0.f;
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < DT; ++j) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  const int pro = min(ns, kRing);
-  for (int s = 0; s < pro; ++s)
-    issue_step<D>(RSPX_RK(kbeg + s * kStep), RSPX_RV(kbeg + s * kStep), voff, ringp + s * G::SLOT, w);
-  // The Q chunks were issued first, so they are done once at most the K/V
-  // chunks are outstanding; each wave reads only its own Q region.
-  wait_vm(L * pro);
-  if (has_rows) {
-#pragma unroll
-    for (int t = 0; t < kRT; ++t)
-#pragma unroll
-      for (int i = 0; i < DQ; ++i)
-        qop[t][i] = __builtin_bit_cast(
-            bf16x8, *(const __attribute__((address_space(3))) u32x4*)(qreg + (t * DQ + i) * 1024 + 16 * lane));
-  }
+  const int pro = min(nr, G::RING);
+  for (int rr = 0; rr < pro; ++rr) issue_round<D>(kpg, vpg, A.skpn, A.svpn, P, s0 + kQuarters * rr, voff, ring + (rr % G::RING) * G::ROUND, w);
 
-  for (int s = 0; s < ns; ++s) {
-    // Own chunks of step s have landed: allow the later steps already issued.
-    const int hi = s == 0 ? pro - 1 : min(ns - 1, s + kRing - 2);
-    wait_vm(L * (hi - s));
-    // Every wave's chunks of step s are in LDS and step s-1 is consumed.  A raw
-    // s_barrier: __syncthreads() would also wait for every LDS DMA in flight.
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's reads of step s-1 are done
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    if (s >= 1 && s + kRing - 1 < ns) {
-      const int kn = kbeg + (s + kRing - 1) * kStep;
-      issue_step<D>(RSPX_RK(kn), RSPX_RV(kn), voff, ringp + ((s - 1) % kRing) * G::SLOT, w);
+  bf16x8 qop[kRT][DQ];
+  for (int r = 0; r < nr; ++r) {
+    // Own chunks of round r (and the Q chunks, issued first) have landed.
+    const int issued = min(nr, G::RING + r);
+    wait_vm(G::OWN * (issued - r - 1));
+    lds_barrier();   // every wave's chunks of round r are in LDS
+    if (r == 0 && has_rows) {
+#pragma unroll
+      for (int t = 0; t < kRT; ++t)
+#pragma unroll
+        for (int i = 0; i < DQ; ++i)
+          qop[t][i] = __builtin_bit_cast(
+              bf16x8, *(const __attribute__((address_space(3))) u32x4*)(
+                          qreg + ((kRT * h + t) * DQ + i) * 1024 + 16 * lane));
     }
-    if (!has_rows) continue;
+    const int sl = kQuarters * r + k;  // step of this wave within the group
+    if (has_rows && sl < ns) {
 
-    const lds_char* slot = ringp + (s % kRing) * G::SLOT;
-    const int ks = kbeg + s * kStep;
+    const lds_char* slot = ring + (r % G::RING) * G::ROUND + k * G::SLOT;
+    const int ks = (s0 + sl) * kStep;
     u32x4 kf[2][DQ];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int i = 0; i < DQ; ++i)
         kf[kb][i] = *(const __attribute__((address_space(3))) u32x4*)(slot + (kb * DQ + i) * 1024 + 16 * lane);
-    typename VRow<D>::T vf[8];
-#pragma unroll
-    for (int ii = 0; ii < 8; ++ii) {
-      if constexpr (G::VPER == 1) {
-        vf[ii] = *(const __attribute__((address_space(3))) typename VRow<D>::T*)(
-            slot + G::KBYTES + ii * 1024 + 16 * lane);
-      } else {
-#pragma unroll
-        for (int part = 0; part < G::VPER; ++part)
-          vf[ii][part] = *(const __attribute__((address_space(3))) uint32_t*)(
-              slot + G::KBYTES + (ii * G::VPER + part) * 256 + 4 * lane);
-      }
-    }
 
     // S^T = K Q^T for two blocks of 16 keys.
     f32x4 sc[kRT][2];
@@ -432,8 +423,8 @@ __global__ __launch_bounds__(256) void prompt_kernel(TrieAttnArgs A) {
       }
 
     // Lane (n16, g4) holds row n16, keys 16 kb + 4 g4 + e of the step.  Raw
-    // scores; keys past P (only in a group's last step) are masked to -inf.
-    // Since scale > 0, max(s) * c is exactly the max of the scaled scores.
+    // scores; keys past P (only in the last step) are masked to -inf.  Since
+    // scale > 0, max(s) * c is exactly the max of the scaled scores.
     bf16x8 pop[kRT];
     float mx[kRT];
     float s8[kRT][8];
@@ -471,7 +462,7 @@ __global__ __launch_bounds__(256) void prompt_kernel(TrieAttnArgs A) {
         for (int e = 0; e < 4; ++e) {
           const float ae = shfl_idx(alpha, 4 * g4 + e);
 #pragma unroll
-          for (int j = 0; j < DPL; ++j) acc[t][j][e] = acc[t][j][e] * ae;
+          for (int j = 0; j < DT; ++j) acc[t][j][e] = acc[t][j][e] * ae;
         }
       }
     }
@@ -490,187 +481,295 @@ __global__ __launch_bounds__(256) void prompt_kernel(TrieAttnArgs A) {
       pop[t] = __builtin_bit_cast(bf16x8, pw);
     }
 
-    // O += bf16(P) V.  B operand of MFMA j: lane (n16, g4) supplies
-    // V[key(8 g4 + ii)][DPL n16 + j], ii = 0..7 -- a register transpose of the
-    // 8 rows it holds.  Output lane: rows 4 g4 + e, head_dim DPL n16 + j.
+    // O += bf16(P) V.  A operand: lane (n16, g4) holds row n16's p at k-slots
+    // 8 g4 + i <-> keys 4 g4 + i (i < 4) and 12 + 4 g4 + i.  B operand of
+    // head_dim tile j: V[key(k-slot)][16 j + n16], two transposing reads.
+    // Output lane: rows 4 g4 + e, head_dim 16 j + n16.
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      u32x4 bj;
-#pragma unroll
-      for (int pp = 0; pp < 4; ++pp) {
-        const uint32_t wa = vf[2 * pp][j >> 1];
-        const uint32_t wb = vf[2 * pp + 1][j >> 1];
-        bj[pp] = (j & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
-      }
-      const bf16x8 vop = __builtin_bit_cast(bf16x8, bj);
+    for (int j = 0; j < DT; ++j) {
+      const s16x4 lo = lds_read_tr(slot + trv[0][j]);
+      const s16x4 hi = lds_read_tr(slot + trv[1][j]);
+      const bf16x8 vop = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
       for (int t = 0; t < kRT; ++t)
         acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop[t], vop, acc[t][j], 0, 0, 0);
     }
+    }
+    // Round r is consumed by every wave: its ring slot takes round r + RING.
+    if (r + G::RING < nr) {
+      lds_barrier();
+      issue_round<D>(kpg, vpg, A.skpn, A.svpn, P, s0 + kQuarters * (r + G::RING), voff,
+                     ring + (r % G::RING) * G::ROUND, w);
+    }
   }
+
+  // Quarter partials through LDS (ring and Q area are free once every wave
+  // is past its last step): wave w's acc[t][j] as [t][j][lane] f32x4 in the
+  // ring, its (m, l) of rows 16 t + n16 in the Q area.
+  lds_barrier();
+  constexpr int REG = kRT * DT * 1024;
+  constexpr int REGML = kRT * 16 * 8;
+  if (has_rows) {
+#pragma unroll
+    for (int t = 0; t < kRT; ++t) {
+#pragma unroll
+      for (int j = 0; j < DT; ++j)
+        *(__attribute__((address_space(3))) f32x4*)(ring + w * REG + (t * DT + j) * 1024 + 16 * lane) = acc[t][j];
+      if (g4 == 0) {
+        __attribute__((address_space(3))) float* ml =
+            (__attribute__((address_space(3))) float*)(qreg + w * REGML) + 2 * (16 * t + n16);
+        ml[0] = mref[t];
+        ml[1] = lrow[t];
+      }
+    }
+  }
+  lds_barrier();
   if (!has_rows) return;
 
-  // Group partial of each row straight from the MFMA layout.
+  // Wave (h, k) combines units u = k UPW .. of its half (all in tile
+  // t = u / DT): quarters 0..3 in order, per row, then stores the group
+  // partial.  The combine weights of a row depend on its (m, l) only, so they
+  // are formed once per row and applied to every unit.
+  constexpr int UNITS = kRT * DT;
+  constexpr int UPW = UNITS / kQuarters;
+  static_assert(UNITS % kQuarters == 0 && DT % UPW == 0, "units split evenly over the quarters");
+  const int u0 = k * UPW;
+  const int t = u0 / DT;
+  float wa[4][kQuarters], wb[4][kQuarters], cm[4], cl[4];
 #pragma unroll
-  for (int t = 0; t < kRT; ++t) {
-    if (g4 == 0) {
-      const int r = 16 * (t0 + t) + n16;
-      if (r < A.R) {
-        const size_t idx = ((size_t)g * A.R + r) * A.NG + q;
-        A.gp_ml[idx * 2] = mref[t];
-        A.gp_ml[idx * 2 + 1] = lrow[t];
+  for (int e = 0; e < 4; ++e) {
+    cm[e] = kNegInf;
+    cl[e] = 0.f;
+#pragma unroll
+    for (int kq = 0; kq < kQuarters; ++kq) {
+      const __attribute__((address_space(3))) float* ml =
+          (const __attribute__((address_space(3))) float*)(qreg + (4 * h + kq) * REGML) + 2 * (16 * t + 4 * g4 + e);
+      const float m2 = ml[0], l2 = ml[1];
+      // combine() with the accumulator update left for later: an empty
+      // quarter (m2 = -inf) contributes a = 1, b = 0 (an exact no-op).
+      if (m2 == kNegInf) {
+        wa[e][kq] = 1.f;
+        wb[e][kq] = 0.f;
+      } else {
+        const float mn = fmaxf(cm[e], m2);
+        wa[e][kq] = fexp2(cm[e] - mn);
+        wb[e][kq] = fexp2(m2 - mn);
+        cl[e] = __builtin_fmaf(l2, wb[e][kq], cl[e] * wa[e][kq]);
+        cm[e] = mn;
       }
+    }
+  }
+#pragma unroll
+  for (int uu = 0; uu < UPW; ++uu) {
+    const int j = (u0 + uu) - t * DT;
+    float ca[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kq = 0; kq < kQuarters; ++kq) {
+      const f32x4 a4 =
+          *(const __attribute__((address_space(3))) f32x4*)(ring + (4 * h + kq) * REG + (u0 + uu) * 1024 + 16 * lane);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ca[e] = __builtin_fmaf(a4[e], wb[e][kq], ca[e] * wa[e][kq]);
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int r = 16 * (t0 + t) + 4 * g4 + e;
+      const int r = trow + 16 * t + 4 * g4 + e;
       if (r < A.R) {
-        float* dst = A.gp_acc + (((size_t)g * A.R + r) * A.NG + q) * D + DPL * n16;
-#pragma unroll
-        for (int j = 0; j < DPL; j += 4)
-          *reinterpret_cast<f32x4*>(dst + j) = f32x4{acc[t][j][e], acc[t][j + 1][e], acc[t][j + 2][e], acc[t][j + 3][e]};
+        const size_t idx = ((size_t)g * A.R + r) * A.NG + q;
+        A.gp_acc[idx * D + 16 * j + n16] = ca[e];
+        if (j == 0 && n16 == 0) {
+          A.gp_ml[idx * 2] = cm[e];
+          A.gp_ml[idx * 2 + 1] = cl[e];
+        }
       }
     }
   }
 }
 
-#undef RSPX_RK
-#undef RSPX_RV
-
 // ------------------------------------------------------------------ kernel B
-// One wave per (query row mq, head h); a workgroup holds 4 consecutive heads of
-// the same row (they share the node list and, for GQA >= 4, the kv head).
-// Lanes split head_dim (DN = D / 64 values each).  Node fold, then the final
-// combine (groups in order, node partial last) and the bf16 store.
+template <int DN> struct NodeVec;
+template <> struct NodeVec<8> { typedef u32x4 T; };
+template <> struct NodeVec<4> { typedef u32x2 T; };
+
+constexpr int kChunk = 64;  // node slots staged in LDS at a time
+
+// Workgroup (g, c8): rows r = 8 c8 + 4 w + e of kv head g (wave w, lane
+// 16 e + n holds head_dim [DN n, +DN) of row e).  The node K/V of a 64-slot
+// chunk is copied into LDS once for the 8 rows while their masks are read;
+// each row folds its allowed slots in slot order; then the group partials are
+// combined in group order and the node partial last, and bf16 is stored.
 template <int D>
-__global__ __launch_bounds__(256) void node_merge_kernel(TrieAttnArgs A) {
-  constexpr int DN = D / 64;
-  constexpr int kB = 8;            // node slots per load batch
-  constexpr int kMaxG = 16;        // groups per kv head (NG <= 16 by construction)
-  __shared__ int16_t lds_list[4][kMaxNodeSlots];
+__global__ __launch_bounds__(64 * kWavesB) void node_merge_kernel(TrieAttnArgs A) {
+  constexpr int DN = D / 16;
+  constexpr int RB = 2 * D;                          // bytes per node row
+  constexpr int CHB = kChunk * RB;                   // bytes of K (or V) per chunk
+  constexpr int NDMA = 2 * CHB / 1024 / kWavesB;     // 1 KB loads per wave per chunk
+  constexpr int kB = 8;                              // slots per fold batch
+  typedef typename NodeVec<DN>::T VecT;
+  constexpr int NW = DN / 2;                         // 32-bit words per lane vector
+  __shared__ __attribute__((aligned(16))) char kv[2 * CHB];  // K rows, then V rows
 
   const int lane = __lane_id();
-  const int w = threadIdx.x >> 6;
-  const int HB = (A.HK * A.GQA + 3) / 4;
-  const int hb = blockIdx.x % HB;
-  const int mq = blockIdx.x / HB;
-  const int h = hb * 4 + w;
-  if (h >= A.HK * A.GQA) return;
-  const int g = h / A.GQA;
-  const int r = mq * A.GQA + (h - g * A.GQA);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+  const int e = lane >> 4, n = lane & 15;
+  const int RC8 = (A.R + 7) / 8;
+  const int g = blockIdx.x / RC8;
+  const int c8 = blockIdx.x - g * RC8;
+  const int r = 8 * c8 + 4 * w + e;
+  const bool live = r < A.R;
+  const int rr = live ? r : 8 * c8;  // rows past R shadow the block's first row
+  const int mq = rr / A.GQA;
+  const int hd = g * A.GQA + (rr - mq * A.GQA);
+  const int d0 = DN * n;
   const int NG = A.NG;
-  const int d0 = lane * DN;
+  const int NN = A.NN;
+  lds_char* kvl = (lds_char*)kv;
+
+  // In issue order: q, the mask of chunk 0, chunk 0's K/V into LDS, the group
+  // partials (consumed last).
+  const VecT qv = *reinterpret_cast<const VecT*>(A.q + hd * A.sqh + (int64_t)mq * A.sqm + d0);
+  const uint8_t* mrow = A.msk + (int64_t)mq * A.smm;
+  uint8_t mb[4];
+  auto load_mask = [&](int c0) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int t = c0 + 16 * b + n;
+      mb[b] = (live && t < NN) ? mrow[(int64_t)t * A.smn] : (uint8_t)0;
+    }
+  };
+  const uint16_t* knb = A.kn + g * A.sknh;
+  const uint16_t* vnb = A.vn + g * A.svnh;
+  auto load_chunk = [&](int c0) {
+    const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(knb + (int64_t)c0 * A.sknn, 2 * ((int64_t)(NN - c0 - 1) * A.sknn + D));
+    const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(vnb + (int64_t)c0 * A.svnn, 2 * ((int64_t)(NN - c0 - 1) * A.svnn + D));
+#pragma unroll
+    for (int jj = 0; jj < NDMA; ++jj) {
+      const int x = w + kWavesB * jj;          // 1 KB piece of [K rows | V rows]
+      const int byte = (x * 1024 + 16 * lane) % CHB;
+      const int slot = byte / RB, unit = (byte % RB) / 16;
+      if (x * 1024 < CHB) bdma16(rk, 2 * slot * (int)A.sknn + 16 * unit, kvl + x * 1024);
+      else bdma16(rv, 2 * slot * (int)A.svnn + 16 * unit, kvl + x * 1024);
+    }
+  };
+  if (NN > 0) {
+    load_mask(0);
+    load_chunk(0);
+  }
+  asm volatile("" ::: "memory");  // the waits below count on this issue order
+  float gm[kGroupTarget], gl[kGroupTarget];
+  f32x4 ga[kGroupTarget][DN / 4];
+  const size_t gbase = ((size_t)g * A.R + rr) * NG;
+#pragma unroll
+  for (int qq = 0; qq < kGroupTarget; ++qq) {
+    if (qq < NG) {
+      const float2 ml = *reinterpret_cast<const float2*>(A.gp_ml + (gbase + qq) * 2);
+      gm[qq] = ml.x;
+      gl[qq] = ml.y;
+#pragma unroll
+      for (int v = 0; v < DN / 4; ++v)
+        ga[qq][v] = *reinterpret_cast<const f32x4*>(A.gp_acc + (gbase + qq) * D + d0 + 4 * v);
+    }
+  }
+  const int npart = NG * (DN / 4 + 1);  // partial loads still in flight behind the chunk
 
   float qf[DN];
-  load_row_f32<DN>(A.q + h * A.sqh + (int64_t)mq * A.sqm + d0, qf);
-
-  // List the allowed node slots in slot order.
-  int16_t* list = lds_list[w];
-  const uint8_t* mrow = A.msk + (int64_t)mq * A.smm;
-  int T = 0;
-  for (int c0 = 0; c0 < A.NN; c0 += 64) {
-    const int t = c0 + lane;
-    const bool allowed = (t < A.NN) && (mrow[(int64_t)t * A.smn] != 0);
-    const uint64_t bits = __builtin_amdgcn_ballot_w64(allowed);
-    const int pos = __builtin_amdgcn_mbcnt_hi((uint32_t)(bits >> 32),
-                                              __builtin_amdgcn_mbcnt_lo((uint32_t)bits, 0));
-    if (allowed) list[T + pos] = (int16_t)t;
-    T += __builtin_popcountll(bits);
-  }
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the list writes are visible to the wave
-  __builtin_amdgcn_wave_barrier();
-
+#pragma unroll
+  for (int i = 0; i < NW; ++i) { qf[2 * i] = bf16_lo(qv[i]); qf[2 * i + 1] = bf16_hi(qv[i]); }
   float m = kNegInf, l = 0.f, acc[DN];
 #pragma unroll
   for (int i = 0; i < DN; ++i) acc[i] = 0.f;
-  const uint16_t* kb = A.kn + g * A.sknh + d0;
-  const uint16_t* vb = A.vn + g * A.svnh + d0;
 
-  uint32_t kr[2][kB], vr[2][kB];   // DN bf16 per lane: one packed word (DN = 2) or a half (DN = 1)
-  auto ld = [&](const uint16_t* p) -> uint32_t {
-    if constexpr (DN == 2) return *reinterpret_cast<const uint32_t*>(p);
-    else return *p;
-  };
-  auto load_batch = [&](int b0, int buf) {
-#pragma unroll
-    for (int u = 0; u < kB; ++u) {
-      const int tt = list[min(b0 + u, T - 1)];
-      kr[buf][u] = ld(kb + (int64_t)tt * A.sknn);
-      vr[buf][u] = ld(vb + (int64_t)tt * A.svnn);
+  for (int c0 = 0; c0 < NN; c0 += kChunk) {
+    if (c0 > 0) {
+      lds_barrier();       // both waves are done with the previous chunk
+      load_mask(c0);
+      load_chunk(c0);
+      wait_vm(NDMA);       // the mask
+    } else {
+      wait_vm(NDMA + npart);
     }
-  };
-  if (T > 0) load_batch(0, 0);
-  // Group partials of this row, requested after the first K/V batch (loads
-  // complete in order) and consumed after the fold.
-  float gm[kMaxG], gl[kMaxG], ga[kMaxG][DN];
-  const size_t gbase = ((size_t)g * A.R + r) * NG;
+    // Row e's allowed slots of the chunk: lane (e, n) tested slots 16 b + n.
+    uint64_t mm = 0;
 #pragma unroll
-  for (int qq = 0; qq < kMaxG; ++qq) {
-    if (qq < NG) {
-      gm[qq] = A.gp_ml[(gbase + qq) * 2];
-      gl[qq] = A.gp_ml[(gbase + qq) * 2 + 1];
-      const float* src = A.gp_acc + (gbase + qq) * D + d0;
-      if constexpr (DN == 2) {
-        const float2 v2 = *reinterpret_cast<const float2*>(src);
-        ga[qq][0] = v2.x; ga[qq][1] = v2.y;
-      } else {
-        ga[qq][0] = src[0];
+    for (int b = 0; b < 4; ++b) {
+      const uint64_t bits = __builtin_amdgcn_ballot_w64(mb[b] != 0);
+      mm |= ((bits >> (16 * e)) & 0xffffull) << (16 * b);
+    }
+    const int cnt = __builtin_popcountll(mm);
+    const int cmax = max(max(__shfl(cnt, 0), __shfl(cnt, 16)), max(__shfl(cnt, 32), __shfl(cnt, 48)));
+    wait_vm(c0 > 0 ? 0 : npart);  // this wave's part of the chunk is in LDS
+    lds_barrier();                // and the other wave's part
+
+    for (int b0 = 0; b0 < cmax; b0 += kB) {
+      int js[kB];
+      bool ok[kB];
+#pragma unroll
+      for (int u = 0; u < kB; ++u) {
+        ok[u] = mm != 0;
+        js[u] = ok[u] ? __builtin_ctzll(mm) : 0;
+        mm &= mm - 1;
+      }
+      VecT kr[kB], vr[kB];
+#pragma unroll
+      for (int u = 0; u < kB; ++u) {
+        kr[u] = *(const __attribute__((address_space(3))) VecT*)(kvl + js[u] * RB + 2 * d0);
+        vr[u] = *(const __attribute__((address_space(3))) VecT*)(kvl + CHB + js[u] * RB + 2 * d0);
+      }
+      float sc[kB];
+#pragma unroll
+      for (int u = 0; u < kB; ++u) {
+        float dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+          dot = __builtin_fmaf(qf[2 * i], bf16_lo(kr[u][i]), dot);
+          dot = __builtin_fmaf(qf[2 * i + 1], bf16_hi(kr[u][i]), dot);
+        }
+        sc[u] = sum16(dot) * A.c;
+      }
+#pragma unroll
+      for (int u = 0; u < kB; ++u) {
+        if (ok[u]) {
+          const float mn = fmaxf(m, sc[u]);
+          const float a = fexp2(m - mn);
+          const float p = fexp2(sc[u] - mn);
+          l = __builtin_fmaf(l, a, p);
+#pragma unroll
+          for (int i = 0; i < NW; ++i) {
+            acc[2 * i] = __builtin_fmaf(p, bf16_lo(vr[u][i]), acc[2 * i] * a);
+            acc[2 * i + 1] = __builtin_fmaf(p, bf16_hi(vr[u][i]), acc[2 * i + 1] * a);
+          }
+          m = mn;
+        }
       }
     }
   }
-
-  for (int b0 = 0; b0 < T; b0 += 2 * kB) {
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const int bb = b0 + half * kB;
-      if (bb >= T) break;
-      if (bb + kB < T) load_batch(bb + kB, half ^ 1);
-      float s[kB];
-#pragma unroll
-      for (int u = 0; u < kB; ++u) {
-        float dot = __builtin_fmaf(qf[0], bf16_lo(kr[half][u]), 0.f);
-        if constexpr (DN == 2) dot = __builtin_fmaf(qf[1], bf16_hi(kr[half][u]), dot);
-        s[u] = group_sum<64>(dot) * A.c;
-      }
-#pragma unroll
-      for (int u = 0; u < kB; ++u) {
-        if (bb + u >= T) break;
-        const float mn = fmaxf(m, s[u]);
-        const float a = fexp2(m - mn);
-        const float p = fexp2(s[u] - mn);
-        l = __builtin_fmaf(l, a, p);
-        acc[0] = __builtin_fmaf(p, bf16_lo(vr[half][u]), acc[0] * a);
-        if constexpr (DN == 2) acc[1] = __builtin_fmaf(p, bf16_hi(vr[half][u]), acc[1] * a);
-        m = mn;
-      }
-    }
-  }
+  wait_vm(0);  // the group partials
 
   // Final: groups in order, then the node partial.
   float fm = kNegInf, fl = 0.f, facc[DN];
 #pragma unroll
   for (int i = 0; i < DN; ++i) facc[i] = 0.f;
 #pragma unroll
-  for (int qq = 0; qq < kMaxG; ++qq)
-    if (qq < NG) combine<DN>(fm, fl, facc, gm[qq], gl[qq], ga[qq]);
+  for (int qq = 0; qq < kGroupTarget; ++qq)
+    if (qq < NG) combine<DN>(fm, fl, facc, gm[qq], gl[qq], reinterpret_cast<const float*>(ga[qq]));
   combine<DN>(fm, fl, facc, m, l, acc);
 
-  uint16_t* o = A.out + h * A.soh + (int64_t)mq * A.som + d0;
-  if constexpr (DN == 2) *reinterpret_cast<uint32_t*>(o) = pack_bf16x2(facc[0] / fl, facc[1] / fl);
-  else o[0] = f32_to_bf16_rne(facc[0] / fl);
+  if (!live) return;
+  VecT ov;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) ov[i] = pack_bf16x2(facc[2 * i] / fl, facc[2 * i + 1] / fl);
+  *reinterpret_cast<VecT*>(A.out + hd * A.soh + (int64_t)mq * A.som + d0) = ov;
 }
 
 // ------------------------------------------------------------------ host side
 
 struct Plan {
-  int GQA, R, NT, RT, NG, RL, prompt_wgs, node_wgs;
+  int GQA, R, RT, NRB, NG, S, prompt_wgs, node_wgs;
   size_t off_gp_ml, off_gp_acc, total;
 };
 
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Group length RL (keys) and count NG depend on P only: NG <= 16 groups of a
-// whole number of 32-key steps.
+// Steps per group S = 4 NR and the group count NG <= 8 depend on P only.
 static int make_plan(int H, int HK, int M, int P, int NN, int D, int rows_per_wave, Plan* pl) {
   if (H <= 0 || HK <= 0 || M < 0 || P < 0 || NN < 0 || H % HK != 0) return RSPX_EINVAL;
   if (NN > kMaxNodeSlots) return RSPX_EINVAL;
@@ -679,22 +778,21 @@ static int make_plan(int H, int HK, int M, int P, int NN, int D, int rows_per_wa
   if (GQA != 1 && GQA != 2 && GQA != 4 && GQA != 8 && GQA != 16) return RSPX_EUNSUPPORTED;
   pl->GQA = GQA;
   pl->R = M * GQA;
-  pl->NT = (pl->R + 15) / 16;
   if (P > 0) {
     const int steps = (P + kStep - 1) / kStep;
-    const int ns = (steps + kNGTarget - 1) / kNGTarget;
-    pl->RL = ns * kStep;
-    pl->NG = (P + pl->RL - 1) / pl->RL;
+    const int nr = (steps + kQuarters * kGroupTarget - 1) / (kQuarters * kGroupTarget);
+    pl->S = kQuarters * nr;
+    pl->NG = (steps + pl->S - 1) / pl->S;
   } else {
-    pl->RL = kStep;
+    pl->S = kQuarters;
     pl->NG = 0;
   }
   const int rt = rows_per_wave == 0 ? 2 : rows_per_wave;
   if (rt != 1 && rt != 2) return RSPX_EINVAL;
   pl->RT = rt;
-  const int rows_per_wg = kWaves * rt * 16;
-  pl->prompt_wgs = HK * ((pl->R + rows_per_wg - 1) / rows_per_wg) * pl->NG;
-  pl->node_wgs = M * ((H + 3) / 4);
+  pl->NRB = (pl->R + 32 * rt - 1) / (32 * rt);
+  pl->prompt_wgs = HK * pl->NRB * pl->NG;
+  pl->node_wgs = HK * ((pl->R + 7) / 8);
   const size_t parts = (size_t)HK * pl->R * pl->NG;
   size_t off = 0;
   pl->off_gp_ml = off;  off = align256(off + parts * 2 * sizeof(float));
@@ -706,10 +804,10 @@ static int make_plan(int H, int HK, int M, int P, int NN, int D, int rows_per_wa
 template <int D>
 static void launch_all(const TrieAttnArgs& a, const Plan& pl, hipStream_t s) {
   if (pl.prompt_wgs > 0) {
-    if (pl.RT == 1) hipLaunchKernelGGL((prompt_kernel<D, 1>), dim3(pl.prompt_wgs), dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((prompt_kernel<D, 2>), dim3(pl.prompt_wgs), dim3(256), 0, s, a);
+    if (pl.RT == 1) hipLaunchKernelGGL((prompt_kernel<D, 1>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);
+    else hipLaunchKernelGGL((prompt_kernel<D, 2>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);
   }
-  hipLaunchKernelGGL((node_merge_kernel<D>), dim3(pl.node_wgs), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((node_merge_kernel<D>), dim3(pl.node_wgs), dim3(64 * kWavesB), 0, s, a);
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -748,6 +846,11 @@ extern "C" int rspx_trie_attn(const void* q, int64_t sqh, int64_t sqm,
   const int64_t strides[] = {sqh, sqm, skph, skpn, svph, svpn, sknh, sknn, svnh, svnn, soh, som};
   for (int64_t s : strides)
     if (s % 8 != 0) return RSPX_EALIGN;
+  // Byte offsets inside one kv head's prompt K/V are 32-bit.
+  if (P > 0 && ((int64_t)P * skpn * 2 >= (1ll << 31) || (int64_t)P * svpn * 2 >= (1ll << 31)))
+    return RSPX_EUNSUPPORTED;
+  if (NN > 0 && ((int64_t)NN * sknn * 2 >= (1ll << 31) || (int64_t)NN * svnn * 2 >= (1ll << 31)))
+    return RSPX_EUNSUPPORTED;
 
   TrieAttnArgs a;
   a.q = static_cast<const uint16_t*>(q);   a.sqh = sqh;   a.sqm = sqm;
@@ -758,7 +861,7 @@ extern "C" int rspx_trie_attn(const void* q, int64_t sqh, int64_t sqm,
   a.msk = msk; a.smm = smm; a.smn = smn;
   a.out = static_cast<uint16_t*>(out); a.soh = soh; a.som = som;
   a.HK = HK; a.GQA = pl.GQA; a.M = M; a.P = P; a.NN = NN;
-  a.R = pl.R; a.NT = pl.NT; a.NG = pl.NG; a.RL = pl.RL;
+  a.R = pl.R; a.NRB = pl.NRB; a.NG = pl.NG; a.S = pl.S;
   a.c = (float)((double)sm_scale * 1.4426950408889634);
   char* ws = static_cast<char*>(workspace);
   a.gp_ml = reinterpret_cast<float*>(ws + pl.off_gp_ml);
