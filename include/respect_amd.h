@@ -15,6 +15,13 @@
  *   rspx_qk_norm_rope   respect/kernels/rmsnorm.py:25 followed by the RoPE of
  *                       HF apply_rotary_pos_emb (q_norm/k_norm + RoPE of one decoder layer)
  *   rspx_silu_mul       respect/system/fused.py:116      silu_mul(g, u)
+ *   rspx_linear         respect/kernels/gemm.py:30       linear(x, w, ..., out_dtype)
+ *   rspx_add_rmsnorm    residual add (HF decoder layer) followed by rmsnorm, rmsnorm.py:25
+ *   rspx_qkv_rope_cache q_norm/k_norm + RoPE + KV write of one decoder layer
+ *                       (rmsnorm.py:25, HF apply_rotary_pos_emb, kv_buffer.py:32-36 update)
+ *   rspx_trie_mask      respect/decoding/verify.py:22-41 mask + dispatch.py:94-115 padding
+ *   rspx_kv_compact     respect/decoding/kv_buffer.py:93 compact(cache, prompt_len, base, slots)
+ *   rspx_argmax_rows    respect/decoding/acceptance.py:20 greedy_token(logits, offset, size)
  */
 #ifndef RESPECT_AMD_H
 #define RESPECT_AMD_H
@@ -124,6 +131,71 @@ int rspx_qk_norm_rope(const void* q, int64_t sqt, int64_t sqh, const void* k, in
  */
 int rspx_silu_mul(const void* g, int64_t sg, const void* u, int64_t su, void* y, int64_t sy, int rows, int cols,
                   void* stream);
+
+/* ---------------------------------------------------------------- linear
+ * out[M, N] = x[M, K] . w[N, K]^T, bf16 inputs, fp32 accumulation, output
+ * bf16 (out_fp32 = 0) or fp32 (out_fp32 = 1) (replaces
+ * respect/kernels/gemm.py:30 linear(x, w, ..., out_dtype); bias is the
+ * caller's, as in the reference).  Row strides sx, sw, so in elements; rows
+ * 16-byte aligned.  N % 16 == 0, K % 256 == 0.
+ *
+ * Reduction order: K is cut into rspx_linear_splits(N, K) equal chunks (a
+ * function of N and K only); each chunk is a fixed chain of bf16 MFMAs in
+ * increasing k; chunk results are added in chunk order and rounded once.  A
+ * row's output bits therefore do not depend on M.  With more than one chunk
+ * the fp32 chunk partials go through `workspace`
+ * (rspx_linear_workspace_bytes(M, N, K) bytes, 16-byte aligned).
+ */
+int rspx_linear_splits(int N, int K);
+int64_t rspx_linear_workspace_bytes(int M, int N, int K);
+int rspx_linear(const void* x, int64_t sx, const void* w, int64_t sw, void* out, int64_t so, int M, int N, int K,
+                int out_fp32, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- residual add + RMSNorm
+ * xo[r] = bf16(r[r] + h[r]) (PyTorch's bf16 add), y[r] = rmsnorm(xo[r], w, eps)
+ * bit for bit as rspx_rmsnorm would give on xo.  Same size rules as
+ * rspx_rmsnorm; xo may alias r.
+ */
+int rspx_add_rmsnorm(const void* r, int64_t sr, const void* h, int64_t sh, const void* w, void* xo, int64_t sxo,
+                     void* y, int64_t sy, int rows, int n, float eps, void* stream);
+
+/* ---------------------------------------------------------------- q/k/v epilogue of a decoder layer
+ * qkv: [T, (HQ + 2 HK) D] packed projection rows [q | k | v] (row stride
+ * sqkv).  q and k get RMSNorm over head_dim (wq / wk) and RoPE (cos/sin rows
+ * per token, stride scs) with the arithmetic of rspx_qk_norm_rope; q goes to
+ * qo [T, HQ, D] (contiguous); k and v are written into the KV cache of the
+ * layer: cache_k[h * skh + slots[t] * skn + d] (likewise v).  D == 128.
+ */
+int rspx_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* wq, const void* wk, const void* cos,
+                        const void* sin, int64_t scs, const int32_t* slots, void* cache_k, int64_t skh, int64_t skn,
+                        void* cache_v, int64_t svh, int64_t svn, void* qo, int T, int HQ, int HK, int D, float eps,
+                        void* stream);
+
+/* ---------------------------------------------------------------- trie mask from a parent array
+ * parent: [N] int32 (parent index, -1 for a root; parents precede children).
+ * msk: [M, NN] uint8 (row stride smm): row i < N opens slots [0, base) (the
+ * committed tokens) and base + a for every ancestor a of i and i itself;
+ * rows N..M-1 (query padding) open slot 0 only.  depth: [N] int32 out.
+ * base + N <= NN.
+ */
+int rspx_trie_mask(const int32_t* parent, int N, int base, int M, int NN, uint8_t* msk, int64_t smm, int32_t* depth,
+                   void* stream);
+
+/* ---------------------------------------------------------------- KV compaction
+ * For each of n_tensors cache tensors (device array `bases` of base
+ * addresses, each [HK][cap][D] bf16 with head stride sh and slot stride sn)
+ * and each head: rows src[0..n) are moved to rows dst0 .. dst0 + n - 1.  All
+ * sources are read before any destination is written.  n <= 128, D <= 128.
+ */
+int rspx_kv_compact(const uint64_t* bases, int n_tensors, int HK, int D, int64_t sh, int64_t sn, int cap, int dst0,
+                    const int32_t* src, int n, void* stream);
+
+/* ---------------------------------------------------------------- greedy token per row
+ * out[m] = argmax over j of logits[m][j] (fp32, row stride sl), columns
+ * [off, off + size) counted as -inf; NaN is the largest value; ties go to the
+ * lowest index.
+ */
+int rspx_argmax_rows(const float* logits, int64_t sl, int M, int V, int off, int size, int64_t* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -41,6 +41,15 @@ SIGNATURES: dict[str, tuple] = {
     "rspx_qk_norm_rope": (_i32, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _c_p,
                                  _i32, _i32, _i32, _i32, _f32, _c_p]),
     "rspx_silu_mul": (_i32, [_c_p, _i64, _c_p, _i64, _c_p, _i64, _i32, _i32, _c_p]),
+    "rspx_linear_splits": (_i32, [_i32, _i32]),
+    "rspx_linear_workspace_bytes": (_i64, [_i32, _i32, _i32]),
+    "rspx_linear": (_i32, [_c_p, _i64, _c_p, _i64, _c_p, _i64, _i32, _i32, _i32, _i32, _c_p, _i64, _c_p]),
+    "rspx_add_rmsnorm": (_i32, [_c_p, _i64, _c_p, _i64, _c_p, _c_p, _i64, _c_p, _i64, _i32, _i32, _f32, _c_p]),
+    "rspx_qkv_rope_cache": (_i32, [_c_p, _i64, _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _c_p, _i64, _i64, _c_p, _i64,
+                                   _i64, _c_p, _i32, _i32, _i32, _i32, _f32, _c_p]),
+    "rspx_trie_mask": (_i32, [_c_p, _i32, _i32, _i32, _i32, _c_p, _i64, _c_p, _c_p]),
+    "rspx_kv_compact": (_i32, [_c_p, _i32, _i32, _i32, _i64, _i64, _i32, _i32, _c_p, _i32, _c_p]),
+    "rspx_argmax_rows": (_i32, [_c_p, _i64, _i32, _i32, _i32, _i32, _c_p, _c_p]),
 }
 
 _lib = None
@@ -85,14 +94,14 @@ def stream_ptr(device: torch.device) -> int:
 _WORKSPACES: dict = {}
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-(device, stream) scratch of at least ``nbytes`` bytes, grown on demand.
+def workspace(device: torch.device, nbytes: int, tag: str = "attn") -> torch.Tensor:
+    """Per-(device, stream, tag) scratch of at least ``nbytes`` bytes, grown on demand.
 
     Keyed by stream so that calls on different streams never share it; calls on
     one stream are ordered, so reuse is safe.
     """
     stream = torch.cuda.current_stream(device)
-    key = (device.index, stream.cuda_stream)
+    key = (device.index, stream.cuda_stream, tag)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         size = max(nbytes, 256, 0 if ws is None else 2 * ws.numel())

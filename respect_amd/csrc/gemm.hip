@@ -1,0 +1,262 @@
+// Row-invariant linear layer for gfx950: C[M, N] = X[M, K] . W[N, K]^T.
+//
+// Replaces linear / _gemm of respect/kernels/gemm.py:11-41 (FixedLinear,
+// respect/kernels/patch.py:26-37): bf16 inputs, fp32 accumulation, output in
+// bf16 (the layers) or fp32 (the vocabulary projection, patch.py:23).
+//
+// Reduction order of every output element, fixed by (N, K) only:
+//   K is cut into S equal chunks (S from splits(N, K), never from M); each
+//   chunk is a chain of v_mfma_f32_16x16x32_bf16 over its 32-wide k-blocks in
+//   increasing k; the chunk results are added in chunk order,
+//   ((c0 + c1) + c2) + ..., then rounded once to the output type.
+// So a row's output bits do not depend on how many rows the call carries.
+//
+// Work split: workgroup = (64 output columns, chunk s, 64-row tile), 4 waves
+// of 16 columns each.  W -- the large operand, read exactly once -- goes
+// straight from HBM into the MFMA A operand registers (lane (n16, g4) loads
+// W[col n16][k + 8 g4, +8): 16 contiguous bytes), double-buffered in rounds
+// of 8 k-blocks.  X (at most 64 rows) is shared by the 4 waves: each round of
+// it is copied into LDS with direct-to-LDS loads laid out as MFMA B fragments
+// (one conflict-free ds_read_b128 per 16-row tile and k-block).  The output
+// tile D[n][m] comes back as 4 consecutive columns per lane.
+//
+// S > 1 writes fp32 chunk partials [S][M][N] into the caller's workspace and
+// a second kernel sums them in chunk order and rounds.
+
+#include "common.h"
+#include "respect_amd.h"
+
+namespace rspx {
+
+namespace gemm {
+
+constexpr int kCols = 64;      // output columns per workgroup (4 waves x 16)
+constexpr int kRows = 64;      // rows per workgroup (4 MFMA tiles)
+constexpr int kRoundKB = 8;    // k-blocks of 32 per round
+constexpr int kRoundK = 32 * kRoundKB;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) char lds_char_t;
+
+__device__ __forceinline__ void x_dma16(__amdgpu_buffer_rsrc_t r, int voff, lds_char_t* dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)dst, 16, voff, 0, 0, 0);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           (int)(nbytes > 0 ? nbytes : 0), 0x00020000);
+}
+
+struct Args {
+  const uint16_t* x; int64_t sx;  // [M, K]
+  const uint16_t* w; int64_t sw;  // [N, K]
+  void* out; int64_t so;          // [M, N]: bf16 or fp32 (S == 1)
+  float* part;                    // [S][M][N] fp32 (S > 1)
+  int M, N, K, S, KC, out_fp32;
+};
+
+constexpr int kOOB = 0x7ffffff0;  // a buffer offset past any descriptor: loads return 0, touch nothing
+
+__device__ __forceinline__ void vm_wait16() {
+  __builtin_amdgcn_s_waitcnt((16 & 15) | ((16 >> 4) << 14) | 0x70 | 0xF00);  // vmcnt(16)
+}
+__device__ __forceinline__ void vm_wait0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+__device__ __forceinline__ void raw_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// acc[t] += W . X^T over one round: X B-fragments of row tile t, k-block kb
+// from LDS buffer xb, W A-fragments from registers wf.
+template <int MT>
+__device__ __forceinline__ void round_compute(const lds_char_t* xb, const u32x4 (&wf)[kRoundKB], f32x4 (&acc)[4],
+                                              int lane) {
+#pragma unroll
+  for (int kb = 0; kb < kRoundKB; ++kb) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const u32x4 xf = *(const __attribute__((address_space(3))) u32x4*)(xb + (kb * 4 + t) * 1024 + 16 * lane);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wf[kb]),
+                                                       __builtin_bit_cast(bf16x8, xf), acc[t], 0, 0, 0);
+    }
+  }
+}
+
+// Every wave issues, per round and in this order, 8 X chunks into LDS (row
+// tile t = w, k-blocks 0..7: rows 16 t + n16, k [8 g4, +8) of the block) and
+// 8 W loads into registers.  Rounds past the chunk (the last prefetch) and
+// rows past M use out-of-range offsets: zeros, no memory traffic.  Issuing
+// the same number of loads on every path keeps the waits exact.
+__device__ __forceinline__ void issue_round(__amdgpu_buffer_rsrc_t rx, int xoff, __amdgpu_buffer_rsrc_t rw, int woff,
+                                            int rr, int nr, lds_char_t* xb, int w, u32x4 (&wf)[kRoundKB]) {
+  const bool live = rr < nr;
+#pragma unroll
+  for (int kb = 0; kb < kRoundKB; ++kb)
+    x_dma16(rx, live ? xoff + 2 * (rr * kRoundK + 32 * kb) : kOOB, xb + (kb * 4 + w) * 1024);
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int kb = 0; kb < kRoundKB; ++kb)
+    wf[kb] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rw, live ? woff + 2 * (rr * kRoundK + 32 * kb) : kOOB, 0, 0));
+  asm volatile("" ::: "memory");
+}
+
+template <int MT>
+__global__ __launch_bounds__(256) void gemm_kernel(Args A) {
+  __shared__ __attribute__((aligned(16))) char xs[2][kRoundKB * 4 * 1024];  // 2 x 32 KB
+  constexpr int XB = kRoundKB * 4 * 1024;
+  const int lane = __lane_id();
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n16 = lane & 15, g4 = lane >> 4;
+  const int NT = (A.N + kCols - 1) / kCols;
+  const int nt = blockIdx.x % NT;
+  const int rest = blockIdx.x / NT;
+  const int s = rest % A.S;
+  const int mt = rest / A.S;
+  const int col = nt * kCols + 16 * w;        // this wave's first column
+  const int row0 = mt * kRows;
+  const int k0 = s * A.KC;
+  const int nr = A.KC / kRoundK;
+  const bool has_cols = col < A.N;            // N % 16 == 0: whole tiles only
+
+  // X: rows [row0, M) from column k0.  W: this wave's 16 rows, columns
+  // [k0, k0 + KC) (no bytes at all for a wave past N).
+  const int mrows = min(kRows, A.M - row0);
+  const __amdgpu_buffer_rsrc_t rx =
+      rsrc(A.x + (int64_t)row0 * A.sx + k0, 2 * ((int64_t)(mrows - 1) * A.sx + (A.K - k0)));
+  const int xoff = 2 * ((16 * w + n16) * (int)A.sx + 8 * g4);
+  const __amdgpu_buffer_rsrc_t rw =
+      rsrc(A.w + (int64_t)(has_cols ? col : 0) * A.sw + k0, has_cols ? 2 * (15 * A.sw + A.KC) : 0);
+  const int woff = 2 * (n16 * (int)A.sw + 8 * g4);
+
+  lds_char_t* xl = (lds_char_t*)xs[0];
+  f32x4 acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  u32x4 wa[kRoundKB], wb[kRoundKB];
+  issue_round(rx, xoff, rw, woff, 0, nr, xl, w, wa);
+  for (int r = 0; r < nr; r += 2) {
+    // round r: X in buffer 0, W in wa; prefetch round r + 1 into buffer 1 / wb
+    issue_round(rx, xoff, rw, woff, r + 1, nr, xl + XB, w, wb);
+    vm_wait16();
+    raw_barrier();
+    round_compute<MT>(xl, wa, acc, lane);
+    raw_barrier();  // buffer 0 is free
+    if (r + 1 >= nr) break;
+    // round r + 1: X in buffer 1, W in wb; prefetch round r + 2 into buffer 0 / wa
+    issue_round(rx, xoff, rw, woff, r + 2, nr, xl, w, wa);
+    vm_wait16();
+    raw_barrier();
+    round_compute<MT>(xl + XB, wb, acc, lane);
+    raw_barrier();  // buffer 1 is free
+  }
+  vm_wait0();
+  if (!has_cols) return;
+
+  // D[n][m]: lane (n16, g4) holds columns col + 4 g4 + e of row 16 t + n16.
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int m = row0 + 16 * t + n16;
+    if (m >= A.M) continue;
+    const int n = col + 4 * g4;
+    if (A.S > 1) {
+      *reinterpret_cast<f32x4*>(A.part + ((size_t)s * A.M + m) * A.N + n) = acc[t];
+    } else if (A.out_fp32) {
+      *reinterpret_cast<f32x4*>(static_cast<float*>(A.out) + (int64_t)m * A.so + n) = acc[t];
+    } else {
+      u32x2 o;
+      o[0] = pack_bf16x2(acc[t][0], acc[t][1]);
+      o[1] = pack_bf16x2(acc[t][2], acc[t][3]);
+      *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(A.out) + (int64_t)m * A.so + n) = o;
+    }
+  }
+}
+
+// out[m][n] = round(((p0 + p1) + p2) + ...), 4 columns per thread.
+__global__ __launch_bounds__(256) void reduce_kernel(const float* part, int S, int M, int N, void* out, int64_t so,
+                                                     int out_fp32) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= (int64_t)M * N) return;
+  const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
+  f32x4 v = *reinterpret_cast<const f32x4*>(part + i);
+  for (int s = 1; s < S; ++s) {
+    const f32x4 p = *reinterpret_cast<const f32x4*>(part + (size_t)s * M * N + i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = v[e] + p[e];
+  }
+  if (out_fp32) {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(out) + (int64_t)m * so + n) = v;
+  } else {
+    u32x2 o;
+    o[0] = pack_bf16x2(v[0], v[1]);
+    o[1] = pack_bf16x2(v[2], v[3]);
+    *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(out) + (int64_t)m * so + n) = o;
+  }
+}
+
+}  // namespace gemm
+
+// Chunk count of the K reduction: a function of (N, K) only.  More chunks
+// until the grid has >= 256 workgroups per 64-row tile, at most 8, each chunk
+// a whole number of 256-wide rounds.
+static int linear_splits(int N, int K) {
+  const int nt = (N + gemm::kCols - 1) / gemm::kCols;
+  int S = 1;
+  while (nt * S < 256 && S < 8 && K % (gemm::kRoundK * 2 * S) == 0) S *= 2;
+  return S;
+}
+
+}  // namespace rspx
+
+using namespace rspx;
+
+extern "C" int rspx_linear_splits(int N, int K) {
+  if (N <= 0 || K <= 0 || K % gemm::kRoundK != 0) return -1;
+  return linear_splits(N, K);
+}
+
+extern "C" int64_t rspx_linear_workspace_bytes(int M, int N, int K) {
+  if (M < 0 || N <= 0 || K <= 0 || K % gemm::kRoundK != 0) return -1;
+  const int S = linear_splits(N, K);
+  return S > 1 ? (int64_t)S * M * N * (int64_t)sizeof(float) : 0;
+}
+
+extern "C" int rspx_linear(const void* x, int64_t sx, const void* w, int64_t sw, void* out, int64_t so, int M, int N,
+                           int K, int out_fp32, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (M < 0 || N <= 0 || K <= 0) return RSPX_EINVAL;
+  if (N % 16 != 0 || K % gemm::kRoundK != 0) return RSPX_EUNSUPPORTED;
+  if (M == 0) return RSPX_OK;
+  if (!x || !w || !out) return RSPX_EINVAL;
+  if (sx < K || sw < K || so < N) return RSPX_EINVAL;
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  if (!al(x) || !al(w) || !al(out) || sx % 8 || sw % 8 || so % 4) return RSPX_EALIGN;
+  if ((int64_t)64 * sx * 2 >= (1ll << 31) || (int64_t)16 * sw * 2 >= (1ll << 31)) return RSPX_EUNSUPPORTED;
+  const int S = linear_splits(N, K);
+  const int64_t need = S > 1 ? (int64_t)S * M * N * (int64_t)sizeof(float) : 0;
+  if (need > 0 && (!workspace || workspace_bytes < need || !al(workspace))) return RSPX_EWORKSPACE;
+
+  gemm::Args a;
+  a.x = static_cast<const uint16_t*>(x); a.sx = sx;
+  a.w = static_cast<const uint16_t*>(w); a.sw = sw;
+  a.out = out; a.so = so;
+  a.part = static_cast<float*>(workspace);
+  a.M = M; a.N = N; a.K = K; a.S = S; a.KC = K / S; a.out_fp32 = out_fp32 ? 1 : 0;
+  const int NT = (N + gemm::kCols - 1) / gemm::kCols;
+  const int MTILES = (M + gemm::kRows - 1) / gemm::kRows;
+  const int64_t grid = (int64_t)NT * S * MTILES;
+  if (grid > 0x7fffffff) return RSPX_EUNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int mt = M >= 64 ? 4 : (M + 15) / 16;  // row tiles of the (only or first) 64-row tile
+  if (MTILES > 1 || mt == 4) hipLaunchKernelGGL(gemm::gemm_kernel<4>, dim3((unsigned)grid), dim3(256), 0, s, a);
+  else if (mt == 3) hipLaunchKernelGGL(gemm::gemm_kernel<3>, dim3((unsigned)grid), dim3(256), 0, s, a);
+  else if (mt == 2) hipLaunchKernelGGL(gemm::gemm_kernel<2>, dim3((unsigned)grid), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(gemm::gemm_kernel<1>, dim3((unsigned)grid), dim3(256), 0, s, a);
+  if (S > 1) {
+    const int64_t quads = (int64_t)M * N / 4;
+    hipLaunchKernelGGL(gemm::reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s,
+                       static_cast<const float*>(workspace), S, M, N, out, so, a.out_fp32);
+  }
+  return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
+}

@@ -64,18 +64,33 @@ __device__ __forceinline__ u32x4 pack8(const float* f) {
 // 1 / sqrt(v): correctly rounded square root, then a correctly rounded divide.
 __device__ __forceinline__ float rsqrt_rn(float v) { return 1.0f / __builtin_sqrtf(v); }
 
-// Normalise one 8-element vector per iteration for a row held by TPR lanes
-// (TPR <= 64, all in one wave), VPL vectors per lane.  Returns nothing; writes y.
-template <int TPR, int VPL>
-__device__ __forceinline__ void rms_row_wave(const uint16_t* x, const uint16_t* w, uint16_t* y, int sub,
-                                             int n, float eps) {
+// Load one 8-element vector of the row: x, or with ADD the residual sum
+// bf16(r + h) (one fp32 add rounded once, as PyTorch's bf16 add), which is
+// then also stored to xo.
+template <bool ADD>
+__device__ __forceinline__ void load_row_vec(const uint16_t* x, const uint16_t* h, uint16_t* xo, int c, float* v) {
+  unpack8(*reinterpret_cast<const u32x4*>(x + c), v);
+  if constexpr (ADD) {
+    float hv[8];
+    unpack8(*reinterpret_cast<const u32x4*>(h + c), hv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = round_bf16(v[i] + hv[i]);
+    *reinterpret_cast<u32x4*>(xo + c) = pack8(v);
+  }
+}
+
+// Normalise a row held by TPR lanes (TPR <= 64, all in one wave), VPL
+// 8-element vectors per lane.
+template <int TPR, int VPL, bool ADD>
+__device__ __forceinline__ void rms_row_wave(const uint16_t* x, const uint16_t* h, uint16_t* xo, const uint16_t* w,
+                                             uint16_t* y, int sub, int n, float eps) {
   float xv[VPL][8];
   float ss = 0.f;
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
     const int c = (v * TPR + sub) * 8;
     if (c < n) {
-      unpack8(*reinterpret_cast<const u32x4*>(x + c), xv[v]);
+      load_row_vec<ADD>(x, h, xo, c, xv[v]);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) xv[v][i] = 0.f;
@@ -101,32 +116,36 @@ __device__ __forceinline__ void rms_row_wave(const uint16_t* x, const uint16_t* 
 }  // namespace
 
 // Rows of up to 64*8*VPL elements: one row per TPR lanes of a wave.
-template <int TPR, int VPL>
-__global__ __launch_bounds__(256) void rmsnorm_small_kernel(const uint16_t* x, int64_t sx, const uint16_t* w,
+template <int TPR, int VPL, bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_small_kernel(const uint16_t* x, int64_t sx, const uint16_t* h,
+                                                            int64_t sh, uint16_t* xo, int64_t sxo, const uint16_t* w,
                                                             uint16_t* y, int64_t sy, int rows, int n, float eps) {
   const int lane = __lane_id();
   const int row = (blockIdx.x * 256 + threadIdx.x) / TPR;
   const int sub = lane % TPR;
   if (row >= rows) return;   // whole lane groups leave together (TPR divides 64)
-  rms_row_wave<TPR, VPL>(x + row * sx, w, y + row * sy, sub, n, eps);
+  rms_row_wave<TPR, VPL, ADD>(x + row * sx, h + row * sh, xo + row * sxo, w, y + row * sy, sub, n, eps);
 }
 
 // Long rows: one 256-thread workgroup per row, VPL 8-element vectors per
 // thread.  Wave sums are combined in wave order through LDS.
-template <int VPL>
-__global__ __launch_bounds__(256) void rmsnorm_row_kernel(const uint16_t* x, int64_t sx, const uint16_t* w,
+template <int VPL, bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_row_kernel(const uint16_t* x, int64_t sx, const uint16_t* h,
+                                                          int64_t sh, uint16_t* xo, int64_t sxo, const uint16_t* w,
                                                           uint16_t* y, int64_t sy, int n, float eps) {
   __shared__ float part[4];
   const int row = blockIdx.x;
   const int t = threadIdx.x, lane = __lane_id(), wv = t >> 6;
   const uint16_t* xr = x + row * sx;
+  const uint16_t* hr = h + row * sh;
+  uint16_t* xor_ = xo + row * sxo;
   float xv[VPL][8];
   float ss = 0.f;
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
     const int c = (v * 256 + t) * 8;
     if (c < n) {
-      unpack8(*reinterpret_cast<const u32x4*>(xr + c), xv[v]);
+      load_row_vec<ADD>(xr, hr, xor_, c, xv[v]);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) xv[v][i] = 0.f;
@@ -151,7 +170,6 @@ __global__ __launch_bounds__(256) void rmsnorm_row_kernel(const uint16_t* x, int
       *reinterpret_cast<u32x4*>(yr + c) = pack8(o);
     }
   }
-  (void)lane;
 }
 
 namespace {
@@ -237,11 +255,81 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* q, in
   *reinterpret_cast<u32x4*>(dst + sub * 8) = pack8(o);
 }
 
+// One decoder layer's q/k/v epilogue for T tokens, one launch: from the packed
+// projection row qkv[t] = [q (HQ D) | k (HK D) | v (HK D)], q and k get the
+// q_norm / k_norm RMSNorm and RoPE (the arithmetic of qk_norm_rope_kernel);
+// q goes to qo [T, HQ, D], k and v are written straight into the KV cache at
+// the token's physical slot: cache[h][slot[t]][:] (head stride sh, slot
+// stride sn).
+__global__ __launch_bounds__(256) void qkv_rope_cache_kernel(const uint16_t* qkv, int64_t sqkv, const uint16_t* wq,
+                                                             const uint16_t* wk, const uint16_t* cosb,
+                                                             const uint16_t* sinb, int64_t scs, const int* slots,
+                                                             uint16_t* ck, int64_t skh, int64_t skn, uint16_t* cv,
+                                                             int64_t svh, int64_t svn, uint16_t* qo, int T, int HQ,
+                                                             int HK, float eps) {
+  constexpr int D = 128;
+  const int gid = blockIdx.x * 256 + threadIdx.x;
+  const int rowid = gid >> 4;
+  const int sub = gid & 15;
+  const int nq = T * HQ, nk = T * HK;
+  if (rowid >= nq + 2 * nk) return;
+  int kind, t, hh;
+  if (rowid < nq) { kind = 0; t = rowid / HQ; hh = rowid - t * HQ; }
+  else if (rowid < nq + nk) { kind = 1; t = (rowid - nq) / HK; hh = rowid - nq - t * HK; }
+  else { kind = 2; t = (rowid - nq - nk) / HK; hh = rowid - nq - nk - t * HK; }
+  const uint16_t* row = qkv + (int64_t)t * sqkv + (kind == 0 ? hh * D : kind == 1 ? (HQ + hh) * D : (HQ + HK + hh) * D);
+  const u32x4 raw = *reinterpret_cast<const u32x4*>(row + sub * 8);
+  if (kind == 2) {
+    *reinterpret_cast<u32x4*>(cv + hh * svh + (int64_t)slots[t] * svn + sub * 8) = raw;
+    return;
+  }
+  float xv[8];
+  unpack8(raw, xv);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(xv[i], xv[i], ss);
+  ss = lane_group_sum<16>(ss);
+  const float rr = rsqrt_rn(ss / (float)D + eps);
+  float wv[8], nv[8], cs[8], sn[8], o[8];
+  unpack8(*reinterpret_cast<const u32x4*>((kind == 0 ? wq : wk) + sub * 8), wv);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) nv[i] = round_bf16(wv[i] * round_bf16(xv[i] * rr));
+  unpack8(*reinterpret_cast<const u32x4*>(cosb + (int64_t)t * scs + sub * 8), cs);
+  unpack8(*reinterpret_cast<const u32x4*>(sinb + (int64_t)t * scs + sub * 8), sn);
+  rope_vec(nv, cs, sn, sub, o);
+  uint16_t* dst = kind == 0 ? qo + ((int64_t)t * HQ + hh) * D : ck + hh * skh + (int64_t)slots[t] * skn;
+  *reinterpret_cast<u32x4*>(dst + sub * 8) = pack8(o);
+}
+
 }  // namespace rspx
 
 using namespace rspx;
 
 static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+namespace rspx {
+// The split depends on n only (never on rows), for plain and residual-add rows.
+template <bool ADD>
+static void launch_rmsnorm(const uint16_t* X, int64_t sx, const uint16_t* Hp, int64_t sh, uint16_t* XO, int64_t sxo,
+                           const uint16_t* W, uint16_t* Y, int64_t sy, int rows, int n, float eps, hipStream_t s) {
+  const int vec = n / 8;
+  if (vec <= 16) {
+    hipLaunchKernelGGL((rmsnorm_small_kernel<16, 1, ADD>), dim3((rows * 16 + 255) / 256), dim3(256), 0, s, X, sx, Hp,
+                       sh, XO, sxo, W, Y, sy, rows, n, eps);
+  } else if (vec <= 64) {
+    hipLaunchKernelGGL((rmsnorm_small_kernel<64, 1, ADD>), dim3((rows * 64 + 255) / 256), dim3(256), 0, s, X, sx, Hp,
+                       sh, XO, sxo, W, Y, sy, rows, n, eps);
+  } else if (vec <= 256) {
+    hipLaunchKernelGGL((rmsnorm_row_kernel<1, ADD>), dim3(rows), dim3(256), 0, s, X, sx, Hp, sh, XO, sxo, W, Y, sy, n, eps);
+  } else if (vec <= 512) {
+    hipLaunchKernelGGL((rmsnorm_row_kernel<2, ADD>), dim3(rows), dim3(256), 0, s, X, sx, Hp, sh, XO, sxo, W, Y, sy, n, eps);
+  } else if (vec <= 1024) {
+    hipLaunchKernelGGL((rmsnorm_row_kernel<4, ADD>), dim3(rows), dim3(256), 0, s, X, sx, Hp, sh, XO, sxo, W, Y, sy, n, eps);
+  } else {
+    hipLaunchKernelGGL((rmsnorm_row_kernel<8, ADD>), dim3(rows), dim3(256), 0, s, X, sx, Hp, sh, XO, sxo, W, Y, sy, n, eps);
+  }
+}
+}  // namespace rspx
 
 extern "C" int rspx_rmsnorm(const void* x, int64_t sx, const void* w, void* y, int64_t sy, int rows, int n,
                             float eps, void* stream) {
@@ -249,25 +337,22 @@ extern "C" int rspx_rmsnorm(const void* x, int64_t sx, const void* w, void* y, i
   if (rows == 0) return RSPX_OK;
   if (!x || !w || !y) return RSPX_EINVAL;
   if (!al16(x) || !al16(w) || !al16(y) || sx % 8 || sy % 8) return RSPX_EALIGN;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   auto X = static_cast<const uint16_t*>(x);
-  auto W = static_cast<const uint16_t*>(w);
-  auto Y = static_cast<uint16_t*>(y);
-  const int vec = n / 8;
-  // The split depends on n only.
-  if (vec <= 16) {
-    hipLaunchKernelGGL((rmsnorm_small_kernel<16, 1>), dim3((rows * 16 + 255) / 256), dim3(256), 0, s, X, sx, W, Y, sy, rows, n, eps);
-  } else if (vec <= 64) {
-    hipLaunchKernelGGL((rmsnorm_small_kernel<64, 1>), dim3((rows * 64 + 255) / 256), dim3(256), 0, s, X, sx, W, Y, sy, rows, n, eps);
-  } else if (vec <= 256) {
-    hipLaunchKernelGGL((rmsnorm_row_kernel<1>), dim3(rows), dim3(256), 0, s, X, sx, W, Y, sy, n, eps);
-  } else if (vec <= 512) {
-    hipLaunchKernelGGL((rmsnorm_row_kernel<2>), dim3(rows), dim3(256), 0, s, X, sx, W, Y, sy, n, eps);
-  } else if (vec <= 1024) {
-    hipLaunchKernelGGL((rmsnorm_row_kernel<4>), dim3(rows), dim3(256), 0, s, X, sx, W, Y, sy, n, eps);
-  } else {
-    hipLaunchKernelGGL((rmsnorm_row_kernel<8>), dim3(rows), dim3(256), 0, s, X, sx, W, Y, sy, n, eps);
-  }
+  launch_rmsnorm<false>(X, sx, X, sx, nullptr, 0, static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy,
+                        rows, n, eps, static_cast<hipStream_t>(stream));
+  return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
+}
+
+extern "C" int rspx_add_rmsnorm(const void* r, int64_t sr, const void* h, int64_t sh, const void* w, void* xo,
+                                int64_t sxo, void* y, int64_t sy, int rows, int n, float eps, void* stream) {
+  if (rows < 0 || n <= 0 || n % 8 != 0 || n > 16384) return n % 8 ? RSPX_EUNSUPPORTED : RSPX_EINVAL;
+  if (rows == 0) return RSPX_OK;
+  if (!r || !h || !w || !xo || !y) return RSPX_EINVAL;
+  if (!al16(r) || !al16(h) || !al16(w) || !al16(xo) || !al16(y) || sr % 8 || sh % 8 || sxo % 8 || sy % 8)
+    return RSPX_EALIGN;
+  launch_rmsnorm<true>(static_cast<const uint16_t*>(r), sr, static_cast<const uint16_t*>(h), sh,
+                       static_cast<uint16_t*>(xo), sxo, static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy,
+                       rows, n, eps, static_cast<hipStream_t>(stream));
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }
 
@@ -308,5 +393,28 @@ extern "C" int rspx_qk_norm_rope(const void* q, int64_t sqt, int64_t sqh, const 
                      static_cast<const uint16_t*>(wk), static_cast<const uint16_t*>(cosb),
                      static_cast<const uint16_t*>(sinb), scs, static_cast<uint16_t*>(qo),
                      static_cast<uint16_t*>(ko), T, HQ, HK, eps);
+  return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
+}
+
+extern "C" int rspx_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* wq, const void* wk, const void* cosb,
+                                   const void* sinb, int64_t scs, const int32_t* slots, void* cache_k, int64_t skh,
+                                   int64_t skn, void* cache_v, int64_t svh, int64_t svn, void* qo, int T, int HQ,
+                                   int HK, int D, float eps, void* stream) {
+  if (T < 0 || HQ <= 0 || HK <= 0) return RSPX_EINVAL;
+  if (D != 128) return RSPX_EUNSUPPORTED;
+  if (T == 0) return RSPX_OK;
+  if (!qkv || !wq || !wk || !cosb || !sinb || !slots || !cache_k || !cache_v || !qo) return RSPX_EINVAL;
+  const void* ps[] = {qkv, wq, wk, cosb, sinb, cache_k, cache_v, qo};
+  for (const void* p : ps)
+    if (!al16(p)) return RSPX_EALIGN;
+  if (sqkv % 8 || scs % 8 || skh % 8 || skn % 8 || svh % 8 || svn % 8) return RSPX_EALIGN;
+  if (sqkv < (int64_t)(HQ + 2 * HK) * D) return RSPX_EINVAL;
+  const int64_t threads = (int64_t)T * (HQ + 2 * HK) * 16;
+  hipLaunchKernelGGL(qkv_rope_cache_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(qkv), sqkv,
+                     static_cast<const uint16_t*>(wq), static_cast<const uint16_t*>(wk),
+                     static_cast<const uint16_t*>(cosb), static_cast<const uint16_t*>(sinb), scs, slots,
+                     static_cast<uint16_t*>(cache_k), skh, skn, static_cast<uint16_t*>(cache_v), svh, svn,
+                     static_cast<uint16_t*>(qo), T, HQ, HK, eps);
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }

@@ -1,0 +1,45 @@
+"""Greedy token choice and the acceptance walk (respect/decoding/acceptance.py:11-46).
+
+``greedy_token`` runs on the GPU (rspx_argmax_rows): the index of the largest
+fp32 logit with the excluded vocabulary range counted as -inf, ties to the
+lowest index -- the same choice as ``mask_action_vocab(...).argmax(-1)``.
+``walk`` is host code: it follows the trie while the target's choice matches.
+"""
+from __future__ import annotations
+
+from typing import Callable
+
+import torch
+
+from .. import _lib
+from ..candidates.trie import Trie
+
+
+def greedy_token(logits: torch.Tensor, offset: int = 0, size: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """logits [M, V] fp32 on the GPU -> int64 [M]."""
+    if logits.dtype != torch.float32 or not logits.is_cuda or logits.dim() != 2 or logits.stride(1) != 1:
+        raise TypeError("greedy_token: fp32 [M, V] GPU logits with contiguous rows are required")
+    M, V = logits.shape
+    if out is None:
+        out = torch.empty(M, dtype=torch.int64, device=logits.device)
+    rc = _lib.lib().rspx_argmax_rows(logits.data_ptr(), logits.stride(0), M, V, int(offset), int(size),
+                                     out.data_ptr(), _lib.stream_ptr(logits.device))
+    _lib.check("rspx_argmax_rows", rc)
+    return out
+
+
+def walk(tree: Trie, first: int, cap: int, eos: int,
+         pick: Callable[[list[int], int], int]) -> tuple[list[int], list[int], int]:
+    """Follow the trie from ``first`` while candidates match the target's choice
+    (acceptance.py:26-46).  Returns (node path, accepted tokens, correction token)."""
+    path, acc = [], []
+    ch, rec = tree.roots.get(first), first
+    while ch is not None and len(acc) < cap:
+        nd = tree.nodes[ch]
+        path.append(ch)
+        acc.append(nd.token)
+        if nd.token == eos:
+            break
+        rec = pick(acc, ch)
+        ch = nd.children.get(rec)
+    return path, acc, rec

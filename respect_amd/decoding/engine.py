@@ -1,0 +1,162 @@
+"""Decoder forward of the verification step, on the C-ABI kernels only.
+
+A Qwen3-style dense GQA decoder (the text model the reference verifies with:
+pre-norm layers, q_norm / k_norm, RoPE, SwiGLU MLP, untied vocabulary head)
+with random-initialised weights -- there is no network to fetch checkpoints.
+Every arithmetic step goes through librespect_amd:
+
+    x = embed[ids]                                   (row gather)
+    y = rmsnorm(x)                                   rspx_rmsnorm
+    per layer:
+      qkv = y . Wqkv^T                               rspx_linear
+      q, cache[k, v] at the tokens' slots            rspx_qkv_rope_cache
+      a = attention(q; prompt K/V, node K/V, mask)   rspx_trie_attn
+      h = a . Wo^T                                   rspx_linear
+      x, y = x + h, rmsnorm(x + h)                   rspx_add_rmsnorm
+      g|u = y . Wgu^T ; m = silu(g) * u              rspx_linear, rspx_silu_mul
+      h = m . Wd^T ; x, y = x + h, rmsnorm(x + h)    rspx_linear, rspx_add_rmsnorm
+    logits = y . Wlm^T (fp32)                        rspx_linear
+
+Each kernel computes a row with arithmetic that does not depend on how many
+rows the call carries, and attention folds a row's node slots in slot order,
+so a token verified inside a trie gets the same logits and KV bits as when it
+is decoded alone -- the property the reference's verification relies on
+(respect/decoding/verify.py:12-46, respect/decoding/sequential.py:17-42).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from .. import _lib
+from ..kernels.attention import trie_attn
+from ..kernels.gemm import linear
+from ..system.fused import rope_tables
+
+
+@dataclass(frozen=True)
+class DecoderConfig:
+    layers: int = 36
+    hidden: int = 4096
+    heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    ffn: int = 12288
+    vocab: int = 151936
+    eps: float = 1e-6
+    theta: float = 1.0e6
+
+    @property
+    def qkv_rows(self) -> int:
+        return (self.heads + 2 * self.kv_heads) * self.head_dim
+
+    def weight_bytes(self) -> int:
+        """bf16 bytes of every weight one forward reads (embedding rows aside)."""
+        H, F, V = self.hidden, self.ffn, self.vocab
+        per_layer = self.qkv_rows * H + H * self.heads * self.head_dim + 2 * F * H + H * F + 2 * H + 2 * self.head_dim
+        return 2 * (self.layers * per_layer + V * H + H)
+
+
+class Layer:
+    def __init__(self, cfg: DecoderConfig, g: torch.Generator, device, std: float):
+        H, D, F = cfg.hidden, cfg.head_dim, cfg.ffn
+
+        def w(*shape):
+            return (torch.randn(*shape, generator=g, device=device) * std).to(torch.bfloat16)
+
+        def norm_w(n):
+            return (1.0 + torch.randn(n, generator=g, device=device) * std).to(torch.bfloat16)
+
+        self.in_norm = norm_w(H)
+        self.wqkv = w(cfg.qkv_rows, H)              # [q | k | v] rows
+        self.q_norm = norm_w(D)
+        self.k_norm = norm_w(D)
+        self.wo = w(H, cfg.heads * D)
+        self.post_norm = norm_w(H)
+        self.wgu = w(2 * F, H)                      # [gate | up] rows
+        self.wd = w(H, F)
+
+
+class Decoder:
+    """Random-initialised decoder; weights ~ N(0, std), norm weights 1 + N(0, std)."""
+
+    def __init__(self, cfg: DecoderConfig = DecoderConfig(), device="cuda", seed: int = 0, std: float = 0.02):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        g = torch.Generator(device=self.device)
+        g.manual_seed(seed)
+        self.embed = (torch.randn(cfg.vocab, cfg.hidden, generator=g, device=self.device) * std).to(torch.bfloat16)
+        self.layers = [Layer(cfg, g, self.device, std) for _ in range(cfg.layers)]
+        self.final_norm = (1.0 + torch.randn(cfg.hidden, generator=g, device=self.device) * std).to(torch.bfloat16)
+        self.lm_head = (torch.randn(cfg.vocab, cfg.hidden, generator=g, device=self.device) * std).to(torch.bfloat16)
+        self.sm_scale = cfg.head_dim ** -0.5
+
+    # ------------------------------------------------------------------ forward
+    @torch.no_grad()
+    def forward(self, ids: torch.Tensor, slots: torch.Tensor, positions: torch.Tensor, cache, P: int,
+                msk: torch.Tensor, NN: int) -> torch.Tensor:
+        """Run ``T = len(ids)`` tokens through every layer.
+
+        ids [T] int64, slots [T] int32 (cache slot written by each token),
+        positions [T] (rotary positions), cache: KVCache whose slots [0, P) are
+        the prompt segment and [P, P + NN) the node segment; msk [T, NN] uint8
+        (row t may attend to node slot j).  Returns fp32 logits [T, V].
+        """
+        cfg = self.cfg
+        L = _lib.lib()
+        dev = self.device
+        s = _lib.stream_ptr(dev)
+        T = int(ids.shape[0])
+        Hd, HQ, HK, D = cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim
+        bf = torch.bfloat16
+        x = self.embed.index_select(0, ids)                       # residual stream [T, H]
+        y = torch.empty_like(x)
+        _lib.check("rspx_rmsnorm", L.rspx_rmsnorm(x.data_ptr(), Hd, self.layers[0].in_norm.data_ptr(), y.data_ptr(),
+                                                  Hd, T, Hd, cfg.eps, s))
+        cos, sin = rope_tables(positions, D, cfg.theta, device=dev)
+        slots32 = slots.to(torch.int32)
+        qo = torch.empty((T, HQ, D), dtype=bf, device=dev)
+        att = torch.empty((T, HQ, D), dtype=bf, device=dev)
+        mlp = torch.empty((T, cfg.ffn), dtype=bf, device=dev)
+        for li, lay in enumerate(self.layers):
+            ck, cv = cache.k[li], cache.v[li]
+            qkv = linear(y, lay.wqkv)
+            _lib.check("rspx_qkv_rope_cache", L.rspx_qkv_rope_cache(
+                qkv.data_ptr(), qkv.stride(0), lay.q_norm.data_ptr(), lay.k_norm.data_ptr(), cos.data_ptr(),
+                sin.data_ptr(), cos.stride(0), slots32.data_ptr(), ck.data_ptr(), ck.stride(0), ck.stride(1),
+                cv.data_ptr(), cv.stride(0), cv.stride(1), qo.data_ptr(), T, HQ, HK, D, cfg.eps, s))
+            trie_attn(qo.permute(1, 0, 2), ck[:, :P], cv[:, :P], ck[:, P:P + NN], cv[:, P:P + NN], msk,
+                      self.sm_scale, out=att.permute(1, 0, 2))
+            h = linear(att.view(T, HQ * D), lay.wo)
+            _lib.check("rspx_add_rmsnorm", L.rspx_add_rmsnorm(
+                x.data_ptr(), Hd, h.data_ptr(), Hd, lay.post_norm.data_ptr(), x.data_ptr(), Hd, y.data_ptr(), Hd,
+                T, Hd, cfg.eps, s))
+            gu = linear(y, lay.wgu)
+            F = cfg.ffn
+            _lib.check("rspx_silu_mul", L.rspx_silu_mul(gu.data_ptr(), gu.stride(0), gu.data_ptr() + 2 * F,
+                                                        gu.stride(0), mlp.data_ptr(), F, T, F, s))
+            h = linear(mlp, lay.wd)
+            nxt = self.layers[li + 1].in_norm if li + 1 < len(self.layers) else self.final_norm
+            _lib.check("rspx_add_rmsnorm", L.rspx_add_rmsnorm(
+                x.data_ptr(), Hd, h.data_ptr(), Hd, nxt.data_ptr(), x.data_ptr(), Hd, y.data_ptr(), Hd,
+                T, Hd, cfg.eps, s))
+        return linear(y, self.lm_head, out_dtype=torch.float32)
+
+    # ------------------------------------------------------------------ prompt
+    @torch.no_grad()
+    def prefill(self, ids: torch.Tensor, cache, chunk: int = 512) -> torch.Tensor:
+        """Fill cache slots [0, len(ids)) with the prompt's KV, ``chunk`` tokens per
+        forward: a chunk sees the earlier chunks as its prompt segment and
+        itself causally as its node segment.  Returns the last row's logits."""
+        n = int(ids.shape[0])
+        dev = self.device
+        logits = None
+        for c0 in range(0, n, chunk):
+            c1 = min(n, c0 + chunk)
+            T = c1 - c0
+            NN = -(-T // 32) * 32
+            msk = torch.tril(torch.ones(T, NN, dtype=torch.uint8, device=dev))
+            pos = torch.arange(c0, c1, device=dev)
+            logits = self.forward(ids[c0:c1], pos.to(torch.int32), pos, cache, c0, msk, NN)
+        return logits[-1:]

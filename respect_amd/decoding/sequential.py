@@ -1,0 +1,36 @@
+"""Token-by-token greedy decoding (respect/decoding/sequential.py:17-42): the
+reference a verification step must reproduce bit for bit."""
+from __future__ import annotations
+
+import torch
+
+from .acceptance import greedy_token
+from .verify import node_slots
+
+
+@torch.no_grad()
+def forward_token(model, cache, token: int, P: int, c: int) -> torch.Tensor:
+    """Feed ``token`` at node-segment index ``c`` (cache slot P + c, position
+    P + c); it sees the prompt and node slots [0, c].  Returns fp32 logits [1, V]."""
+    dev = model.device
+    NN = node_slots(c, 1)
+    msk = (torch.arange(NN, device=dev) <= c).to(torch.uint8)[None]
+    slot = torch.tensor([P + c], dtype=torch.int32, device=dev)
+    return model.forward(torch.tensor([token], device=dev), slot, slot.to(torch.int64), cache, P, msk, NN)
+
+
+@torch.no_grad()
+def sequential(model, cache, token: int, P: int, base: int, eos: int, offset: int, size: int,
+               max_tokens: int) -> list[int]:
+    """Generate from ``token`` (already chosen) until EOS or ``max_tokens``, one
+    forward per token; ``base`` committed tokens precede it.  Returns the fed
+    tokens, ``token`` first."""
+    out, c = [], base
+    while len(out) < max_tokens:
+        out.append(token)
+        logits = forward_token(model, cache, token, P, c)
+        c += 1
+        if token == eos:
+            break
+        token = int(greedy_token(logits, offset, size).item())
+    return out

@@ -1,0 +1,46 @@
+"""One forward pass that verifies every node of a trie (respect/decoding/verify.py:12-46).
+
+Node i is written to cache slot P + base + i (its physical slot) while its
+rotary position follows its depth (P + base + depth, its logical position);
+the mask opens the prompt and the ``base`` committed tokens to every node and
+each node to its ancestors.  The mask and the depths are built on the GPU
+from the parent array (rspx_trie_mask) instead of a host-built dense mask.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ..candidates.trie import Trie
+
+
+def node_slots(base: int, n: int) -> int:
+    """Node-segment width of a call: committed + trie slots, padded to 32."""
+    return max(32, -(-(base + n) // 32) * 32)
+
+
+def trie_mask(tree: Trie, base: int, NN: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """(msk [N, NN] uint8, depth [N] int32) on the GPU."""
+    N = len(tree.nodes)
+    parent = torch.from_numpy(tree.parents).to(device)
+    msk = torch.empty((N, NN), dtype=torch.uint8, device=device)
+    depth = torch.empty(N, dtype=torch.int32, device=device)
+    rc = _lib.lib().rspx_trie_mask(parent.data_ptr(), N, base, N, NN, msk.data_ptr(), NN, depth.data_ptr(),
+                                   _lib.stream_ptr(torch.device(device)))
+    _lib.check("rspx_trie_mask", rc)
+    return msk, depth
+
+
+@torch.no_grad()
+def verify_trie(model, cache, tree: Trie, P: int, base: int) -> torch.Tensor:
+    """fp32 logits [N, V] of every trie node."""
+    dev = model.device
+    N = len(tree.nodes)
+    NN = node_slots(base, N)
+    if P + NN > cache.cap:
+        raise ValueError("KV cache too small for the trie")
+    msk, depth = trie_mask(tree, base, NN, dev)
+    ids = torch.from_numpy(tree.tokens).to(dev)
+    start = P + base
+    slots = torch.arange(start, start + N, dtype=torch.int32, device=dev)
+    return model.forward(ids, slots, depth.to(torch.int64) + start, cache, P, msk, NN)

@@ -1,0 +1,43 @@
+"""Linear layer whose result does not depend on the number of rows.
+
+Same call signature and meaning as respect/kernels/gemm.py:30-41 (``linear``):
+x (..., K) @ w (N, K)^T -> (..., N), bf16 inputs, fp32 accumulation, output in
+``out_dtype`` (default x.dtype; torch.float32 for the vocabulary projection as
+respect/kernels/patch.py:23 asks).  The Triton tuning keywords (BM, BN, BK,
+num_warps, num_stages) are accepted and ignored: the HIP kernel
+(respect_amd/csrc/gemm.hip) fixes its own K order from (N, K) alone.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ._tensor import as_kernel_input
+
+
+def linear(x, w, BM=32, BN=128, BK=64, num_warps=4, num_stages=2, out_dtype=None, out=None):
+    """x (M, K) @ w (N, K)^T -> (M, N). Bias is handled by the caller."""
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise TypeError("linear: bf16 x and w are required")
+    out_dtype = out_dtype or x.dtype
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("linear: out_dtype must be bf16 or fp32")
+    K = x.shape[-1]
+    N = w.shape[0]
+    if w.dim() != 2 or w.shape[1] != K:
+        raise ValueError(f"linear: w must be [N, {K}], got {tuple(w.shape)}")
+    xs = as_kernel_input(x.reshape(-1, K), "x")
+    w2 = as_kernel_input(w, "w")
+    M = xs.shape[0]
+    if out is None:
+        out = torch.empty((M, N), device=x.device, dtype=out_dtype)
+    L = _lib.lib()
+    need = L.rspx_linear_workspace_bytes(M, N, K)
+    if need < 0:
+        _lib.check("rspx_linear_workspace_bytes", -2)
+    ws = _lib.workspace(x.device, max(need, 16), tag="linear")
+    rc = L.rspx_linear(xs.data_ptr(), xs.stride(0), w2.data_ptr(), w2.stride(0), out.data_ptr(), out.stride(0),
+                       M, N, K, 1 if out_dtype == torch.float32 else 0, ws.data_ptr(), ws.numel(),
+                       _lib.stream_ptr(x.device))
+    _lib.check("rspx_linear", rc)
+    return out.reshape(*x.shape[:-1], N)

@@ -1,0 +1,157 @@
+"""The verification step on a small random decoder, end to end on the GPU.
+
+Bar (the reference's output-preservation check, summary.json "tokens and
+committed KV equal"): tokens accepted by trie verification, and the KV they
+leave in the cache, are bitwise identical to token-by-token greedy decoding
+with the same kernels; the verified logits of every accepted node equal the
+1-token logits bit for bit.  A CPU float64/fp32 reference decoder
+(oracle/decoder.py) checks the wiring of the forward within a loose bound.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+CFG = dict(layers=2, hidden=512, heads=4, kv_heads=2, head_dim=128, ffn=1024, vocab=4096)
+P = 100
+
+
+@pytest.fixture(scope="module")
+def model():
+    from respect_amd.decoding.engine import Decoder, DecoderConfig
+    return Decoder(DecoderConfig(**CFG), seed=1, std=0.05)
+
+
+def _prompt(seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, CFG["vocab"], (P,), generator=g)
+
+
+def _filled_cache(model, chunk=64):
+    from respect_amd.decoding.kv_buffer import KVCache
+    c = model.cfg
+    cache = KVCache(c.layers, c.kv_heads, c.head_dim, P + 256)
+    last = model.prefill(_prompt().cuda(), cache, chunk=chunk)
+    return cache, last
+
+
+def _trie(seq, rng, n_other=3, vocab=4096, length=24):
+    from respect_amd.candidates.trie import build_trie
+    seqs = [list(seq[:length])]
+    for _ in range(n_other):
+        p = int(rng.integers(1, 17))
+        seqs.append(list(seq[:p]) + [int(t) for t in rng.integers(0, vocab, length - p)])
+    return build_trie(seqs)
+
+
+def test_prefill_is_deterministic(model):
+    """Same chunking twice: the same bits.  A different chunking changes which
+    keys a row sees as prompt (grouped tree) and which as nodes (slot-order
+    fold), so only layer 0's K/V -- computed before any attention -- must
+    agree across chunkings."""
+    a, la = _filled_cache(model, chunk=64)
+    b, lb = _filled_cache(model, chunk=64)
+    c, _ = _filled_cache(model, chunk=100)
+    for li in range(model.cfg.layers):
+        assert torch.equal(a.k[li][:, :P], b.k[li][:, :P]) and torch.equal(a.v[li][:, :P], b.v[li][:, :P])
+    assert torch.equal(la, lb)
+    assert torch.equal(a.k[0][:, :P], c.k[0][:, :P]) and torch.equal(a.v[0][:, :P], c.v[0][:, :P])
+
+
+def test_forward_wiring_matches_cpu_reference(model):
+    from oracle.decoder import RefDecoder
+    from respect_amd.decoding.acceptance import greedy_token
+    from respect_amd.decoding.sequential import forward_token
+    cache, last = _filled_cache(model)
+    ref = RefDecoder(model)
+    ids = _prompt()
+    S = P + 8
+    allow = torch.tril(torch.ones(P, S, dtype=torch.bool))
+    rl, kv = ref.forward(ids.tolist(), list(range(P)), list(range(P)), allow)
+    got = last.cpu()
+    assert (got - rl[-1:]).abs().max() <= 0.05 * rl.abs().max()
+    tok = int(greedy_token(last).item())
+    lg = forward_token(model, cache, tok, P, 0).cpu()
+    allow1 = torch.zeros(1, S, dtype=torch.bool)
+    allow1[0, :P + 1] = True
+    r1, _ = ref.forward([tok], [P], [P], allow1, kv)
+    assert (lg - r1).abs().max() <= 0.05 * r1.abs().max()
+
+
+def test_trie_verification_equals_token_by_token(model):
+    from respect_amd.decoding.acceptance import greedy_token
+    from respect_amd.decoding.respect import respect_step
+    from respect_amd.decoding.sequential import forward_token
+    from respect_amd.decoding.verify import verify_trie
+    # token-by-token reference: 60 greedy tokens, their logits and KV
+    ar, last = _filled_cache(model)
+    t0 = int(greedy_token(last).item())
+    G, logits_ar = [t0], []
+    for c in range(60):
+        lg = forward_token(model, ar, G[-1], P, c)
+        logits_ar.append(lg)
+        G.append(int(greedy_token(lg).item()))
+    # trie verification from the same prompt KV
+    sp, _ = _filled_cache(model)
+    rng = np.random.default_rng(0)
+    base, first = 0, t0
+    for step, length in enumerate((24, 24, 4)):
+        if length == 24:
+            tree = _trie(G[base:], rng)
+        else:  # the target's path leaves the trie after 4 tokens
+            from respect_amd.candidates.trie import build_trie
+            tree = build_trie([G[base:base + 4] + [(G[base + 4] + 1) % 4096] * 4,
+                               G[base:base + 2] + [7, 7, 7, 7, 7, 7]])
+        logits = verify_trie(model, sp, tree, P, base)
+        acc, rec, path = respect_step(model, sp, tree, first, P, base, eos=-1)
+        print(f"[respect] step {step}: base {base}, {len(tree.nodes)} nodes, accepted {len(acc)}", flush=True)
+        assert acc == G[base:base + length] and rec == G[base + length]
+        for j, node in enumerate(path):  # verified logits == 1-token logits, bitwise
+            assert torch.equal(logits[node:node + 1], logits_ar[base + j])
+        for li in range(model.cfg.layers):  # committed KV == token-by-token KV, bitwise
+            s0, s1 = P + base, P + base + length
+            assert torch.equal(sp.k[li][:, s0:s1], ar.k[li][:, s0:s1])
+            assert torch.equal(sp.v[li][:, s0:s1], ar.v[li][:, s0:s1])
+        base += length
+        first = rec
+
+
+def test_greedy_token_rules():
+    from respect_amd.decoding.acceptance import greedy_token
+    lg = torch.tensor([[0.0, 5.0, 5.0, 1.0], [9.0, 1.0, 2.0, 2.0], [1.0, float("nan"), 3.0, float("nan")]],
+                      device="cuda")
+    assert greedy_token(lg).tolist() == [1, 0, 1]
+    assert greedy_token(lg, 0, 1).tolist() == [1, 2, 1]
+    assert greedy_token(lg[:2], 1, 2).tolist() == [3, 0]
+    big = torch.randn(3, 151936, device="cuda")
+    big[1, 100000] = 1e9
+    big[2, 7] = big[2, 150000] = 1e9
+    assert greedy_token(big).tolist() == [int(big[0].argmax()), 100000, 7]
+    # action-vocabulary range excluded (acceptance.py:11-17)
+    assert greedy_token(big, 100000, 50001).tolist()[1:] == [int(torch.cat([big[1, :100000], big[1, 150001:]]).argmax()), 7]
+
+
+def test_trie_mask_from_parents():
+    from respect_amd.candidates.trie import build_trie, node_mask
+    from respect_amd.decoding.verify import trie_mask
+    tree = build_trie([(1, 2, 3, 4), (1, 2, 5), (6, 7), (1, 8, 9, 10, 11)])
+    for base in (0, 5, 37):
+        NN = max(32, -(-(base + len(tree.nodes)) // 32) * 32)
+        msk, depth = trie_mask(tree, base, NN, "cuda")
+        assert np.array_equal(msk.cpu().numpy().astype(bool), node_mask(tree, base, NN))
+        assert depth.cpu().tolist() == tree.depths.tolist()
+
+
+def test_kv_compact_overlapping_moves():
+    from respect_amd.decoding.kv_buffer import KVCache
+    c = KVCache(3, 2, 128, 64)
+    for t in c.k + c.v:
+        t.copy_(torch.randn_like(t, dtype=torch.float32).to(torch.bfloat16))
+    before = [t.clone() for t in c.k + c.v]
+    path = [0, 2, 3, 7, 8]          # destination of one is the source of the next
+    c.compact(10, path)
+    for t, b in zip(c.k + c.v, before):
+        exp = b.clone()
+        exp[:, 10:15] = b[:, [10 + s for s in path]]
+        assert torch.equal(t, exp)

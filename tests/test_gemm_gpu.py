@@ -1,0 +1,90 @@
+"""GPU parity and row-count invariance of the linear layer (csrc/gemm.hip).
+
+Parity bar: every bf16 output within the fp32-accumulation error bound
+(K 2^-24 sum|x w|) plus one bf16 rounding of the float64 result, and equal
+to the float64 result rounded to bf16 on at least 99% of elements (the
+accumulation error is far below half a bf16 ulp except near rounding ties
+and for results that cancel to much less than sum|x w|); fp32 outputs within
+the accumulation bound.  Row invariance is bitwise.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import bf16
+from oracle import gemm as G
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16).cuda()
+
+
+def _xw(seed, M, N, K):
+    rng = np.random.default_rng(seed)
+    x = bf16.round_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    w = bf16.round_bf16(0.02 * rng.standard_normal((N, K)).astype(np.float32))
+    return x, w
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (64, 6144, 4096), (7, 1024, 4096), (64, 4096, 12288),
+                                   (33, 256, 256), (130, 512, 768), (64, 24576, 4096)])
+def test_linear_parity_bf16(M, N, K):
+    from respect_amd.kernels.gemm import linear
+    print(f"[linear] M={M} N={N} K={K}", flush=True)
+    x, w = _xw(M * 7 + N, M, N, K)
+    out = linear(_dev(x), _dev(w)).float().cpu().numpy()
+    ex = G.linear_exact(x, w)
+    ref = bf16.round_bf16(ex.astype(np.float32))
+    bound = G.linear_error_bound(x, w)
+    allowed = bound + bf16.ulp(np.abs(ex) + bound)
+    d = bf16.ulp_diff(out, ref)
+    print(f"  max ulp {d.max():.2f} equal {(out == ref).mean():.5f} "
+          f"max err/allowed {(np.abs(out - ex) / allowed).max():.3f}", flush=True)
+    assert np.all(np.abs(out - ex) <= allowed)
+    assert (out == ref).mean() >= 0.99
+
+
+def test_linear_parity_fp32_out():
+    from respect_amd.kernels.gemm import linear
+    x, w = _xw(5, 64, 16384, 4096)
+    out = linear(_dev(x), _dev(w), out_dtype=torch.float32).cpu().numpy().astype(np.float64)
+    ex = G.linear_exact(x, w)
+    assert np.all(np.abs(out - ex) <= G.linear_error_bound(x, w) + 1e-30)
+
+
+def test_linear_is_row_count_invariant():
+    """tests/test_kernel_invariance.py:8-17 of the reference, plus more row sets."""
+    from respect_amd.kernels.gemm import linear
+    torch.manual_seed(0)
+    x = torch.randn(64, 4096, device="cuda", dtype=torch.bfloat16)
+    w = torch.randn(1024, 4096, device="cuda", dtype=torch.bfloat16)
+    kw = dict(BM=32, BN=128, BK=128, num_warps=4, num_stages=3)
+    full = linear(x, w, **kw)
+    for m in (1, 7, 33):
+        assert torch.equal(linear(x[:m], w, **kw), full[:m])
+    assert torch.equal(linear(x[20:23], w), full[20:23])
+    big = torch.cat([x, x.flip(0), x[:5]])  # 133 rows: three 64-row tiles
+    fb = linear(big, w)
+    assert torch.equal(fb[:64], full) and torch.equal(fb[64:128], full.flip(0)) and torch.equal(fb[128:], full[:5])
+    # fp32 output (the vocabulary projection) too
+    f32 = linear(x, w, out_dtype=torch.float32)
+    assert torch.equal(linear(x[7:8], w, out_dtype=torch.float32), f32[7:8])
+
+
+def test_linear_strided_and_errors():
+    from respect_amd._lib import RspxError, lib
+    from respect_amd.kernels.gemm import linear
+    x, w = _xw(9, 16, 512, 1024)
+    xd, wd = _dev(x), _dev(w)
+    big = torch.zeros(16, 2048, device="cuda", dtype=torch.bfloat16)
+    big[:, 512:1536] = xd
+    assert torch.equal(linear(big[:, 512:1536], wd), linear(xd, wd))
+    # the chunk count depends on (N, K) only
+    assert lib().rspx_linear_splits(4096, 4096) == lib().rspx_linear_splits(4096, 4096) > 0
+    with pytest.raises(RspxError):
+        linear(torch.zeros(4, 100, device="cuda", dtype=torch.bfloat16),
+               torch.zeros(16, 100, device="cuda", dtype=torch.bfloat16))
+    with pytest.raises(TypeError):
+        linear(xd.float(), wd)
