@@ -282,6 +282,98 @@ def bench_swiglu(args) -> dict:
             "hbm_frac_of_peak": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def _target_trie(cont, rng, n_seqs=4, length=24, target_nodes=64, vocab=151936):
+    """Trie of ``n_seqs`` candidates of ``length`` tokens rooted at cont[0]: one is
+    the target's own greedy continuation ``cont``, the others share a prefix of
+    it (length uniform in [1, 16]) and continue randomly; redrawn until the trie
+    has ``target_nodes`` nodes."""
+    from respect_amd.candidates.trie import build_trie
+    for _ in range(10000):
+        seqs = [list(cont[:length])]
+        for _ in range(n_seqs - 1):
+            p = int(rng.integers(1, 17))
+            seqs.append(list(cont[:p]) + [int(t) for t in rng.integers(0, vocab, length - p)])
+        tree = build_trie(seqs)
+        if len(tree.nodes) == target_nodes:
+            return tree
+    return tree
+
+
+def bench_decoder(args) -> dict:
+    """One speculative verification step of a random-init 36-layer 8B-shape GQA
+    decoder (hidden 4096, 32 q / 8 kv heads, head_dim 128, FFN 12288 SwiGLU,
+    vocab 151936, bf16 weights ~ N(0, 0.02)) over a 3072-token prompt KV built
+    from random ids: a 64-node trie is verified in one forward, walked with the
+    target's greedy choices, and the accepted path's KV compacted; then the
+    same tokens are decoded one forward per token.  Tokens and committed KV
+    must match bitwise; committed tok/s = accepted tokens / verification time."""
+    import numpy as np
+    import torch
+
+    from respect_amd.decoding.acceptance import greedy_token
+    from respect_amd.decoding.engine import Decoder, DecoderConfig
+    from respect_amd.decoding.kv_buffer import KVCache
+    from respect_amd.decoding.respect import respect_step
+    from respect_amd.decoding.sequential import forward_token
+
+    cfg = DecoderConfig()
+    P, steps = 3072, args.decoder_steps
+    _log("decoder: random-initialising the 36-layer 8B-shape model")
+    model = Decoder(cfg, seed=0, std=0.02)
+    g = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, cfg.vocab, (P,), generator=g).cuda()
+    cap = P + 24 * (steps + 2) + 128
+    caches = []
+    t0 = time.perf_counter()
+    for _ in range(2):
+        c = KVCache(cfg.layers, cfg.kv_heads, cfg.head_dim, cap)
+        last = model.prefill(prompt, c, chunk=512)
+        caches.append(c)
+    torch.cuda.synchronize()
+    _log(f"decoder: prompt KV of {P} tokens built twice in {time.perf_counter() - t0:.1f} s")
+    ar, sp = caches
+    # Token-by-token greedy reference: the tokens the tries are built from.
+    first = int(greedy_token(last).item())
+    n_ar = 24 * (steps + 1) + 1
+    G = [first]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for c in range(n_ar):
+        G.append(int(greedy_token(forward_token(model, ar, G[-1], P, c)).item()))
+    torch.cuda.synchronize()
+    ar_ms = (time.perf_counter() - t0) / n_ar * 1e3
+    _log(f"decoder: {n_ar} tokens decoded one by one, {ar_ms:.2f} ms per token")
+    rng = np.random.default_rng(0)
+    base, nxt, accepted, times, nodes, ok = 0, first, 0, [], [], True
+    for step in range(steps + 1):          # step 0 is the warm-up
+        tree = _target_trie(G[base:], rng)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        acc, rec, path = respect_step(model, sp, tree, nxt, P, base, eos=-1)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t1
+        ok &= acc == G[base:base + len(acc)] and rec == G[base + len(acc)]
+        if step > 0:
+            times.append(dt)
+            accepted += len(acc)
+            nodes.append(len(tree.nodes))
+        base += len(acc)
+        nxt = rec
+    kv_equal = all(torch.equal(sp.k[i][:, P:P + base], ar.k[i][:, P:P + base]) and
+                   torch.equal(sp.v[i][:, P:P + base], ar.v[i][:, P:P + base]) for i in range(cfg.layers))
+    step_s = sum(times) / len(times)
+    wbytes = cfg.weight_bytes()
+    return {"workload": "speculative verification step, random-init 36-layer 8B-shape GQA decoder "
+                        "(hidden 4096, 32q/8kv, hd128, FFN 12288, vocab 151936), 3072-token prompt KV, "
+                        "64-node trie of 4 candidates x 24 tokens (one is the target's greedy continuation)",
+            "steps": len(times), "trie_nodes": nodes, "ms_per_verify_step": round(step_s * 1e3, 3),
+            "accepted_per_step": accepted / len(times),
+            "committed_tok_s": round(accepted / sum(times), 1),
+            "ar_ms_per_token": round(ar_ms, 3), "ar_tok_s": round(1e3 / ar_ms, 1),
+            "weight_GBps_verify": round(wbytes / step_s / 1e9, 1),
+            "tokens_equal_1token_decoding": bool(ok), "committed_kv_bitwise_equal": bool(kv_equal)}
+
+
 def bench_copy(args) -> dict:
     """Device-to-device copy of a 1 GiB bf16 buffer (torch's copy kernel): the
     measured HBM ceiling the kernels above are compared with, and the known-size
@@ -307,6 +399,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 PMC passes")
+    ap.add_argument("--no-decoder", action="store_true", help="skip the 36-layer verification-step line")
+    ap.add_argument("--decoder-steps", type=int, default=4, help="timed verification steps")
     ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.traffic_probe:
@@ -332,6 +426,10 @@ def main() -> int:
         _log("timing RMSNorm + q/k norm+RoPE and SwiGLU")
         res["extra"] = {"norm_rope": bench_norm_rope(args), "swiglu": bench_swiglu(args),
                         "copy": bench_copy(args)}
+    if not args.no_decoder:
+        dec = bench_decoder(args)
+        res["committed_tok_s"] = dec["committed_tok_s"]
+        res.setdefault("extra", {})["verify_step"] = dec
     res.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "scaling": "weak",
                 "vs_baseline": None, "data": "synthetic (seeded torch.randn / numpy tries)"})
     res["wall_s"] = round(time.time() - t0, 2)
