@@ -322,7 +322,10 @@ def bench_decoder(args) -> dict:
     model = Decoder(cfg, seed=0, std=0.02)
     g = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, cfg.vocab, (P,), generator=g).cuda()
-    cap = P + 24 * (steps + 2) + 128
+    from respect_amd.decoding.verify import node_slots
+    max_base = 24 * (steps + 2)
+    nn_max = node_slots(max_base, 64, 64)
+    cap = P + nn_max + 64                     # + scratch slots of the 64-row graphs
     caches = []
     t0 = time.perf_counter()
     for _ in range(2):
@@ -332,6 +335,13 @@ def bench_decoder(args) -> dict:
     torch.cuda.synchronize()
     _log(f"decoder: prompt KV of {P} tokens built twice in {time.perf_counter() - t0:.1f} s")
     ar, sp = caches
+    # HIP graphs of the forwards the run will replay (node segments padded to 64).
+    t0 = time.perf_counter()
+    for NN in range(64, nn_max + 1, 64):
+        model.graphed(ar, P, 1, NN)
+        model.graphed(sp, P, 64, NN)
+    torch.cuda.synchronize()
+    _log(f"decoder: {len(model._graphs)} forwards captured in {time.perf_counter() - t0:.1f} s")
     # Token-by-token greedy reference: the tokens the tries are built from.
     first = int(greedy_token(last).item())
     n_ar = 24 * (steps + 1) + 1
@@ -339,7 +349,7 @@ def bench_decoder(args) -> dict:
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for c in range(n_ar):
-        G.append(int(greedy_token(forward_token(model, ar, G[-1], P, c)).item()))
+        G.append(int(greedy_token(forward_token(model, ar, G[-1], P, c, graph=True)).item()))
     torch.cuda.synchronize()
     ar_ms = (time.perf_counter() - t0) / n_ar * 1e3
     _log(f"decoder: {n_ar} tokens decoded one by one, {ar_ms:.2f} ms per token")
@@ -349,7 +359,7 @@ def bench_decoder(args) -> dict:
         tree = _target_trie(G[base:], rng)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-        acc, rec, path = respect_step(model, sp, tree, nxt, P, base, eos=-1)
+        acc, rec, path = respect_step(model, sp, tree, nxt, P, base, eos=-1, graph=True)
         torch.cuda.synchronize()
         dt = time.perf_counter() - t1
         ok &= acc == G[base:base + len(acc)] and rec == G[base + len(acc)]
@@ -371,7 +381,8 @@ def bench_decoder(args) -> dict:
             "committed_tok_s": round(accepted / sum(times), 1),
             "ar_ms_per_token": round(ar_ms, 3), "ar_tok_s": round(1e3 / ar_ms, 1),
             "weight_GBps_verify": round(wbytes / step_s / 1e9, 1),
-            "tokens_equal_1token_decoding": bool(ok), "committed_kv_bitwise_equal": bool(kv_equal)}
+            "tokens_equal_1token_decoding": bool(ok), "committed_kv_bitwise_equal": bool(kv_equal),
+            "launch": "HIP graphs (one captured forward per node-segment width), both paths"}
 
 
 def bench_copy(args) -> dict:

@@ -151,6 +151,14 @@ int64_t rspx_linear_workspace_bytes(int M, int N, int K);
 int rspx_linear(const void* x, int64_t sx, const void* w, int64_t sw, void* out, int64_t so, int M, int N, int K,
                 int out_fp32, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* The same product, left as its fp32 chunk partials part[S][M][N] (S =
+ * rspx_linear_splits(N, K), also when S == 1) for a consumer that adds them
+ * in chunk order and rounds -- rspx_add_rmsnorm_partials,
+ * rspx_qkv_rope_cache_partials -- so the sum never takes a launch of its own.
+ */
+int rspx_linear_partials(const void* x, int64_t sx, const void* w, int64_t sw, float* part, int M, int N, int K,
+                         void* stream);
+
 /* ---------------------------------------------------------------- residual add + RMSNorm
  * xo[r] = bf16(r[r] + h[r]) (PyTorch's bf16 add), y[r] = rmsnorm(xo[r], w, eps)
  * bit for bit as rspx_rmsnorm would give on xo.  Same size rules as
@@ -158,6 +166,13 @@ int rspx_linear(const void* x, int64_t sx, const void* w, int64_t sw, void* out,
  */
 int rspx_add_rmsnorm(const void* r, int64_t sr, const void* h, int64_t sh, const void* w, void* xo, int64_t sxo,
                      void* y, int64_t sy, int rows, int n, float eps, void* stream);
+
+/* The same with h given as the fp32 chunk partials hp[S][rows][n] of a
+ * linear layer (rspx_linear_partials): h = bf16 of their chunk-order sum,
+ * bit for bit the h rspx_linear would have produced.
+ */
+int rspx_add_rmsnorm_partials(const void* r, int64_t sr, const float* hp, int S, const void* w, void* xo, int64_t sxo,
+                              void* y, int64_t sy, int rows, int n, float eps, void* stream);
 
 /* ---------------------------------------------------------------- q/k/v epilogue of a decoder layer
  * qkv: [T, (HQ + 2 HK) D] packed projection rows [q | k | v] (row stride
@@ -170,6 +185,14 @@ int rspx_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* wq, const voi
                         const void* sin, int64_t scs, const int32_t* slots, void* cache_k, int64_t skh, int64_t skn,
                         void* cache_v, int64_t svh, int64_t svn, void* qo, int T, int HQ, int HK, int D, float eps,
                         void* stream);
+
+/* The same with the projection given as fp32 chunk partials
+ * qkvp[S][T][(HQ + 2 HK) D] (rspx_linear_partials).
+ */
+int rspx_qkv_rope_cache_partials(const float* qkvp, int S, const void* wq, const void* wk, const void* cos,
+                                 const void* sin, int64_t scs, const int32_t* slots, void* cache_k, int64_t skh,
+                                 int64_t skn, void* cache_v, int64_t svh, int64_t svn, void* qo, int T, int HQ, int HK,
+                                 int D, float eps, void* stream);
 
 /* ---------------------------------------------------------------- trie mask from a parent array
  * parent: [N] int32 (parent index, -1 for a root; parents precede children).
@@ -191,11 +214,14 @@ int rspx_kv_compact(const uint64_t* bases, int n_tensors, int HK, int D, int64_t
                     const int32_t* src, int n, void* stream);
 
 /* ---------------------------------------------------------------- greedy token per row
- * out[m] = argmax over j of logits[m][j] (fp32, row stride sl), columns
- * [off, off + size) counted as -inf; NaN is the largest value; ties go to the
- * lowest index.
+ * out[m] = argmax over j of logits[m][j] (fp32, row stride sl, 16-byte
+ * aligned rows), columns [off, off + size) counted as -inf; NaN is the
+ * largest value; ties go to the lowest index.  workspace: at least
+ * rspx_argmax_workspace_bytes(M, V) bytes.
  */
-int rspx_argmax_rows(const float* logits, int64_t sl, int M, int V, int off, int size, int64_t* out, void* stream);
+int64_t rspx_argmax_workspace_bytes(int M, int V);
+int rspx_argmax_rows(const float* logits, int64_t sl, int M, int V, int off, int size, int64_t* out, void* workspace,
+                     int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -53,4 +53,18 @@ __device__ __forceinline__ int shfl_idx_i(int v, int src) {
   return __builtin_amdgcn_ds_bpermute(src << 2, v);
 }
 
+// The output of a K-split linear layer: the fp32 chunk partials of one
+// element added in chunk order, ((p0 + p1) + p2) + ... (stride = elements
+// between chunks).  Every consumer of split partials uses this, so the value
+// (and its bf16 rounding) is the same wherever the sum is taken.
+__device__ __forceinline__ f32x4 sum_parts4(const float* p, int S, int64_t stride) {
+  f32x4 v = *reinterpret_cast<const f32x4*>(p);
+  for (int s = 1; s < S; ++s) {
+    const f32x4 q = *reinterpret_cast<const f32x4*>(p + s * stride);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = v[e] + q[e];
+  }
+  return v;
+}
+
 }  // namespace rspx

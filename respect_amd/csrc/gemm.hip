@@ -52,6 +52,7 @@ struct Args {
   void* out; int64_t so;          // [M, N]: bf16 or fp32 (S == 1)
   float* part;                    // [S][M][N] fp32 (S > 1)
   int M, N, K, S, KC, out_fp32;
+  int to_part;                    // write chunk partials even when S == 1
 };
 
 constexpr int kOOB = 0x7ffffff0;  // a buffer offset past any descriptor: loads return 0, touch nothing
@@ -83,18 +84,21 @@ __device__ __forceinline__ void round_compute(const lds_char_t* xb, const u32x4 
   }
 }
 
-// Every wave issues, per round and in this order, 8 X chunks into LDS (row
-// tile t = w, k-blocks 0..7: rows 16 t + n16, k [8 g4, +8) of the block) and
-// 8 W loads into registers.  Rounds past the chunk (the last prefetch) and
-// rows past M use out-of-range offsets: zeros, no memory traffic.  Issuing
-// the same number of loads on every path keeps the waits exact.
-__device__ __forceinline__ void issue_round(__amdgpu_buffer_rsrc_t rx, int xoff, __amdgpu_buffer_rsrc_t rw, int woff,
-                                            int rr, int nr, lds_char_t* xb, int w, u32x4 (&wf)[kRoundKB]) {
+// X chunks of round rr into LDS buffer xb: wave w issues row tile t = w,
+// k-blocks 0..7 (rows 16 t + n16, k [8 g4, +8) of the block).  W loads of
+// round rr into registers.  Rounds past the chunk and rows past M use
+// out-of-range offsets: zeros, no memory traffic.  Every wave issues exactly
+// 8 X chunks and 8 W loads per round on every path, so the waits below are
+// exact counts.
+__device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t rx, int xoff, int rr, int nr, lds_char_t* xb, int w) {
   const bool live = rr < nr;
 #pragma unroll
   for (int kb = 0; kb < kRoundKB; ++kb)
     x_dma16(rx, live ? xoff + 2 * (rr * kRoundK + 32 * kb) : kOOB, xb + (kb * 4 + w) * 1024);
   asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ void issue_w(__amdgpu_buffer_rsrc_t rw, int woff, int rr, int nr, u32x4 (&wf)[kRoundKB]) {
+  const bool live = rr < nr;
 #pragma unroll
   for (int kb = 0; kb < kRoundKB; ++kb)
     wf[kb] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -102,7 +106,30 @@ __device__ __forceinline__ void issue_round(__amdgpu_buffer_rsrc_t rx, int xoff,
   asm volatile("" ::: "memory");
 }
 
-template <int MT>
+// s_waitcnt vmcnt(n) for the counts the unrolled pipeline uses.
+__device__ __forceinline__ void vm_wait_n(int n) {
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    case 8: __builtin_amdgcn_s_waitcnt(8 | 0x70 | 0xF00); break;
+    case 16: __builtin_amdgcn_s_waitcnt((16 & 15) | ((16 >> 4) << 14) | 0x70 | 0xF00); break;
+    case 24: __builtin_amdgcn_s_waitcnt((24 & 15) | ((24 >> 4) << 14) | 0x70 | 0xF00); break;
+    default: __builtin_amdgcn_s_waitcnt((32 & 15) | ((32 >> 4) << 14) | 0x70 | 0xF00); break;
+  }
+}
+__device__ __forceinline__ void vm_wait24() {
+  __builtin_amdgcn_s_waitcnt((24 & 15) | ((24 >> 4) << 14) | 0x70 | 0xF00);  // vmcnt(24)
+}
+__device__ __forceinline__ void vm_wait32() {
+  __builtin_amdgcn_s_waitcnt((32 & 15) | ((32 >> 4) << 14) | 0x70 | 0xF00);  // vmcnt(32)
+}
+
+// Pipeline: W (the HBM stream) is requested 3 rounds ahead into a ring of 4
+// register buffers, X (L2-resident) 1 round ahead into 2 LDS buffers.  Round
+// r issues X(r + 1) and W(r + 3), then waits until X(r) and W(r) have landed.
+// NR > 0: the NR rounds are unrolled at compile time, so every wait count is
+// exact and the compiler's own waits for the W registers never drain the
+// prefetch; NR == 0: a run-time loop (any round count, shallower prefetch).
+template <int MT, int NR>
 __global__ __launch_bounds__(256) void gemm_kernel(Args A) {
   __shared__ __attribute__((aligned(16))) char xs[2][kRoundKB * 4 * 1024];  // 2 x 32 KB
   constexpr int XB = kRoundKB * 4 * 1024;
@@ -117,7 +144,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(Args A) {
   const int col = nt * kCols + 16 * w;        // this wave's first column
   const int row0 = mt * kRows;
   const int k0 = s * A.KC;
-  const int nr = A.KC / kRoundK;
+  const int nr = NR > 0 ? NR : A.KC / kRoundK;
   const bool has_cols = col < A.N;            // N % 16 == 0: whole tiles only
 
   // X: rows [row0, M) from column k0.  W: this wave's 16 rows, columns
@@ -135,22 +162,45 @@ __global__ __launch_bounds__(256) void gemm_kernel(Args A) {
 #pragma unroll
   for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  u32x4 wa[kRoundKB], wb[kRoundKB];
-  issue_round(rx, xoff, rw, woff, 0, nr, xl, w, wa);
-  for (int r = 0; r < nr; r += 2) {
-    // round r: X in buffer 0, W in wa; prefetch round r + 1 into buffer 1 / wb
-    issue_round(rx, xoff, rw, woff, r + 1, nr, xl + XB, w, wb);
-    vm_wait16();
-    raw_barrier();
-    round_compute<MT>(xl, wa, acc, lane);
-    raw_barrier();  // buffer 0 is free
-    if (r + 1 >= nr) break;
-    // round r + 1: X in buffer 1, W in wb; prefetch round r + 2 into buffer 0 / wa
-    issue_round(rx, xoff, rw, woff, r + 2, nr, xl, w, wa);
-    vm_wait16();
-    raw_barrier();
-    round_compute<MT>(xl + XB, wb, acc, lane);
-    raw_barrier();  // buffer 1 is free
+  if constexpr (NR > 0) {
+    // Only loads whose data is used are issued (the compiler would drop the
+    // others and the counts below would be off).  Exact wait per round: the
+    // loads issued after the later of X(r) and W(r).
+    u32x4 wbuf[4][kRoundKB];
+    issue_x(rx, xoff, 0, nr, xl, w);
+    issue_w(rw, woff, 0, nr, wbuf[0]);
+    if constexpr (NR > 1) issue_w(rw, woff, 1, nr, wbuf[1]);
+    if constexpr (NR > 2) issue_w(rw, woff, 2, nr, wbuf[2]);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      if (r + 1 < NR) issue_x(rx, xoff, r + 1, nr, xl + ((r + 1) & 1) * XB, w);
+      if (r + 3 < NR) issue_w(rw, woff, r + 3, nr, wbuf[(r + 3) & 3]);
+      const int younger = r == 0 ? 8 * ((1 < NR) + (2 < NR) + (1 < NR) + (3 < NR))
+                                 : 8 * ((r + 2 < NR) + (r + 1 < NR) + (r + 3 < NR));
+      vm_wait_n(younger);
+      raw_barrier();
+      round_compute<MT>(xl + (r & 1) * XB, wbuf[r & 3], acc, lane);
+      raw_barrier();
+    }
+  } else {
+    u32x4 wa[kRoundKB], wb[kRoundKB];
+    issue_x(rx, xoff, 0, nr, xl, w);
+    issue_w(rw, woff, 0, nr, wa);
+    for (int r = 0; r < nr; r += 2) {
+      issue_x(rx, xoff, r + 1, nr, xl + XB, w);
+      issue_w(rw, woff, r + 1, nr, wb);
+      vm_wait16();
+      raw_barrier();
+      round_compute<MT>(xl, wa, acc, lane);
+      raw_barrier();
+      if (r + 1 >= nr) break;
+      issue_x(rx, xoff, r + 2, nr, xl, w);
+      issue_w(rw, woff, r + 2, nr, wa);
+      vm_wait16();
+      raw_barrier();
+      round_compute<MT>(xl + XB, wb, acc, lane);
+      raw_barrier();
+    }
   }
   vm_wait0();
   if (!has_cols) return;
@@ -161,7 +211,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(Args A) {
     const int m = row0 + 16 * t + n16;
     if (m >= A.M) continue;
     const int n = col + 4 * g4;
-    if (A.S > 1) {
+    if (A.S > 1 || A.to_part) {
       *reinterpret_cast<f32x4*>(A.part + ((size_t)s * A.M + m) * A.N + n) = acc[t];
     } else if (A.out_fp32) {
       *reinterpret_cast<f32x4*>(static_cast<float*>(A.out) + (int64_t)m * A.so + n) = acc[t];
@@ -180,12 +230,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* part, int S, i
   const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (i >= (int64_t)M * N) return;
   const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
-  f32x4 v = *reinterpret_cast<const f32x4*>(part + i);
-  for (int s = 1; s < S; ++s) {
-    const f32x4 p = *reinterpret_cast<const f32x4*>(part + (size_t)s * M * N + i);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = v[e] + p[e];
-  }
+  const f32x4 v = sum_parts4(part + i, S, (int64_t)M * N);
   if (out_fp32) {
     *reinterpret_cast<f32x4*>(static_cast<float*>(out) + (int64_t)m * so + n) = v;
   } else {
@@ -223,40 +268,80 @@ extern "C" int64_t rspx_linear_workspace_bytes(int M, int N, int K) {
   return S > 1 ? (int64_t)S * M * N * (int64_t)sizeof(float) : 0;
 }
 
-extern "C" int rspx_linear(const void* x, int64_t sx, const void* w, int64_t sw, void* out, int64_t so, int M, int N,
-                           int K, int out_fp32, void* workspace, int64_t workspace_bytes, void* stream) {
-  if (M < 0 || N <= 0 || K <= 0) return RSPX_EINVAL;
-  if (N % 16 != 0 || K % gemm::kRoundK != 0) return RSPX_EUNSUPPORTED;
-  if (M == 0) return RSPX_OK;
-  if (!x || !w || !out) return RSPX_EINVAL;
-  if (sx < K || sw < K || so < N) return RSPX_EINVAL;
-  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-  if (!al(x) || !al(w) || !al(out) || sx % 8 || sw % 8 || so % 4) return RSPX_EALIGN;
-  if ((int64_t)64 * sx * 2 >= (1ll << 31) || (int64_t)16 * sw * 2 >= (1ll << 31)) return RSPX_EUNSUPPORTED;
+namespace rspx {
+static int linear_launch(const void* x, int64_t sx, const void* w, int64_t sw, void* out, int64_t so, int M, int N,
+                         int K, int out_fp32, float* part, int to_part, hipStream_t s) {
   const int S = linear_splits(N, K);
-  const int64_t need = S > 1 ? (int64_t)S * M * N * (int64_t)sizeof(float) : 0;
-  if (need > 0 && (!workspace || workspace_bytes < need || !al(workspace))) return RSPX_EWORKSPACE;
-
   gemm::Args a;
   a.x = static_cast<const uint16_t*>(x); a.sx = sx;
   a.w = static_cast<const uint16_t*>(w); a.sw = sw;
   a.out = out; a.so = so;
-  a.part = static_cast<float*>(workspace);
-  a.M = M; a.N = N; a.K = K; a.S = S; a.KC = K / S; a.out_fp32 = out_fp32 ? 1 : 0;
+  a.part = part;
+  a.M = M; a.N = N; a.K = K; a.S = S; a.KC = K / S; a.out_fp32 = out_fp32 ? 1 : 0; a.to_part = to_part;
   const int NT = (N + gemm::kCols - 1) / gemm::kCols;
   const int MTILES = (M + gemm::kRows - 1) / gemm::kRows;
   const int64_t grid = (int64_t)NT * S * MTILES;
   if (grid > 0x7fffffff) return RSPX_EUNSUPPORTED;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int mt = M >= 64 ? 4 : (M + 15) / 16;  // row tiles of the (only or first) 64-row tile
-  if (MTILES > 1 || mt == 4) hipLaunchKernelGGL(gemm::gemm_kernel<4>, dim3((unsigned)grid), dim3(256), 0, s, a);
-  else if (mt == 3) hipLaunchKernelGGL(gemm::gemm_kernel<3>, dim3((unsigned)grid), dim3(256), 0, s, a);
-  else if (mt == 2) hipLaunchKernelGGL(gemm::gemm_kernel<2>, dim3((unsigned)grid), dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(gemm::gemm_kernel<1>, dim3((unsigned)grid), dim3(256), 0, s, a);
-  if (S > 1) {
+  const int mt = (MTILES > 1 || M >= 64) ? 4 : (M + 15) / 16;  // row tiles per 64-row tile
+  const int nr = a.KC / gemm::kRoundK;
+  const dim3 g((unsigned)grid), b(256);
+#define RSPX_GEMM_NR(MTV)                                                                         \
+  switch (nr) {                                                                                  \
+    case 1: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 1>), g, b, 0, s, a); break;               \
+    case 2: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 2>), g, b, 0, s, a); break;               \
+    case 3: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 3>), g, b, 0, s, a); break;               \
+    case 4: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 4>), g, b, 0, s, a); break;               \
+    case 6: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 6>), g, b, 0, s, a); break;               \
+    case 8: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 8>), g, b, 0, s, a); break;               \
+    case 12: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 12>), g, b, 0, s, a); break;             \
+    case 16: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 16>), g, b, 0, s, a); break;             \
+    default: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 0>), g, b, 0, s, a); break;              \
+  }
+  if (mt == 4) { RSPX_GEMM_NR(4) }
+  else if (mt == 3) { RSPX_GEMM_NR(3) }
+  else if (mt == 2) { RSPX_GEMM_NR(2) }
+  else { RSPX_GEMM_NR(1) }
+#undef RSPX_GEMM_NR
+  if (S > 1 && !to_part) {
     const int64_t quads = (int64_t)M * N / 4;
-    hipLaunchKernelGGL(gemm::reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s,
-                       static_cast<const float*>(workspace), S, M, N, out, so, a.out_fp32);
+    hipLaunchKernelGGL(gemm::reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, part, S, M, N,
+                       out, so, a.out_fp32);
   }
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
+}
+
+static int linear_check(const void* x, int64_t sx, const void* w, int64_t sw, int M, int N, int K) {
+  if (M < 0 || N <= 0 || K <= 0) return RSPX_EINVAL;
+  if (N % 16 != 0 || K % gemm::kRoundK != 0) return RSPX_EUNSUPPORTED;
+  if (M == 0) return RSPX_OK;
+  if (!x || !w) return RSPX_EINVAL;
+  if (sx < K || sw < K) return RSPX_EINVAL;
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  if (!al(x) || !al(w) || sx % 8 || sw % 8) return RSPX_EALIGN;
+  if ((int64_t)64 * sx * 2 >= (1ll << 31) || (int64_t)16 * sw * 2 >= (1ll << 31)) return RSPX_EUNSUPPORTED;
+  return RSPX_OK;
+}
+}  // namespace rspx
+
+extern "C" int rspx_linear(const void* x, int64_t sx, const void* w, int64_t sw, void* out, int64_t so, int M, int N,
+                           int K, int out_fp32, void* workspace, int64_t workspace_bytes, void* stream) {
+  int rc = linear_check(x, sx, w, sw, M, N, K);
+  if (rc != RSPX_OK || M == 0) return rc;
+  if (!out) return RSPX_EINVAL;
+  if (so < N) return RSPX_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(out) & 15u) || so % 4) return RSPX_EALIGN;
+  const int S = linear_splits(N, K);
+  const int64_t need = S > 1 ? (int64_t)S * M * N * (int64_t)sizeof(float) : 0;
+  if (need > 0 && (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 15u)))
+    return RSPX_EWORKSPACE;
+  return linear_launch(x, sx, w, sw, out, so, M, N, K, out_fp32, static_cast<float*>(workspace), 0,
+                       static_cast<hipStream_t>(stream));
+}
+
+extern "C" int rspx_linear_partials(const void* x, int64_t sx, const void* w, int64_t sw, float* part, int M, int N,
+                                    int K, void* stream) {
+  int rc = linear_check(x, sx, w, sw, M, N, K);
+  if (rc != RSPX_OK || M == 0) return rc;
+  if (!part || (reinterpret_cast<uintptr_t>(part) & 15u)) return RSPX_EINVAL;
+  return linear_launch(x, sx, w, sw, nullptr, N, M, N, K, 1, part, 1, static_cast<hipStream_t>(stream));
 }

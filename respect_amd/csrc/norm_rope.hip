@@ -64,33 +64,49 @@ __device__ __forceinline__ u32x4 pack8(const float* f) {
 // 1 / sqrt(v): correctly rounded square root, then a correctly rounded divide.
 __device__ __forceinline__ float rsqrt_rn(float v) { return 1.0f / __builtin_sqrtf(v); }
 
-// Load one 8-element vector of the row: x, or with ADD the residual sum
-// bf16(r + h) (one fp32 add rounded once, as PyTorch's bf16 add), which is
-// then also stored to xo.
-template <bool ADD>
-__device__ __forceinline__ void load_row_vec(const uint16_t* x, const uint16_t* h, uint16_t* xo, int c, float* v) {
-  unpack8(*reinterpret_cast<const u32x4*>(x + c), v);
-  if constexpr (ADD) {
+// Input of a normalised row.  MODE 0: x.  MODE 1: the residual sum
+// bf16(x + h) with h bf16 (one fp32 add rounded once, as PyTorch's bf16 add),
+// also stored to xo.  MODE 2: the same with h the output of a K-split linear
+// layer given by its fp32 chunk partials (h = bf16(((p0 + p1) + ...)), the
+// value rspx_linear would have stored).
+struct RowIn {
+  const uint16_t* x; int64_t sx;
+  const uint16_t* h; int64_t sh;
+  const float* hp; int64_t shp, sps; int S;
+  uint16_t* xo; int64_t sxo;
+};
+
+template <int MODE>
+__device__ __forceinline__ void load_row_vec(const RowIn& in, int row, int c, float* v) {
+  unpack8(*reinterpret_cast<const u32x4*>(in.x + row * in.sx + c), v);
+  if constexpr (MODE >= 1) {
     float hv[8];
-    unpack8(*reinterpret_cast<const u32x4*>(h + c), hv);
+    if constexpr (MODE == 1) {
+      unpack8(*reinterpret_cast<const u32x4*>(in.h + row * in.sh + c), hv);
+    } else {
+      const float* hp = in.hp + row * in.shp + c;
+      const f32x4 a = sum_parts4(hp, in.S, in.sps), b = sum_parts4(hp + 4, in.S, in.sps);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) { hv[e] = round_bf16(a[e]); hv[4 + e] = round_bf16(b[e]); }
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = round_bf16(v[i] + hv[i]);
-    *reinterpret_cast<u32x4*>(xo + c) = pack8(v);
+    *reinterpret_cast<u32x4*>(in.xo + row * in.sxo + c) = pack8(v);
   }
 }
 
 // Normalise a row held by TPR lanes (TPR <= 64, all in one wave), VPL
 // 8-element vectors per lane.
-template <int TPR, int VPL, bool ADD>
-__device__ __forceinline__ void rms_row_wave(const uint16_t* x, const uint16_t* h, uint16_t* xo, const uint16_t* w,
-                                             uint16_t* y, int sub, int n, float eps) {
+template <int TPR, int VPL, int MODE>
+__device__ __forceinline__ void rms_row_wave(const RowIn& in, int row, const uint16_t* w, uint16_t* y, int sub,
+                                             int n, float eps) {
   float xv[VPL][8];
   float ss = 0.f;
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
     const int c = (v * TPR + sub) * 8;
     if (c < n) {
-      load_row_vec<ADD>(x, h, xo, c, xv[v]);
+      load_row_vec<MODE>(in, row, c, xv[v]);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) xv[v][i] = 0.f;
@@ -116,36 +132,31 @@ __device__ __forceinline__ void rms_row_wave(const uint16_t* x, const uint16_t* 
 }  // namespace
 
 // Rows of up to 64*8*VPL elements: one row per TPR lanes of a wave.
-template <int TPR, int VPL, bool ADD>
-__global__ __launch_bounds__(256) void rmsnorm_small_kernel(const uint16_t* x, int64_t sx, const uint16_t* h,
-                                                            int64_t sh, uint16_t* xo, int64_t sxo, const uint16_t* w,
-                                                            uint16_t* y, int64_t sy, int rows, int n, float eps) {
+template <int TPR, int VPL, int MODE>
+__global__ __launch_bounds__(256) void rmsnorm_small_kernel(RowIn in, const uint16_t* w, uint16_t* y, int64_t sy,
+                                                            int rows, int n, float eps) {
   const int lane = __lane_id();
   const int row = (blockIdx.x * 256 + threadIdx.x) / TPR;
   const int sub = lane % TPR;
   if (row >= rows) return;   // whole lane groups leave together (TPR divides 64)
-  rms_row_wave<TPR, VPL, ADD>(x + row * sx, h + row * sh, xo + row * sxo, w, y + row * sy, sub, n, eps);
+  rms_row_wave<TPR, VPL, MODE>(in, row, w, y + row * sy, sub, n, eps);
 }
 
 // Long rows: one 256-thread workgroup per row, VPL 8-element vectors per
 // thread.  Wave sums are combined in wave order through LDS.
-template <int VPL, bool ADD>
-__global__ __launch_bounds__(256) void rmsnorm_row_kernel(const uint16_t* x, int64_t sx, const uint16_t* h,
-                                                          int64_t sh, uint16_t* xo, int64_t sxo, const uint16_t* w,
-                                                          uint16_t* y, int64_t sy, int n, float eps) {
+template <int VPL, int MODE>
+__global__ __launch_bounds__(256) void rmsnorm_row_kernel(RowIn in, const uint16_t* w, uint16_t* y, int64_t sy, int n,
+                                                          float eps) {
   __shared__ float part[4];
   const int row = blockIdx.x;
   const int t = threadIdx.x, lane = __lane_id(), wv = t >> 6;
-  const uint16_t* xr = x + row * sx;
-  const uint16_t* hr = h + row * sh;
-  uint16_t* xor_ = xo + row * sxo;
   float xv[VPL][8];
   float ss = 0.f;
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
     const int c = (v * 256 + t) * 8;
     if (c < n) {
-      load_row_vec<ADD>(xr, hr, xor_, c, xv[v]);
+      load_row_vec<MODE>(in, row, c, xv[v]);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) xv[v][i] = 0.f;
@@ -170,6 +181,7 @@ __global__ __launch_bounds__(256) void rmsnorm_row_kernel(const uint16_t* x, int
       *reinterpret_cast<u32x4*>(yr + c) = pack8(o);
     }
   }
+  (void)lane;
 }
 
 namespace {
@@ -261,7 +273,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* q, in
 // q goes to qo [T, HQ, D], k and v are written straight into the KV cache at
 // the token's physical slot: cache[h][slot[t]][:] (head stride sh, slot
 // stride sn).
-__global__ __launch_bounds__(256) void qkv_rope_cache_kernel(const uint16_t* qkv, int64_t sqkv, const uint16_t* wq,
+__global__ __launch_bounds__(256) void qkv_rope_cache_kernel(const uint16_t* qkv, int64_t sqkv, const float* qp,
+                                                             int S, int64_t sps, const uint16_t* wq,
                                                              const uint16_t* wk, const uint16_t* cosb,
                                                              const uint16_t* sinb, int64_t scs, const int* slots,
                                                              uint16_t* ck, int64_t skh, int64_t skn, uint16_t* cv,
@@ -277,8 +290,16 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(const uint16_t* qkv
   if (rowid < nq) { kind = 0; t = rowid / HQ; hh = rowid - t * HQ; }
   else if (rowid < nq + nk) { kind = 1; t = (rowid - nq) / HK; hh = rowid - nq - t * HK; }
   else { kind = 2; t = (rowid - nq - nk) / HK; hh = rowid - nq - nk - t * HK; }
-  const uint16_t* row = qkv + (int64_t)t * sqkv + (kind == 0 ? hh * D : kind == 1 ? (HQ + hh) * D : (HQ + HK + hh) * D);
-  const u32x4 raw = *reinterpret_cast<const u32x4*>(row + sub * 8);
+  const int col = (kind == 0 ? hh * D : kind == 1 ? (HQ + hh) * D : (HQ + HK + hh) * D) + sub * 8;
+  u32x4 raw;
+  if (qp) {  // the projection's fp32 chunk partials, summed and rounded as rspx_linear would
+    const float* p = qp + (int64_t)t * sqkv + col;
+    const f32x4 a = sum_parts4(p, S, sps), b = sum_parts4(p + 4, S, sps);
+    raw[0] = pack_bf16x2(a[0], a[1]); raw[1] = pack_bf16x2(a[2], a[3]);
+    raw[2] = pack_bf16x2(b[0], b[1]); raw[3] = pack_bf16x2(b[2], b[3]);
+  } else {
+    raw = *reinterpret_cast<const u32x4*>(qkv + (int64_t)t * sqkv + col);
+  }
   if (kind == 2) {
     *reinterpret_cast<u32x4*>(cv + hh * svh + (int64_t)slots[t] * svn + sub * 8) = raw;
     return;
@@ -308,51 +329,71 @@ using namespace rspx;
 static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 namespace rspx {
-// The split depends on n only (never on rows), for plain and residual-add rows.
-template <bool ADD>
-static void launch_rmsnorm(const uint16_t* X, int64_t sx, const uint16_t* Hp, int64_t sh, uint16_t* XO, int64_t sxo,
-                           const uint16_t* W, uint16_t* Y, int64_t sy, int rows, int n, float eps, hipStream_t s) {
+// The split depends on n only (never on rows), for every input mode.
+template <int MODE>
+static void launch_rmsnorm(const RowIn& in, const uint16_t* W, uint16_t* Y, int64_t sy, int rows, int n, float eps,
+                           hipStream_t s) {
   const int vec = n / 8;
   if (vec <= 16) {
-    hipLaunchKernelGGL((rmsnorm_small_kernel<16, 1, ADD>), dim3((rows * 16 + 255) / 256), dim3(256), 0, s, X, sx, Hp,
-                       sh, XO, sxo, W, Y, sy, rows, n, eps);
+    hipLaunchKernelGGL((rmsnorm_small_kernel<16, 1, MODE>), dim3((rows * 16 + 255) / 256), dim3(256), 0, s, in, W, Y,
+                       sy, rows, n, eps);
   } else if (vec <= 64) {
-    hipLaunchKernelGGL((rmsnorm_small_kernel<64, 1, ADD>), dim3((rows * 64 + 255) / 256), dim3(256), 0, s, X, sx, Hp,
-                       sh, XO, sxo, W, Y, sy, rows, n, eps);
+    hipLaunchKernelGGL((rmsnorm_small_kernel<64, 1, MODE>), dim3((rows * 64 + 255) / 256), dim3(256), 0, s, in, W, Y,
+                       sy, rows, n, eps);
   } else if (vec <= 256) {
-    hipLaunchKernelGGL((rmsnorm_row_kernel<1, ADD>), dim3(rows), dim3(256), 0, s, X, sx, Hp, sh, XO, sxo, W, Y, sy, n, eps);
+    hipLaunchKernelGGL((rmsnorm_row_kernel<1, MODE>), dim3(rows), dim3(256), 0, s, in, W, Y, sy, n, eps);
   } else if (vec <= 512) {
-    hipLaunchKernelGGL((rmsnorm_row_kernel<2, ADD>), dim3(rows), dim3(256), 0, s, X, sx, Hp, sh, XO, sxo, W, Y, sy, n, eps);
+    hipLaunchKernelGGL((rmsnorm_row_kernel<2, MODE>), dim3(rows), dim3(256), 0, s, in, W, Y, sy, n, eps);
   } else if (vec <= 1024) {
-    hipLaunchKernelGGL((rmsnorm_row_kernel<4, ADD>), dim3(rows), dim3(256), 0, s, X, sx, Hp, sh, XO, sxo, W, Y, sy, n, eps);
+    hipLaunchKernelGGL((rmsnorm_row_kernel<4, MODE>), dim3(rows), dim3(256), 0, s, in, W, Y, sy, n, eps);
   } else {
-    hipLaunchKernelGGL((rmsnorm_row_kernel<8, ADD>), dim3(rows), dim3(256), 0, s, X, sx, Hp, sh, XO, sxo, W, Y, sy, n, eps);
+    hipLaunchKernelGGL((rmsnorm_row_kernel<8, MODE>), dim3(rows), dim3(256), 0, s, in, W, Y, sy, n, eps);
   }
 }
 }  // namespace rspx
 
+static int norm_args_ok(int rows, int n) {
+  if (rows < 0 || n <= 0 || n % 8 != 0 || n > 16384) return n % 8 ? RSPX_EUNSUPPORTED : RSPX_EINVAL;
+  return RSPX_OK;
+}
+
 extern "C" int rspx_rmsnorm(const void* x, int64_t sx, const void* w, void* y, int64_t sy, int rows, int n,
                             float eps, void* stream) {
-  if (rows < 0 || n <= 0 || n % 8 != 0 || n > 16384) return n % 8 ? RSPX_EUNSUPPORTED : RSPX_EINVAL;
-  if (rows == 0) return RSPX_OK;
+  int rc = norm_args_ok(rows, n);
+  if (rc != RSPX_OK || rows == 0) return rc;
   if (!x || !w || !y) return RSPX_EINVAL;
   if (!al16(x) || !al16(w) || !al16(y) || sx % 8 || sy % 8) return RSPX_EALIGN;
-  auto X = static_cast<const uint16_t*>(x);
-  launch_rmsnorm<false>(X, sx, X, sx, nullptr, 0, static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy,
-                        rows, n, eps, static_cast<hipStream_t>(stream));
+  RowIn in{static_cast<const uint16_t*>(x), sx, nullptr, 0, nullptr, 0, 0, 1, nullptr, 0};
+  launch_rmsnorm<0>(in, static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy, rows, n, eps,
+                    static_cast<hipStream_t>(stream));
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }
 
 extern "C" int rspx_add_rmsnorm(const void* r, int64_t sr, const void* h, int64_t sh, const void* w, void* xo,
                                 int64_t sxo, void* y, int64_t sy, int rows, int n, float eps, void* stream) {
-  if (rows < 0 || n <= 0 || n % 8 != 0 || n > 16384) return n % 8 ? RSPX_EUNSUPPORTED : RSPX_EINVAL;
-  if (rows == 0) return RSPX_OK;
+  int rc = norm_args_ok(rows, n);
+  if (rc != RSPX_OK || rows == 0) return rc;
   if (!r || !h || !w || !xo || !y) return RSPX_EINVAL;
   if (!al16(r) || !al16(h) || !al16(w) || !al16(xo) || !al16(y) || sr % 8 || sh % 8 || sxo % 8 || sy % 8)
     return RSPX_EALIGN;
-  launch_rmsnorm<true>(static_cast<const uint16_t*>(r), sr, static_cast<const uint16_t*>(h), sh,
-                       static_cast<uint16_t*>(xo), sxo, static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy,
-                       rows, n, eps, static_cast<hipStream_t>(stream));
+  RowIn in{static_cast<const uint16_t*>(r), sr, static_cast<const uint16_t*>(h), sh, nullptr, 0, 0, 1,
+           static_cast<uint16_t*>(xo), sxo};
+  launch_rmsnorm<1>(in, static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy, rows, n, eps,
+                    static_cast<hipStream_t>(stream));
+  return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
+}
+
+extern "C" int rspx_add_rmsnorm_partials(const void* r, int64_t sr, const float* hp, int S, const void* w, void* xo,
+                                         int64_t sxo, void* y, int64_t sy, int rows, int n, float eps, void* stream) {
+  int rc = norm_args_ok(rows, n);
+  if (rc != RSPX_OK || rows == 0) return rc;
+  if (S < 1) return RSPX_EINVAL;
+  if (!r || !hp || !w || !xo || !y) return RSPX_EINVAL;
+  if (!al16(r) || !al16(hp) || !al16(w) || !al16(xo) || !al16(y) || sr % 8 || sxo % 8 || sy % 8) return RSPX_EALIGN;
+  RowIn in{static_cast<const uint16_t*>(r), sr, nullptr, 0, hp, n, (int64_t)rows * n, S, static_cast<uint16_t*>(xo),
+           sxo};
+  launch_rmsnorm<2>(in, static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy, rows, n, eps,
+                    static_cast<hipStream_t>(stream));
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }
 
@@ -396,25 +437,47 @@ extern "C" int rspx_qk_norm_rope(const void* q, int64_t sqt, int64_t sqh, const 
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }
 
-extern "C" int rspx_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* wq, const void* wk, const void* cosb,
-                                   const void* sinb, int64_t scs, const int32_t* slots, void* cache_k, int64_t skh,
-                                   int64_t skn, void* cache_v, int64_t svh, int64_t svn, void* qo, int T, int HQ,
-                                   int HK, int D, float eps, void* stream) {
+static int qkv_rope_cache_launch(const uint16_t* qkv, int64_t sqkv, const float* qp, int S, int64_t sps,
+                                 const void* wq, const void* wk, const void* cosb, const void* sinb, int64_t scs,
+                                 const int32_t* slots, void* cache_k, int64_t skh, int64_t skn, void* cache_v,
+                                 int64_t svh, int64_t svn, void* qo, int T, int HQ, int HK, int D, float eps,
+                                 void* stream) {
   if (T < 0 || HQ <= 0 || HK <= 0) return RSPX_EINVAL;
   if (D != 128) return RSPX_EUNSUPPORTED;
   if (T == 0) return RSPX_OK;
-  if (!qkv || !wq || !wk || !cosb || !sinb || !slots || !cache_k || !cache_v || !qo) return RSPX_EINVAL;
-  const void* ps[] = {qkv, wq, wk, cosb, sinb, cache_k, cache_v, qo};
+  if ((!qkv && !qp) || !wq || !wk || !cosb || !sinb || !slots || !cache_k || !cache_v || !qo) return RSPX_EINVAL;
+  const void* ps[] = {wq, wk, cosb, sinb, cache_k, cache_v, qo};
   for (const void* p : ps)
     if (!al16(p)) return RSPX_EALIGN;
+  if ((qkv && !al16(qkv)) || (qp && !al16(qp))) return RSPX_EALIGN;
   if (sqkv % 8 || scs % 8 || skh % 8 || skn % 8 || svh % 8 || svn % 8) return RSPX_EALIGN;
   if (sqkv < (int64_t)(HQ + 2 * HK) * D) return RSPX_EINVAL;
   const int64_t threads = (int64_t)T * (HQ + 2 * HK) * 16;
   hipLaunchKernelGGL(qkv_rope_cache_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(qkv), sqkv,
+                     static_cast<hipStream_t>(stream), qkv, sqkv, qp, S, sps,
                      static_cast<const uint16_t*>(wq), static_cast<const uint16_t*>(wk),
                      static_cast<const uint16_t*>(cosb), static_cast<const uint16_t*>(sinb), scs, slots,
                      static_cast<uint16_t*>(cache_k), skh, skn, static_cast<uint16_t*>(cache_v), svh, svn,
                      static_cast<uint16_t*>(qo), T, HQ, HK, eps);
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
+}
+
+extern "C" int rspx_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* wq, const void* wk, const void* cosb,
+                                   const void* sinb, int64_t scs, const int32_t* slots, void* cache_k, int64_t skh,
+                                   int64_t skn, void* cache_v, int64_t svh, int64_t svn, void* qo, int T, int HQ,
+                                   int HK, int D, float eps, void* stream) {
+  if (!qkv) return RSPX_EINVAL;
+  return qkv_rope_cache_launch(static_cast<const uint16_t*>(qkv), sqkv, nullptr, 1, 0, wq, wk, cosb, sinb, scs, slots,
+                               cache_k, skh, skn, cache_v, svh, svn, qo, T, HQ, HK, D, eps, stream);
+}
+
+extern "C" int rspx_qkv_rope_cache_partials(const float* qkvp, int S, const void* wq, const void* wk,
+                                            const void* cosb, const void* sinb, int64_t scs, const int32_t* slots,
+                                            void* cache_k, int64_t skh, int64_t skn, void* cache_v, int64_t svh,
+                                            int64_t svn, void* qo, int T, int HQ, int HK, int D, float eps,
+                                            void* stream) {
+  if (!qkvp || S < 1) return RSPX_EINVAL;
+  const int64_t n = (int64_t)(HQ + 2 * HK) * D;
+  return qkv_rope_cache_launch(nullptr, n, qkvp, S, (int64_t)T * n, wq, wk, cosb, sinb, scs, slots, cache_k, skh,
+                               skn, cache_v, svh, svn, qo, T, HQ, HK, D, eps, stream);
 }

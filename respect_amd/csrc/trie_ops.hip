@@ -71,24 +71,45 @@ __global__ __launch_bounds__(256) void kv_compact_kernel(const uint64_t* bases, 
 // Greedy token of a row: index of the maximum of the logits with columns
 // [off, off + size) replaced by -inf; NaN counts as the largest value; ties go
 // to the lowest index.  That is a total order on (value, index), so the result
-// does not depend on the reduction order.
+// does not depend on the reduction order (two passes: 4096-logit chunks, then
+// the chunk winners).
 __device__ __forceinline__ bool better(float v, int j, float bv, int bj) {
   const bool vn = v != v, bn = bv != bv;
   if (vn || bn) return vn && (!bn || j < bj);
   return v > bv || (v == bv && j < bj);
 }
 
-__global__ __launch_bounds__(256) void argmax_rows_kernel(const float* logits, int64_t sl, int V, int off, int size,
-                                                          int64_t* out) {
+constexpr int kArgChunk = 4096;  // logits per workgroup of the first pass
+
+// Pass 1, workgroup (row, chunk): the best (value, index) of logits
+// [chunk * 4096, +4096) of the row; 16 per thread from four 16-byte loads
+// issued together.
+__global__ __launch_bounds__(256) void argmax_chunk_kernel(const float* logits, int64_t sl, int V, int off, int size,
+                                                           float* pv, int* pj) {
   __shared__ float sv[4];
   __shared__ int sj[4];
-  const int row = blockIdx.x;
+  const int row = blockIdx.x, c = blockIdx.y, C = gridDim.y;
   const float* lr = logits + (int64_t)row * sl;
   float bv = kNegInf;
   int bj = 0x7fffffff;
-  for (int j = threadIdx.x; j < V; j += 256) {
-    const float v = (j >= off && j < off + size) ? kNegInf : lr[j];
-    if (better(v, j, bv, bj)) { bv = v; bj = j; }
+  f32x4 v4[4];
+  int j0[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    j0[i] = c * kArgChunk + 4 * (threadIdx.x + 256 * i);
+    if (j0[i] + 3 < V) v4[i] = *reinterpret_cast<const f32x4*>(lr + j0[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int j = j0[i] + e;
+      if (j < V) {
+        float v = (j0[i] + 3 < V) ? v4[i][e] : lr[j];
+        if (j >= off && j < off + size) v = kNegInf;
+        if (better(v, j, bv, bj)) { bv = v; bj = j; }
+      }
+    }
   }
   for (int m = 32; m >= 1; m >>= 1) {
     const float ov = __shfl_xor(bv, m);
@@ -101,8 +122,24 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const float* logits, i
   if (threadIdx.x == 0) {
     for (int k = 1; k < 4; ++k)
       if (better(sv[k], sj[k], bv, bj)) { bv = sv[k]; bj = sj[k]; }
-    out[row] = bj == 0x7fffffff ? 0 : bj;
+    pv[row * C + c] = bv;
+    pj[row * C + c] = bj;
   }
+}
+
+// Pass 2, one wave per row: the best of the row's chunk results.
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float* pv, const int* pj, int C, int64_t* out) {
+  const int row = blockIdx.x;
+  float bv = kNegInf;
+  int bj = 0x7fffffff;
+  for (int c = threadIdx.x; c < C; c += 64)
+    if (better(pv[row * C + c], pj[row * C + c], bv, bj)) { bv = pv[row * C + c]; bj = pj[row * C + c]; }
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(bv, m);
+    const int oj = __shfl_xor(bj, m);
+    if (better(ov, oj, bv, bj)) { bv = ov; bj = oj; }
+  }
+  if (threadIdx.x == 0) out[row] = bj == 0x7fffffff ? 0 : bj;
 }
 
 }  // namespace rspx
@@ -132,12 +169,23 @@ extern "C" int rspx_kv_compact(const uint64_t* bases, int n_tensors, int HK, int
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }
 
+extern "C" int64_t rspx_argmax_workspace_bytes(int M, int V) {
+  if (M < 0 || V <= 0) return -1;
+  return (int64_t)M * ((V + kArgChunk - 1) / kArgChunk) * 8;
+}
+
 extern "C" int rspx_argmax_rows(const float* logits, int64_t sl, int M, int V, int off, int size, int64_t* out,
-                                void* stream) {
+                                void* workspace, int64_t workspace_bytes, void* stream) {
   if (M < 0 || V <= 0 || sl < V || off < 0 || size < 0) return RSPX_EINVAL;
   if (M == 0) return RSPX_OK;
   if (!logits || !out) return RSPX_EINVAL;
-  hipLaunchKernelGGL(argmax_rows_kernel, dim3(M), dim3(256), 0, static_cast<hipStream_t>(stream), logits, sl, V, off,
-                     size, out);
+  if ((reinterpret_cast<uintptr_t>(logits) & 15u) || sl % 4) return RSPX_EALIGN;
+  const int C = (V + kArgChunk - 1) / kArgChunk;
+  if (!workspace || workspace_bytes < (int64_t)M * C * 8) return RSPX_EWORKSPACE;
+  float* pv = static_cast<float*>(workspace);
+  int* pj = reinterpret_cast<int*>(pv + (int64_t)M * C);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(argmax_chunk_kernel, dim3(M, C), dim3(256), 0, s, logits, sl, V, off, size, pv, pj);
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(M), dim3(64), 0, s, pv, pj, C, out);
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }

@@ -15,15 +15,21 @@ from .. import _lib
 from ..candidates.trie import Trie
 
 
-def greedy_token(logits: torch.Tensor, offset: int = 0, size: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+def greedy_token(logits: torch.Tensor, offset: int = 0, size: int = 0, out: torch.Tensor | None = None,
+                 workspace: torch.Tensor | None = None) -> torch.Tensor:
     """logits [M, V] fp32 on the GPU -> int64 [M]."""
     if logits.dtype != torch.float32 or not logits.is_cuda or logits.dim() != 2 or logits.stride(1) != 1:
         raise TypeError("greedy_token: fp32 [M, V] GPU logits with contiguous rows are required")
     M, V = logits.shape
+    if logits.stride(0) % 4 or logits.data_ptr() % 16:
+        logits = logits.contiguous().clone()
     if out is None:
         out = torch.empty(M, dtype=torch.int64, device=logits.device)
-    rc = _lib.lib().rspx_argmax_rows(logits.data_ptr(), logits.stride(0), M, V, int(offset), int(size),
-                                     out.data_ptr(), _lib.stream_ptr(logits.device))
+    L = _lib.lib()
+    need = L.rspx_argmax_workspace_bytes(M, V)
+    ws = workspace if workspace is not None else _lib.workspace(logits.device, need, tag="argmax")
+    rc = L.rspx_argmax_rows(logits.data_ptr(), logits.stride(0), M, V, int(offset), int(size),
+                            out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(logits.device))
     _lib.check("rspx_argmax_rows", rc)
     return out
 

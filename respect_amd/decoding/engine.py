@@ -8,13 +8,17 @@ Every arithmetic step goes through librespect_amd:
     x = embed[ids]                                   (row gather)
     y = rmsnorm(x)                                   rspx_rmsnorm
     per layer:
-      qkv = y . Wqkv^T                               rspx_linear
-      q, cache[k, v] at the tokens' slots            rspx_qkv_rope_cache
+      qkv = y . Wqkv^T                               rspx_linear_partials
+      q, cache[k, v] at the tokens' slots            rspx_qkv_rope_cache_partials
       a = attention(q; prompt K/V, node K/V, mask)   rspx_trie_attn
-      h = a . Wo^T                                   rspx_linear
-      x, y = x + h, rmsnorm(x + h)                   rspx_add_rmsnorm
+      h = a . Wo^T                                   rspx_linear_partials
+      x, y = x + h, rmsnorm(x + h)                   rspx_add_rmsnorm_partials
       g|u = y . Wgu^T ; m = silu(g) * u              rspx_linear, rspx_silu_mul
-      h = m . Wd^T ; x, y = x + h, rmsnorm(x + h)    rspx_linear, rspx_add_rmsnorm
+      h = m . Wd^T ; x, y = x + h, rmsnorm(x + h)    rspx_linear_partials, rspx_add_rmsnorm_partials
+
+A projection feeding an epilogue is left as its fp32 K-chunk partials and
+the epilogue adds them in chunk order and rounds to bf16 -- the exact value
+rspx_linear would store -- so no separate reduction launch is needed.
     logits = y . Wlm^T (fp32)                        rspx_linear
 
 Each kernel computes a row with arithmetic that does not depend on how many
@@ -91,6 +95,39 @@ class Decoder:
         self.final_norm = (1.0 + torch.randn(cfg.hidden, generator=g, device=self.device) * std).to(torch.bfloat16)
         self.lm_head = (torch.randn(cfg.vocab, cfg.hidden, generator=g, device=self.device) * std).to(torch.bfloat16)
         self.sm_scale = cfg.head_dim ** -0.5
+        self._ws = {}
+        self._ws_retired = []   # outgrown buffers: a captured graph may still point at them
+        self._graphs = {}
+
+    def _workspace(self, name: str, nbytes: int) -> torch.Tensor:
+        """Scratch owned by the model, grown (never while a graph is being
+        captured) so that captured kernels keep pointing at live memory."""
+        ws = self._ws.get(name)
+        if ws is None or ws.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("decoder workspace must be sized before graph capture")
+            if ws is not None:
+                self._ws_retired.append(ws)
+            ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+            self._ws[name] = ws
+        return ws
+
+    def _linear(self, x, w, out_dtype=None):
+        L = _lib.lib()
+        need = L.rspx_linear_workspace_bytes(x.shape[0], w.shape[0], w.shape[1])
+        return linear(x, w, out_dtype=out_dtype, workspace=self._workspace("linear", need))
+
+    def _partials(self, x, w) -> tuple[int, int]:
+        """x . w^T left as fp32 chunk partials in the model's partial buffer;
+        returns (pointer, chunk count) for a consumer that sums them."""
+        L = _lib.lib()
+        M, K = x.shape
+        N = w.shape[0]
+        S = L.rspx_linear_splits(N, K)
+        buf = self._workspace("partials", S * M * N * 4)
+        _lib.check("rspx_linear_partials", L.rspx_linear_partials(
+            x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), buf.data_ptr(), M, N, K, _lib.stream_ptr(self.device)))
+        return buf.data_ptr(), S
 
     # ------------------------------------------------------------------ forward
     @torch.no_grad()
@@ -119,29 +156,30 @@ class Decoder:
         qo = torch.empty((T, HQ, D), dtype=bf, device=dev)
         att = torch.empty((T, HQ, D), dtype=bf, device=dev)
         mlp = torch.empty((T, cfg.ffn), dtype=bf, device=dev)
+        ws_attn = self._workspace("attn", L.rspx_trie_attn_workspace_bytes(HQ, HK, T, P, D))
         for li, lay in enumerate(self.layers):
             ck, cv = cache.k[li], cache.v[li]
-            qkv = linear(y, lay.wqkv)
-            _lib.check("rspx_qkv_rope_cache", L.rspx_qkv_rope_cache(
-                qkv.data_ptr(), qkv.stride(0), lay.q_norm.data_ptr(), lay.k_norm.data_ptr(), cos.data_ptr(),
+            qkvp, S = self._partials(y, lay.wqkv)
+            _lib.check("rspx_qkv_rope_cache_partials", L.rspx_qkv_rope_cache_partials(
+                qkvp, S, lay.q_norm.data_ptr(), lay.k_norm.data_ptr(), cos.data_ptr(),
                 sin.data_ptr(), cos.stride(0), slots32.data_ptr(), ck.data_ptr(), ck.stride(0), ck.stride(1),
                 cv.data_ptr(), cv.stride(0), cv.stride(1), qo.data_ptr(), T, HQ, HK, D, cfg.eps, s))
             trie_attn(qo.permute(1, 0, 2), ck[:, :P], cv[:, :P], ck[:, P:P + NN], cv[:, P:P + NN], msk,
-                      self.sm_scale, out=att.permute(1, 0, 2))
-            h = linear(att.view(T, HQ * D), lay.wo)
-            _lib.check("rspx_add_rmsnorm", L.rspx_add_rmsnorm(
-                x.data_ptr(), Hd, h.data_ptr(), Hd, lay.post_norm.data_ptr(), x.data_ptr(), Hd, y.data_ptr(), Hd,
+                      self.sm_scale, out=att.permute(1, 0, 2), workspace=ws_attn)
+            hp, S = self._partials(att.view(T, HQ * D), lay.wo)
+            _lib.check("rspx_add_rmsnorm_partials", L.rspx_add_rmsnorm_partials(
+                x.data_ptr(), Hd, hp, S, lay.post_norm.data_ptr(), x.data_ptr(), Hd, y.data_ptr(), Hd,
                 T, Hd, cfg.eps, s))
-            gu = linear(y, lay.wgu)
+            gu = self._linear(y, lay.wgu)
             F = cfg.ffn
             _lib.check("rspx_silu_mul", L.rspx_silu_mul(gu.data_ptr(), gu.stride(0), gu.data_ptr() + 2 * F,
                                                         gu.stride(0), mlp.data_ptr(), F, T, F, s))
-            h = linear(mlp, lay.wd)
+            hp, S = self._partials(mlp, lay.wd)
             nxt = self.layers[li + 1].in_norm if li + 1 < len(self.layers) else self.final_norm
-            _lib.check("rspx_add_rmsnorm", L.rspx_add_rmsnorm(
-                x.data_ptr(), Hd, h.data_ptr(), Hd, nxt.data_ptr(), x.data_ptr(), Hd, y.data_ptr(), Hd,
+            _lib.check("rspx_add_rmsnorm_partials", L.rspx_add_rmsnorm_partials(
+                x.data_ptr(), Hd, hp, S, nxt.data_ptr(), x.data_ptr(), Hd, y.data_ptr(), Hd,
                 T, Hd, cfg.eps, s))
-        return linear(y, self.lm_head, out_dtype=torch.float32)
+        return self._linear(y, self.lm_head, out_dtype=torch.float32)
 
     # ------------------------------------------------------------------ prompt
     @torch.no_grad()
@@ -160,3 +198,57 @@ class Decoder:
             pos = torch.arange(c0, c1, device=dev)
             logits = self.forward(ids[c0:c1], pos.to(torch.int32), pos, cache, c0, msk, NN)
         return logits[-1:]
+
+    # ------------------------------------------------------------------ graphs
+    def graphed(self, cache, P: int, T: int, NN: int) -> "GraphedForward":
+        """A captured forward for T rows, prompt P and node segment NN (cached)."""
+        key = (id(cache), P, T, NN)
+        g = self._graphs.get(key)
+        if g is None:
+            g = GraphedForward(self, cache, P, T, NN)
+            self._graphs[key] = g
+        return g
+
+
+class GraphedForward:
+    """Decoder.forward captured once in a HIP graph for fixed (T, P, NN) and
+    replayed with new inputs copied into its static buffers.  Padding rows
+    (fewer real rows than T) write their K/V to the last T slots of the cache,
+    which no call reads, and attend to node slot 0 only."""
+
+    def __init__(self, model: Decoder, cache, P: int, T: int, NN: int):
+        dev = model.device
+        if P + NN > cache.cap - T:
+            raise ValueError("KV cache has no room for the graph's scratch slots")
+        self.T, self.NN = T, NN
+        self.scratch = cache.cap - T
+        self.ids = torch.zeros(T, dtype=torch.int64, device=dev)
+        self.slots = torch.arange(self.scratch, self.scratch + T, dtype=torch.int32, device=dev)
+        self.pos = torch.zeros(T, dtype=torch.int64, device=dev)
+        self.msk = torch.zeros(T, NN, dtype=torch.uint8, device=dev)
+        self.msk[:, 0] = 1
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):  # sizes the workspaces and the allocator pools
+            model.forward(self.ids, self.slots, self.pos, cache, P, self.msk, NN)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize(dev)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = model.forward(self.ids, self.slots, self.pos, cache, P, self.msk, NN)
+
+    def __call__(self, n: int, ids=None, slots=None, pos=None, msk=None) -> torch.Tensor:
+        """Run with the first ``n`` rows given (device tensors; ``msk`` may also be
+        left in place after writing ``self.msk`` directly).  Returns logits [T, V]."""
+        if ids is not None:
+            self.ids[:n].copy_(ids)
+        if slots is not None:
+            self.slots[:n].copy_(slots)
+            self.slots[n:] = torch.arange(self.scratch + n, self.scratch + self.T, dtype=torch.int32,
+                                          device=self.slots.device)
+        if pos is not None:
+            self.pos[:n].copy_(pos)
+        if msk is not None:
+            self.msk.copy_(msk)
+        self.graph.replay()
+        return self.logits

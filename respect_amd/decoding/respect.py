@@ -12,10 +12,10 @@ from .verify import verify_trie
 
 @torch.no_grad()
 def respect_step(model, cache, tree: Trie, first: int, P: int, base: int, eos: int, offset: int = 0,
-                 size: int = 0, cap: int = 1 << 30) -> tuple[list[int], int, list[int]]:
+                 size: int = 0, cap: int = 1 << 30, graph: bool = False) -> tuple[list[int], int, list[int]]:
     """Returns (accepted tokens, correction token, node path).  The accepted
     tokens' KV ends up in slots P + base .. P + base + len - 1."""
-    logits = verify_trie(model, cache, tree, P, base)
+    logits = verify_trie(model, cache, tree, P, base, graph=graph)
     picks = greedy_token(logits, offset, size).tolist()
     path, acc, rec = walk(tree, first, cap, eos, lambda a, ch: picks[ch])
     cache.compact(P + base, path)

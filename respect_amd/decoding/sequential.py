@@ -9,14 +9,21 @@ from .verify import node_slots
 
 
 @torch.no_grad()
-def forward_token(model, cache, token: int, P: int, c: int) -> torch.Tensor:
+def forward_token(model, cache, token: int, P: int, c: int, graph: bool = False) -> torch.Tensor:
     """Feed ``token`` at node-segment index ``c`` (cache slot P + c, position
-    P + c); it sees the prompt and node slots [0, c].  Returns fp32 logits [1, V]."""
+    P + c); it sees the prompt and node slots [0, c].  Returns fp32 logits [1, V].
+    ``graph``: replay a captured forward (node segment padded to 64)."""
     dev = model.device
+    slot = torch.tensor([P + c], dtype=torch.int32, device=dev)
+    ids = torch.tensor([token], device=dev)
+    if graph:
+        NN = node_slots(c, 1, 64)
+        gf = model.graphed(cache, P, 1, NN)
+        gf.msk[0].copy_(torch.arange(NN, device=dev) <= c)
+        return gf(1, ids, slot, slot.to(torch.int64))
     NN = node_slots(c, 1)
     msk = (torch.arange(NN, device=dev) <= c).to(torch.uint8)[None]
-    slot = torch.tensor([P + c], dtype=torch.int32, device=dev)
-    return model.forward(torch.tensor([token], device=dev), slot, slot.to(torch.int64), cache, P, msk, NN)
+    return model.forward(ids, slot, slot.to(torch.int64), cache, P, msk, NN)
 
 
 @torch.no_grad()

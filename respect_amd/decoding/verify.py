@@ -14,33 +14,43 @@ from .. import _lib
 from ..candidates.trie import Trie
 
 
-def node_slots(base: int, n: int) -> int:
-    """Node-segment width of a call: committed + trie slots, padded to 32."""
-    return max(32, -(-(base + n) // 32) * 32)
+def node_slots(base: int, n: int, step: int = 32) -> int:
+    """Node-segment width of a call: committed + trie slots, padded to ``step``."""
+    return max(step, -(-(base + n) // step) * step)
 
 
-def trie_mask(tree: Trie, base: int, NN: int, device) -> tuple[torch.Tensor, torch.Tensor]:
-    """(msk [N, NN] uint8, depth [N] int32) on the GPU."""
+def trie_mask(tree: Trie, base: int, NN: int, device, rows: int | None = None,
+              out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(msk [rows, NN] uint8, depth [N] int32) on the GPU; rows past N open slot 0 only."""
     N = len(tree.nodes)
+    rows = N if rows is None else rows
     parent = torch.from_numpy(tree.parents).to(device)
-    msk = torch.empty((N, NN), dtype=torch.uint8, device=device)
+    msk = out if out is not None else torch.empty((rows, NN), dtype=torch.uint8, device=device)
     depth = torch.empty(N, dtype=torch.int32, device=device)
-    rc = _lib.lib().rspx_trie_mask(parent.data_ptr(), N, base, N, NN, msk.data_ptr(), NN, depth.data_ptr(),
-                                   _lib.stream_ptr(torch.device(device)))
+    rc = _lib.lib().rspx_trie_mask(parent.data_ptr(), N, base, rows, NN, msk.data_ptr(), msk.stride(0),
+                                   depth.data_ptr(), _lib.stream_ptr(torch.device(device)))
     _lib.check("rspx_trie_mask", rc)
     return msk, depth
 
 
 @torch.no_grad()
-def verify_trie(model, cache, tree: Trie, P: int, base: int) -> torch.Tensor:
-    """fp32 logits [N, V] of every trie node."""
+def verify_trie(model, cache, tree: Trie, P: int, base: int, graph: bool = False) -> torch.Tensor:
+    """fp32 logits [N, V] of every trie node.  ``graph``: replay a captured
+    forward (rows padded to a multiple of 64, node segment to a multiple of 64);
+    the node segment width never changes a row's result."""
     dev = model.device
     N = len(tree.nodes)
+    ids = torch.from_numpy(tree.tokens).to(dev)
+    start = P + base
+    slots = torch.arange(start, start + N, dtype=torch.int32, device=dev)
+    if graph:
+        T = max(64, -(-N // 64) * 64)
+        NN = node_slots(base, N, 64)
+        gf = model.graphed(cache, P, T, NN)
+        _, depth = trie_mask(tree, base, NN, dev, rows=T, out=gf.msk)
+        return gf(N, ids, slots, depth.to(torch.int64) + start)[:N]
     NN = node_slots(base, N)
     if P + NN > cache.cap:
         raise ValueError("KV cache too small for the trie")
     msk, depth = trie_mask(tree, base, NN, dev)
-    ids = torch.from_numpy(tree.tokens).to(dev)
-    start = P + base
-    slots = torch.arange(start, start + N, dtype=torch.int32, device=dev)
     return model.forward(ids, slots, depth.to(torch.int64) + start, cache, P, msk, NN)

@@ -21,9 +21,11 @@ from .. import _lib
 from ._tensor import as_kernel_input
 
 
-def trie_attn(q, kp, vp, kn, vn, msk, sm_scale=None, out=None, rows_per_wave: int = 0):
-    """Launch the kernel on the current stream.  ``rows_per_wave`` (0/1/2/4) only
-    changes the work split, never the result."""
+def trie_attn(q, kp, vp, kn, vn, msk, sm_scale=None, out=None, rows_per_wave: int = 0, workspace=None):
+    """Launch the kernel on the current stream.  ``rows_per_wave`` (0/1/2) only
+    changes the work split, never the result.  ``workspace``: a uint8 GPU tensor
+    of at least rspx_trie_attn_workspace_bytes bytes (default: a per-stream
+    scratch buffer)."""
     H, M, D = q.shape
     HK, P, D2 = kp.shape
     NN = kn.shape[1]
@@ -49,7 +51,9 @@ def trie_attn(q, kp, vp, kn, vn, msk, sm_scale=None, out=None, rows_per_wave: in
     need = L.rspx_trie_attn_workspace_bytes(H, HK, M, P, D)
     if need < 0:
         _lib.check("rspx_trie_attn_workspace_bytes", -2)
-    ws = _lib.workspace(dev, need)
+    ws = workspace if workspace is not None else _lib.workspace(dev, need)
+    if ws.numel() < need:
+        raise ValueError("fused_attn_hyb: workspace too small")
     rc = L.rspx_trie_attn(
         q.data_ptr(), q.stride(0), q.stride(1),
         kp.data_ptr(), kp.stride(0), kp.stride(1),

@@ -15,8 +15,9 @@ from .. import _lib
 from ._tensor import as_kernel_input
 
 
-def linear(x, w, BM=32, BN=128, BK=64, num_warps=4, num_stages=2, out_dtype=None, out=None):
-    """x (M, K) @ w (N, K)^T -> (M, N). Bias is handled by the caller."""
+def linear(x, w, BM=32, BN=128, BK=64, num_warps=4, num_stages=2, out_dtype=None, out=None, workspace=None):
+    """x (M, K) @ w (N, K)^T -> (M, N). Bias is handled by the caller.  ``workspace``:
+    optional uint8 GPU tensor of at least rspx_linear_workspace_bytes bytes."""
     if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
         raise TypeError("linear: bf16 x and w are required")
     out_dtype = out_dtype or x.dtype
@@ -35,7 +36,9 @@ def linear(x, w, BM=32, BN=128, BK=64, num_warps=4, num_stages=2, out_dtype=None
     need = L.rspx_linear_workspace_bytes(M, N, K)
     if need < 0:
         _lib.check("rspx_linear_workspace_bytes", -2)
-    ws = _lib.workspace(x.device, max(need, 16), tag="linear")
+    ws = workspace if workspace is not None else _lib.workspace(x.device, max(need, 16), tag="linear")
+    if ws.numel() < need:
+        raise ValueError("linear: workspace too small")
     rc = L.rspx_linear(xs.data_ptr(), xs.stride(0), w2.data_ptr(), w2.stride(0), out.data_ptr(), out.stride(0),
                        M, N, K, 1 if out_dtype == torch.float32 else 0, ws.data_ptr(), ws.numel(),
                        _lib.stream_ptr(x.device))

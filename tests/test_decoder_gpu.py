@@ -40,7 +40,7 @@ def _trie(seq, rng, n_other=3, vocab=4096, length=24):
     from respect_amd.candidates.trie import build_trie
     seqs = [list(seq[:length])]
     for _ in range(n_other):
-        p = int(rng.integers(1, 17))
+        p = int(rng.integers(1, min(17, length)))
         seqs.append(list(seq[:p]) + [int(t) for t in rng.integers(0, vocab, length - p)])
     return build_trie(seqs)
 
@@ -155,3 +155,27 @@ def test_kv_compact_overlapping_moves():
         exp = b.clone()
         exp[:, 10:15] = b[:, [10 + s for s in path]]
         assert torch.equal(t, exp)
+
+
+def test_graph_replays_equal_eager(model):
+    """Captured forwards (HIP graphs) give the eager bits on every replay, with
+    eager work and synchronisations between replays, for tries of different
+    sizes and offsets and for 1-token calls."""
+    from respect_amd.decoding.acceptance import greedy_token
+    from respect_amd.decoding.sequential import forward_token
+    from respect_amd.decoding.verify import verify_trie
+    cache, last = _filled_cache(model)
+    t0 = int(greedy_token(last).item())
+    rng = np.random.default_rng(1)
+    for rep, base in enumerate((0, 5, 40, 5)):
+        seq = [t0] + [int(t) for t in rng.integers(0, 4096, 30)]
+        tree = _trie(seq, rng) if rep % 2 == 0 else _trie(seq, rng, n_other=1, length=10)
+        eager = verify_trie(model, cache, tree, P, base).clone()
+        torch.cuda.synchronize()
+        graphed = verify_trie(model, cache, tree, P, base, graph=True).clone()
+        torch.cuda.synchronize()
+        print(f"[graph] rep {rep} base {base} nodes {len(tree.nodes)}", flush=True)
+        assert torch.equal(eager, graphed)
+        e1 = forward_token(model, cache, seq[1], P, base).clone()
+        g1 = forward_token(model, cache, seq[1], P, base, graph=True).clone()
+        assert torch.equal(e1, g1)

@@ -88,3 +88,60 @@ def test_linear_strided_and_errors():
                torch.zeros(16, 100, device="cuda", dtype=torch.bfloat16))
     with pytest.raises(TypeError):
         linear(xd.float(), wd)
+
+
+def test_partials_consumers_equal_linear_then_op():
+    """rspx_linear_partials + a consumer that sums the chunks gives the bits of
+    rspx_linear followed by the plain op (residual add + RMSNorm, q/k/v epilogue)."""
+    from respect_amd import _lib
+    from respect_amd.kernels.gemm import linear
+    L = _lib.lib()
+    s = _lib.stream_ptr(torch.device("cuda"))
+    torch.manual_seed(3)
+    T, H = 7, 4096
+    for K in (4096, 12288):
+        x = torch.randn(T, K, device="cuda").to(torch.bfloat16)
+        w = (0.02 * torch.randn(H, K, device="cuda")).to(torch.bfloat16)
+        r = torch.randn(T, H, device="cuda").to(torch.bfloat16)
+        nw = (1 + 0.02 * torch.randn(H, device="cuda")).to(torch.bfloat16)
+        S = L.rspx_linear_splits(H, K)
+        part = torch.empty(S * T * H, device="cuda", dtype=torch.float32)
+        assert L.rspx_linear_partials(x.data_ptr(), K, w.data_ptr(), K, part.data_ptr(), T, H, K, s) == 0
+        h = linear(x, w)
+        xo1, y1 = torch.empty_like(r), torch.empty_like(r)
+        xo2, y2 = torch.empty_like(r), torch.empty_like(r)
+        assert L.rspx_add_rmsnorm(r.data_ptr(), H, h.data_ptr(), H, nw.data_ptr(), xo1.data_ptr(), H, y1.data_ptr(), H,
+                                  T, H, 1e-6, s) == 0
+        assert L.rspx_add_rmsnorm_partials(r.data_ptr(), H, part.data_ptr(), S, nw.data_ptr(), xo2.data_ptr(), H,
+                                           y2.data_ptr(), H, T, H, 1e-6, s) == 0
+        assert torch.equal(xo1, xo2) and torch.equal(y1, y2)
+        assert torch.equal(xo1, (r.float() + h.float()).to(torch.bfloat16))
+    # q/k/v epilogue
+    HQ, HK, D, P = 4, 2, 128, 16
+    n = (HQ + 2 * HK) * D
+    x = torch.randn(T, 512, device="cuda").to(torch.bfloat16)
+    w = (0.05 * torch.randn(n, 512, device="cuda")).to(torch.bfloat16)
+    S = L.rspx_linear_splits(n, 512)
+    part = torch.empty(S * T * n, device="cuda", dtype=torch.float32)
+    assert L.rspx_linear_partials(x.data_ptr(), 512, w.data_ptr(), 512, part.data_ptr(), T, n, 512, s) == 0
+    qkv = linear(x, w)
+    wq = (1 + 0.02 * torch.randn(D, device="cuda")).to(torch.bfloat16)
+    wk = (1 + 0.02 * torch.randn(D, device="cuda")).to(torch.bfloat16)
+    from respect_amd.system.fused import rope_tables
+    cos, sin = rope_tables(torch.arange(T, device="cuda") + 100, D, 1e6, device="cuda")
+    slots = torch.arange(3, 3 + T, dtype=torch.int32, device="cuda")
+    outs = []
+    for use_part in (False, True):
+        ck = torch.zeros(HK, P, D, device="cuda", dtype=torch.bfloat16)
+        cv = torch.zeros_like(ck)
+        qo = torch.empty(T, HQ, D, device="cuda", dtype=torch.bfloat16)
+        common = (wq.data_ptr(), wk.data_ptr(), cos.data_ptr(), sin.data_ptr(), D, slots.data_ptr(), ck.data_ptr(),
+                  P * D, D, cv.data_ptr(), P * D, D, qo.data_ptr(), T, HQ, HK, D, 1e-6, s)
+        if use_part:
+            assert L.rspx_qkv_rope_cache_partials(part.data_ptr(), S, *common) == 0
+        else:
+            assert L.rspx_qkv_rope_cache(qkv.data_ptr(), n, *common) == 0
+        outs.append((qo, ck, cv))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    assert torch.equal(outs[0][2][:, 3:3 + T].transpose(0, 1), qkv[:, (HQ + HK) * D:].view(T, HK, D))
