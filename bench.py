@@ -119,7 +119,7 @@ def bench_attn(args) -> dict:
                    "algorithmic_bytes_per_call": nbytes, "flops_per_call": wl.flops()},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "rspx::prompt_kernel<128,2> + rspx::node_merge_kernel<128> (one call)"},
+                     "kernel": "rspx::fused_kernel<128,2> (one launch per call)"},
     }
     if not args.no_cpu:
         _log("timing CPU baseline (oracle)")
@@ -127,7 +127,9 @@ def bench_attn(args) -> dict:
     return res
 
 
-ATTN_KERNELS = ("rspx::prompt_kernel", "rspx::node_merge_kernel")
+# One call is one fused_kernel launch when its grid fits on the device at once,
+# else prompt_kernel then node_merge_kernel.
+ATTN_KERNELS = ("rspx::fused_kernel", "rspx::prompt_kernel", "rspx::node_merge_kernel")
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 PROBE_COPY_BYTES = 1 << 28   # the probe's device copy: 256 MiB read + 256 MiB written
 
@@ -194,7 +196,8 @@ def measure_traffic(timeout_s: float = 180.0):
                 for k in ATTN_KERNELS:
                     if k in name:
                         per_kernel.setdefault(k, {})[counter] = statistics.median(v) * 1024 * scale[counter]
-    if any(len(per_kernel.get(k, {})) != 2 for k in ATTN_KERNELS):
+    per_kernel = {k: v for k, v in per_kernel.items() if len(v) == 2}
+    if not per_kernel:
         return None
     total = sum(v["FETCH_SIZE"] + v["WRITE_SIZE"] for v in per_kernel.values())
     return {"bytes": total, "scale": scale,
@@ -430,6 +433,7 @@ def main() -> int:
     res = bench_attn(args)
     if traffic is not None:
         res["roofline"]["traffic"] = round(traffic["bytes"])
+        res["roofline"]["kernel"] = " + ".join(f"{k}<128,...>" for k in traffic["by_kernel"]) + " (one call)"
         res["roofline"]["traffic_detail"] = {
             "source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per dispatch, scaled by a 256 MiB device copy",
             "scale": {k: round(v, 4) for k, v in traffic["scale"].items()}, "by_kernel": traffic["by_kernel"]}

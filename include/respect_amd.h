@@ -69,10 +69,18 @@ const char* rspx_version(void);
  * [0, NN), on masked slots, or on the other rows.
  *
  * workspace: device memory of at least rspx_trie_attn_workspace_bytes(...)
- * bytes (16-byte aligned, contents irrelevant) that holds the per-group
- * partial results between the two kernels of a call.  A workspace must not be
- * used by two calls that can run at the same time (different streams).
+ * bytes, 16-byte aligned and zero-filled before its first use; every call
+ * leaves its synchronisation words (the first 16 KiB, at the same place for
+ * every shape) at zero again, so calls of any shapes may share one workspace
+ * in turn.  It holds those words (per-row-block counters of the one-launch
+ * path) and the per-group partial results.  A workspace must not be used by
+ * two calls that can run at the same time.
  * NN <= 4096 (the node-slot limit of the reference dispatcher, NMAX).
+ *
+ * Launches: one (prompt groups, node fold and merge in one kernel whose
+ * workgroups wait for each other; used when the grid fits on the device at
+ * once) or two (prompt groups, then node fold and merge).  Both give the
+ * same bits.
  *
  * rows_per_wave: 0 = automatic, else 1 or 2 (16-row tiles per wave).  It
  * changes only the work distribution, never the result.
@@ -90,6 +98,23 @@ int rspx_trie_attn(const void* q, int64_t sqh, int64_t sqm,
                    int H, int HK, int M, int P, int NN, int D, float sm_scale,
                    void* workspace, int64_t workspace_bytes, int rows_per_wave,
                    void* stream);
+
+/* rspx_trie_attn with the launch count forced: launches = 1 (the one-kernel
+ * path; falls back to two when the grid does not fit) or 2.  For tests and
+ * measurements; the result is the same either way.
+ */
+int rspx_trie_attn_launches(const void* q, int64_t sqh, int64_t sqm, const void* kp, int64_t skph, int64_t skpn,
+                            const void* vp, int64_t svph, int64_t svpn, const void* kn, int64_t sknh, int64_t sknn,
+                            const void* vn, int64_t svnh, int64_t svnn, const uint8_t* msk, int64_t smm, int64_t smn,
+                            void* out, int64_t soh, int64_t som, int H, int HK, int M, int P, int NN, int D,
+                            float sm_scale, void* workspace, int64_t workspace_bytes, int rows_per_wave, int launches,
+                            void* stream);
+
+/* 1 if a one-launch call on this workspace ever ran out of its bounded wait
+ * (its results are then not valid), 0 if not, < 0 on error.  Synchronises the
+ * stream.
+ */
+int rspx_trie_attn_status(const void* workspace, int H, int HK, int M, int P, int D, void* stream);
 
 /* ---------------------------------------------------------------- RMSNorm
  * y[r] = bf16(w * bf16(x[r] * rsqrt(mean(x[r]^2) + eps))), fp32 statistics

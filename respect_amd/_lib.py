@@ -36,6 +36,11 @@ SIGNATURES: dict[str, tuple] = {
         _c_p, _i64, _i32,          # workspace, bytes, rows_per_wave
         _c_p,                      # stream
     ]),
+    "rspx_trie_attn_launches": (_i32, [
+        _c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _i64, _i64,
+        _c_p, _i64, _i64, _c_p, _i64, _i64,
+        _i32, _i32, _i32, _i32, _i32, _i32, _f32, _c_p, _i64, _i32, _i32, _c_p]),
+    "rspx_trie_attn_status": (_i32, [_c_p, _i32, _i32, _i32, _i32, _i32, _c_p]),
     "rspx_rmsnorm": (_i32, [_c_p, _i64, _c_p, _c_p, _i64, _i32, _i32, _f32, _c_p]),
     "rspx_rope": (_i32, [_c_p, _i64, _i64, _i64, _c_p, _c_p, _i64, _i64, _c_p, _i32, _i32, _i32, _i32, _c_p]),
     "rspx_qk_norm_rope": (_i32, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _c_p,
@@ -111,6 +116,6 @@ def workspace(device: torch.device, nbytes: int, tag: str = "attn") -> torch.Ten
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         size = max(nbytes, 256, 0 if ws is None else 2 * ws.numel())
-        ws = torch.empty(size, dtype=torch.uint8, device=device)
+        ws = torch.zeros(size, dtype=torch.uint8, device=device)  # the attention's sync words start at zero
         _WORKSPACES[key] = ws
     return ws

@@ -76,6 +76,7 @@ struct TrieAttnArgs {
   float c;            // sm_scale * log2(e)
   float* gp_ml;       // [HK][R][NG][2]  group partial (m, l)
   float* gp_acc;      // [HK][R][NG][D]
+  int* sync;          // fused launch: a timeout flag, then [HK][NRB][2] counters
 };
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -151,6 +152,16 @@ struct StepGeom {
   static constexpr int RING = D == 128 ? 2 : 4;  // rounds in flight
   static constexpr int OWN = kQuarters * CH / kWavesA;  // chunks one wave issues per round
 };
+
+// K rows in LDS: 16-byte unit u of key row `key` holds the row's unit
+// u ^ kswz(key), so the 16 lanes of an MFMA A-fragment read (keys n16 of a
+// 16-key block, one 16-byte unit each) fall on 16 different bank groups, while
+// each direct-to-LDS load still copies whole rows (KPV of them, 1 KB).
+template <int D>
+__device__ __forceinline__ int kswz(int key) {
+  constexpr int U = D / 8;
+  return (key / (16 / U)) % U;
+}
 
 template <int D>
 __device__ __forceinline__ int vswz(int key) {
@@ -290,25 +301,91 @@ __device__ __forceinline__ void issue_round(const uint16_t* kpg, const uint16_t*
 // Workgroup (g, rb, q): kv head g, rows [32 kRT rb, +32 kRT), key group q =
 // steps [q S, q S + S).  Wave w: row half h = w / 4 (kRT tiles of 16 rows),
 // key quarter k = w % 4 (steps 4 i + k of the group).
+// Quarter partials in LDS: region i holds acc[t][j] as [t][j][lane] f32x4
+// (ring) and (m, l) of rows 16 t + n16 (Q area).
 template <int D, int kRT>
-__global__ __launch_bounds__(512) void prompt_kernel(TrieAttnArgs A) {
+__device__ __forceinline__ void quarter_put(lds_char* ring, lds_char* qreg, int region,
+                                            const f32x4 (&acc)[kRT][D / 16], const float (&mref)[kRT],
+                                            const float (&lrow)[kRT], int lane) {
+  constexpr int DT = D / 16, REG = kRT * DT * 1024, REGML = kRT * 16 * 8;
+  const int n16 = lane & 15, g4 = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < kRT; ++t) {
+#pragma unroll
+    for (int j = 0; j < DT; ++j)
+      *(__attribute__((address_space(3))) f32x4*)(ring + region * REG + (t * DT + j) * 1024 + 16 * lane) = acc[t][j];
+    if (g4 == 0) {
+      __attribute__((address_space(3))) float* ml =
+          (__attribute__((address_space(3))) float*)(qreg + region * REGML) + 2 * (16 * t + n16);
+      ml[0] = mref[t];
+      ml[1] = lrow[t];
+    }
+  }
+}
+
+// state (mref, lrow, acc) <- state (+) the partial in `region`: combine() per
+// row, the row factors moved from the score layout (row n16) to the
+// accumulator layout (rows 4 g4 + e) by a lane shuffle.
+template <int D, int kRT>
+__device__ __forceinline__ void quarter_take(const lds_char* ring, const lds_char* qreg, int region,
+                                             f32x4 (&acc)[kRT][D / 16], float (&mref)[kRT], float (&lrow)[kRT],
+                                             int lane) {
+  constexpr int DT = D / 16, REG = kRT * DT * 1024, REGML = kRT * 16 * 8;
+  const int n16 = lane & 15, g4 = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < kRT; ++t) {
+    const __attribute__((address_space(3))) float* ml =
+        (const __attribute__((address_space(3))) float*)(qreg + region * REGML) + 2 * (16 * t + n16);
+    const float m2 = ml[0], l2 = ml[1];
+    float a = 1.f, b = 0.f;
+    if (m2 != kNegInf) {
+      const float mn = fmaxf(mref[t], m2);
+      a = fexp2(mref[t] - mn);
+      b = fexp2(m2 - mn);
+      lrow[t] = __builtin_fmaf(l2, b, lrow[t] * a);
+      mref[t] = mn;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float ae = shfl_idx(a, 4 * g4 + e), be = shfl_idx(b, 4 * g4 + e);
+#pragma unroll
+      for (int j = 0; j < DT; ++j) {
+        const f32x4 a2 =
+            *(const __attribute__((address_space(3))) f32x4*)(ring + region * REG + (t * DT + j) * 1024 + 16 * lane);
+        acc[t][j][e] = __builtin_fmaf(a2[e], be, acc[t][j][e] * ae);
+      }
+    }
+  }
+}
+
+template <int D, int kRT>
+struct PromptLds {
   using G = StepGeom<D>;
+  static constexpr int QBYTES = 2 * kRT * G::DQ * 1024;
+  static constexpr int RINGBYTES = G::RING * G::ROUND;
+  static constexpr int BYTES = RINGBYTES + QBYTES;
+  static_assert(4 * kRT * G::DT * 1024 <= RINGBYTES / 2, "quarter accumulators use half the ring");
+  static_assert(4 * kRT * 16 * 8 <= QBYTES, "quarter (m, l) reuse the Q area");
+  static_assert(32 * kRT * (D + 4) * 4 <= RINGBYTES / 2, "the staged group partial uses the other half");
+  static_assert(BYTES <= 160 * 1024, "LDS budget");
+};
+
+// The prompt work of workgroup (g, rb, q) -- kv head g, rows [32 kRT rb,
+// +32 kRT), key group q = steps [q S, q S + S) -- up to its group partial in
+// memory.  Wave w: row half h = w / 4 (kRT tiles of 16 rows), key quarter
+// k = w % 4 (steps 4 i + k of the group).  ATOMIC: the partial is stored with
+// agent-scope atomic stores (write-through) for a merge inside the same launch.
+template <int D, int kRT, bool ATOMIC>
+__device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, int g, int rb, int q) {
+  using G = StepGeom<D>;
+  using L = PromptLds<D, kRT>;
   constexpr int DQ = G::DQ, DT = G::DT;
-  constexpr int QBYTES = 2 * kRT * DQ * 1024;
-  constexpr int RINGBYTES = G::RING * G::ROUND;
-  static_assert(kWavesA * kRT * DT * 1024 <= RINGBYTES, "quarter accumulators reuse the ring");
-  static_assert(kWavesA * kRT * 16 * 8 <= QBYTES, "quarter (m, l) reuse the Q area");
-  static_assert(RINGBYTES + QBYTES <= 160 * 1024, "LDS budget");
-  __shared__ __attribute__((aligned(16))) char lds[RINGBYTES + QBYTES];
+  constexpr int RINGBYTES = L::RINGBYTES;
 
   const int lane = __lane_id();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int h = w >> 2, k = w & 3;
   const int n16 = lane & 15, g4 = lane >> 4;
-  const int g = blockIdx.x % A.HK;
-  const int rest = blockIdx.x / A.HK;
-  const int rb = rest % A.NRB;
-  const int q = rest / A.NRB;
   const int P = A.P;
   const int steps = (P + kStep - 1) / kStep;
   const int s0 = q * A.S;                       // first step of the group
@@ -341,8 +418,9 @@ __global__ __launch_bounds__(512) void prompt_kernel(TrieAttnArgs A) {
   for (int t = 0; t < NV; ++t) {
     const int cc = (w + kWavesA * t) % G::CH;
     if (cc < G::KCH) {
-      const int kb = cc / DQ, i = cc - kb * DQ;
-      voff[t] = 2 * ((16 * kb + n16) * (int)A.skpn + 32 * i + 8 * g4);
+      const int key = G::KPV * cc + lane / G::U;
+      const int b = (lane % G::U) ^ kswz<D>(key);
+      voff[t] = 2 * key * (int)A.skpn + 16 * b;
     } else {
       const int key = G::KPV * (cc - G::KCH) + lane / G::U;
       const int b = (lane % G::U) ^ vswz<D>(key);
@@ -367,6 +445,17 @@ __global__ __launch_bounds__(512) void prompt_kernel(TrieAttnArgs A) {
       }
     }
   }
+
+  // A-fragment addresses of the K operand: lane (n16, g4) reads key
+  // 16 kb + n16, head_dim [32 i + 8 g4, +8) = 16-byte unit 4 i + g4.
+  int kro[2][DQ];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) {
+      const int key = 16 * kb + n16;
+      kro[kb][i] = 16 * (key * G::U + ((4 * i + g4) ^ kswz<D>(key)));
+    }
 
   float mref[kRT], lrow[kRT];
   f32x4 acc[kRT][DT];
@@ -406,7 +495,7 @@ __global__ __launch_bounds__(512) void prompt_kernel(TrieAttnArgs A) {
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int i = 0; i < DQ; ++i)
-        kf[kb][i] = *(const __attribute__((address_space(3))) u32x4*)(slot + (kb * DQ + i) * 1024 + 16 * lane);
+        kf[kb][i] = *(const __attribute__((address_space(3))) u32x4*)(slot + kro[kb][i]);
 
     // S^T = K Q^T for two blocks of 16 keys.
     f32x4 sc[kRT][2];
@@ -503,191 +592,153 @@ __global__ __launch_bounds__(512) void prompt_kernel(TrieAttnArgs A) {
     }
   }
 
-  // Quarter partials through LDS (ring and Q area are free once every wave
-  // is past its last step): wave w's acc[t][j] as [t][j][lane] f32x4 in the
-  // ring, its (m, l) of rows 16 t + n16 in the Q area.
+  // Quarter partials combined as ((q0 (+) q1) (+) (q2 (+) q3)) through LDS
+  // (the ring is free once every wave is past its last step): stage 1 waves
+  // k = 1, 3 hand their partial to k = 0, 2; stage 2 wave k = 2 hands to
+  // k = 0, which stores the group partial of its row half.  A partial is
+  // acc[t][j] as [t][j][lane] f32x4 plus (m, l) of rows 16 t + n16.
   lds_barrier();
-  constexpr int REG = kRT * DT * 1024;
-  constexpr int REGML = kRT * 16 * 8;
-  if (has_rows) {
+  if (has_rows && (k & 1)) quarter_put<D, kRT>(ring, qreg, 2 * h + (k >> 1), acc, mref, lrow, lane);
+  lds_barrier();
+  if (has_rows && !(k & 1)) quarter_take<D, kRT>(ring, qreg, 2 * h + (k >> 1), acc, mref, lrow, lane);
+  lds_barrier();
+  if (has_rows && k == 2) quarter_put<D, kRT>(ring, qreg, 2 * h, acc, mref, lrow, lane);
+  lds_barrier();
+  typedef __attribute__((address_space(3))) float lds_float;
+  constexpr int RS = D + 4;  // staged row stride in floats: a write's 4 row groups land on different banks
+  lds_float* stage = (lds_float*)(ring + RINGBYTES / 2);
+  if (has_rows && k == 0) {
+    quarter_take<D, kRT>(ring, qreg, 2 * h, acc, mref, lrow, lane);
+    // Group partial of the wave's rows: (m, l) of rows 16 t + n16 from lanes
+    // g4 == 0 straight out; acc (rows 16 t + 4 g4 + e, head_dim 16 j + n16)
+    // staged row-major in the second half of the ring.
 #pragma unroll
     for (int t = 0; t < kRT; ++t) {
-#pragma unroll
-      for (int j = 0; j < DT; ++j)
-        *(__attribute__((address_space(3))) f32x4*)(ring + w * REG + (t * DT + j) * 1024 + 16 * lane) = acc[t][j];
       if (g4 == 0) {
-        __attribute__((address_space(3))) float* ml =
-            (__attribute__((address_space(3))) float*)(qreg + w * REGML) + 2 * (16 * t + n16);
-        ml[0] = mref[t];
-        ml[1] = lrow[t];
+        const int r = trow + 16 * t + n16;
+        if (r < A.R) {
+          float* ml = A.gp_ml + (((size_t)g * A.R + r) * A.NG + q) * 2;
+          if constexpr (ATOMIC) {
+            __hip_atomic_store(ml, mref[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(ml + 1, lrow[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          } else {
+            ml[0] = mref[t];
+            ml[1] = lrow[t];
+          }
+        }
       }
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int j = 0; j < DT; ++j)
+          stage[(16 * kRT * h + 16 * t + 4 * g4 + e) * RS + 16 * j + n16] = acc[t][j][e];
     }
   }
   lds_barrier();
-  if (!has_rows) return;
-
-  // Wave (h, k) combines units u = k UPW .. of its half (all in tile
-  // t = u / DT): quarters 0..3 in order, per row, then stores the group
-  // partial.  The combine weights of a row depend on its (m, l) only, so they
-  // are formed once per row and applied to every unit.
-  constexpr int UNITS = kRT * DT;
-  constexpr int UPW = UNITS / kQuarters;
-  static_assert(UNITS % kQuarters == 0 && DT % UPW == 0, "units split evenly over the quarters");
-  const int u0 = k * UPW;
-  const int t = u0 / DT;
-  float wa[4][kQuarters], wb[4][kQuarters], cm[4], cl[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    cm[e] = kNegInf;
-    cl[e] = 0.f;
-#pragma unroll
-    for (int kq = 0; kq < kQuarters; ++kq) {
-      const __attribute__((address_space(3))) float* ml =
-          (const __attribute__((address_space(3))) float*)(qreg + (4 * h + kq) * REGML) + 2 * (16 * t + 4 * g4 + e);
-      const float m2 = ml[0], l2 = ml[1];
-      // combine() with the accumulator update left for later: an empty
-      // quarter (m2 = -inf) contributes a = 1, b = 0 (an exact no-op).
-      if (m2 == kNegInf) {
-        wa[e][kq] = 1.f;
-        wb[e][kq] = 0.f;
-      } else {
-        const float mn = fmaxf(cm[e], m2);
-        wa[e][kq] = fexp2(cm[e] - mn);
-        wb[e][kq] = fexp2(m2 - mn);
-        cl[e] = __builtin_fmaf(l2, wb[e][kq], cl[e] * wa[e][kq]);
-        cm[e] = mn;
-      }
-    }
-  }
-#pragma unroll
-  for (int uu = 0; uu < UPW; ++uu) {
-    const int j = (u0 + uu) - t * DT;
-    float ca[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kq = 0; kq < kQuarters; ++kq) {
-      const f32x4 a4 =
-          *(const __attribute__((address_space(3))) f32x4*)(ring + (4 * h + kq) * REG + (u0 + uu) * 1024 + 16 * lane);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ca[e] = __builtin_fmaf(a4[e], wb[e][kq], ca[e] * wa[e][kq]);
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int r = trow + 16 * t + 4 * g4 + e;
-      if (r < A.R) {
-        const size_t idx = ((size_t)g * A.R + r) * A.NG + q;
-        A.gp_acc[idx * D + 16 * j + n16] = ca[e];
-        if (j == 0 && n16 == 0) {
-          A.gp_ml[idx * 2] = cm[e];
-          A.gp_ml[idx * 2 + 1] = cl[e];
-        }
-      }
+  // Every wave stores staged rows with 16-byte stores, 1 KB (RPI rows) per
+  // instruction; ATOMIC: with the coherence of an agent-scope atomic store.
+  constexpr int RPI = 1024 / (4 * D);
+  constexpr int NST = 32 * kRT / RPI;
+  const int c4 = lane % (D / 4);
+  const __amdgpu_buffer_rsrc_t racc = buffer_rsrc(A.gp_acc, 0x7fffffff);
+  for (int x = w; x < NST; x += kWavesA) {
+    const int rl = x * RPI + lane / (D / 4);
+    const int r = row0 + rl;
+    const f32x4 v = *(const __attribute__((address_space(3))) f32x4*)(stage + rl * RS + 4 * c4);
+    if (r < A.R) {
+      const size_t off = (((size_t)g * A.R + r) * A.NG + q) * D + 4 * c4;
+      if constexpr (ATOMIC) __builtin_amdgcn_raw_buffer_store_b128(v, racc, (int)(off * 4), 0, 16);
+      else *reinterpret_cast<f32x4*>(A.gp_acc + off) = v;
     }
   }
 }
 
-// ------------------------------------------------------------------ kernel B
+template <int D, int kRT>
+__global__ __launch_bounds__(512) void prompt_kernel(TrieAttnArgs A) {
+  __shared__ __attribute__((aligned(16))) char lds[PromptLds<D, kRT>::BYTES];
+  const int g = blockIdx.x % A.HK;
+  const int rest = blockIdx.x / A.HK;
+  prompt_block<D, kRT, false>(A, lds, g, rest % A.NRB, rest / A.NRB);
+}
+
+// ------------------------------------------------------------------ node fold and merge
 template <int DN> struct NodeVec;
 template <> struct NodeVec<8> { typedef u32x4 T; };
 template <> struct NodeVec<4> { typedef u32x2 T; };
 
 constexpr int kChunk = 64;  // node slots staged in LDS at a time
 
-// Workgroup (g, c8): rows r = 8 c8 + 4 w + e of kv head g (wave w, lane
-// 16 e + n holds head_dim [DN n, +DN) of row e).  The node K/V of a 64-slot
-// chunk is copied into LDS once for the 8 rows while their masks are read;
-// each row folds its allowed slots in slot order; then the group partials are
-// combined in group order and the node partial last, and bf16 is stored.
+template <int D> struct NodeLds { static constexpr int BYTES = 2 * kChunk * 2 * D; };  // K rows, then V rows
+
+// Where a row's result goes: row r of kv head g is query r / GQA of head
+// g GQA + r % GQA.  Rows past R shadow a valid row and are never stored.
+struct RowRef {
+  int rr, mq, hd;
+  bool live;
+};
+__device__ __forceinline__ RowRef row_ref(const TrieAttnArgs& A, int g, int r, int fallback) {
+  RowRef x;
+  x.live = r < A.R;
+  x.rr = x.live ? r : fallback;
+  x.mq = x.rr / A.GQA;
+  x.hd = g * A.GQA + (x.rr - x.mq * A.GQA);
+  return x;
+}
+
+// Node partial of one row per 16 lanes (lane 16 e + n holds head_dim
+// [DN n, +DN) of the wave's row e): the row's allowed node slots folded one
+// at a time in slot order, fp32 p (attention.py:52-67).  Every wave of the
+// workgroup (nw of them, this is wave w) calls it: 64-slot chunks of kv head
+// g's node K/V are copied into LDS `kv` by all of them; waves whose rows are
+// not live only help with the copies.  Ends with every vector load of the
+// calling wave complete.
 template <int D>
-__global__ __launch_bounds__(64 * kWavesB) void node_merge_kernel(TrieAttnArgs A) {
+__device__ __forceinline__ void node_fold(const TrieAttnArgs& A, int g, const RowRef& R, lds_char* kv, int w, int nw,
+                                          float& m, float& l, float (&acc)[D / 16]) {
   constexpr int DN = D / 16;
   constexpr int RB = 2 * D;                          // bytes per node row
   constexpr int CHB = kChunk * RB;                   // bytes of K (or V) per chunk
-  constexpr int NDMA = 2 * CHB / 1024 / kWavesB;     // 1 KB loads per wave per chunk
   constexpr int kB = 8;                              // slots per fold batch
   typedef typename NodeVec<DN>::T VecT;
   constexpr int NW = DN / 2;                         // 32-bit words per lane vector
-  __shared__ __attribute__((aligned(16))) char kv[2 * CHB];  // K rows, then V rows
-
   const int lane = __lane_id();
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int e = lane >> 4, n = lane & 15;
-  const int RC8 = (A.R + 7) / 8;
-  const int g = blockIdx.x / RC8;
-  const int c8 = blockIdx.x - g * RC8;
-  const int r = 8 * c8 + 4 * w + e;
-  const bool live = r < A.R;
-  const int rr = live ? r : 8 * c8;  // rows past R shadow the block's first row
-  const int mq = rr / A.GQA;
-  const int hd = g * A.GQA + (rr - mq * A.GQA);
   const int d0 = DN * n;
-  const int NG = A.NG;
   const int NN = A.NN;
-  lds_char* kvl = (lds_char*)kv;
+  m = kNegInf;
+  l = 0.f;
+#pragma unroll
+  for (int i = 0; i < DN; ++i) acc[i] = 0.f;
+  if (NN == 0) return;
 
-  // In issue order: q, the mask of chunk 0, chunk 0's K/V into LDS, the group
-  // partials (consumed last).
-  const VecT qv = *reinterpret_cast<const VecT*>(A.q + hd * A.sqh + (int64_t)mq * A.sqm + d0);
-  const uint8_t* mrow = A.msk + (int64_t)mq * A.smm;
-  uint8_t mb[4];
-  auto load_mask = [&](int c0) {
+  float qf[DN];
+  {
+    const VecT qv = *reinterpret_cast<const VecT*>(A.q + R.hd * A.sqh + (int64_t)R.mq * A.sqm + d0);
+#pragma unroll
+    for (int i = 0; i < NW; ++i) { qf[2 * i] = bf16_lo(qv[i]); qf[2 * i + 1] = bf16_hi(qv[i]); }
+  }
+  const uint8_t* mrow = A.msk + (int64_t)R.mq * A.smm;
+  const uint16_t* knb = A.kn + g * A.sknh;
+  const uint16_t* vnb = A.vn + g * A.svnh;
+
+  for (int c0 = 0; c0 < NN; c0 += kChunk) {
+    if (c0 > 0) lds_barrier();  // every wave is done with the previous chunk
+    // Row e's mask bytes of the chunk: lane (e, n) tests slots c0 + 16 b + n.
+    uint8_t mb[4];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const int t = c0 + 16 * b + n;
-      mb[b] = (live && t < NN) ? mrow[(int64_t)t * A.smn] : (uint8_t)0;
+      mb[b] = (R.live && t < NN) ? mrow[(int64_t)t * A.smn] : (uint8_t)0;
     }
-  };
-  const uint16_t* knb = A.kn + g * A.sknh;
-  const uint16_t* vnb = A.vn + g * A.svnh;
-  auto load_chunk = [&](int c0) {
+    // The chunk's K and V rows into LDS: 1 KB pieces x = w, w + nw, ...
     const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(knb + (int64_t)c0 * A.sknn, 2 * ((int64_t)(NN - c0 - 1) * A.sknn + D));
     const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(vnb + (int64_t)c0 * A.svnn, 2 * ((int64_t)(NN - c0 - 1) * A.svnn + D));
-#pragma unroll
-    for (int jj = 0; jj < NDMA; ++jj) {
-      const int x = w + kWavesB * jj;          // 1 KB piece of [K rows | V rows]
+    for (int x = w; x < 2 * CHB / 1024; x += nw) {
       const int byte = (x * 1024 + 16 * lane) % CHB;
       const int slot = byte / RB, unit = (byte % RB) / 16;
-      if (x * 1024 < CHB) bdma16(rk, 2 * slot * (int)A.sknn + 16 * unit, kvl + x * 1024);
-      else bdma16(rv, 2 * slot * (int)A.svnn + 16 * unit, kvl + x * 1024);
+      if (x * 1024 < CHB) bdma16(rk, 2 * slot * (int)A.sknn + 16 * unit, kv + x * 1024);
+      else bdma16(rv, 2 * slot * (int)A.svnn + 16 * unit, kv + x * 1024);
     }
-  };
-  if (NN > 0) {
-    load_mask(0);
-    load_chunk(0);
-  }
-  asm volatile("" ::: "memory");  // the waits below count on this issue order
-  float gm[kGroupTarget], gl[kGroupTarget];
-  f32x4 ga[kGroupTarget][DN / 4];
-  const size_t gbase = ((size_t)g * A.R + rr) * NG;
-#pragma unroll
-  for (int qq = 0; qq < kGroupTarget; ++qq) {
-    if (qq < NG) {
-      const float2 ml = *reinterpret_cast<const float2*>(A.gp_ml + (gbase + qq) * 2);
-      gm[qq] = ml.x;
-      gl[qq] = ml.y;
-#pragma unroll
-      for (int v = 0; v < DN / 4; ++v)
-        ga[qq][v] = *reinterpret_cast<const f32x4*>(A.gp_acc + (gbase + qq) * D + d0 + 4 * v);
-    }
-  }
-  const int npart = NG * (DN / 4 + 1);  // partial loads still in flight behind the chunk
-
-  float qf[DN];
-#pragma unroll
-  for (int i = 0; i < NW; ++i) { qf[2 * i] = bf16_lo(qv[i]); qf[2 * i + 1] = bf16_hi(qv[i]); }
-  float m = kNegInf, l = 0.f, acc[DN];
-#pragma unroll
-  for (int i = 0; i < DN; ++i) acc[i] = 0.f;
-
-  for (int c0 = 0; c0 < NN; c0 += kChunk) {
-    if (c0 > 0) {
-      lds_barrier();       // both waves are done with the previous chunk
-      load_mask(c0);
-      load_chunk(c0);
-      wait_vm(NDMA);       // the mask
-    } else {
-      wait_vm(NDMA + npart);
-    }
-    // Row e's allowed slots of the chunk: lane (e, n) tested slots 16 b + n.
     uint64_t mm = 0;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -696,8 +747,8 @@ __global__ __launch_bounds__(64 * kWavesB) void node_merge_kernel(TrieAttnArgs A
     }
     const int cnt = __builtin_popcountll(mm);
     const int cmax = max(max(__shfl(cnt, 0), __shfl(cnt, 16)), max(__shfl(cnt, 32), __shfl(cnt, 48)));
-    wait_vm(c0 > 0 ? 0 : npart);  // this wave's part of the chunk is in LDS
-    lds_barrier();                // and the other wave's part
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of the chunk is in LDS
+    lds_barrier();                       // and every other wave's part
 
     for (int b0 = 0; b0 < cmax; b0 += kB) {
       int js[kB];
@@ -711,8 +762,8 @@ __global__ __launch_bounds__(64 * kWavesB) void node_merge_kernel(TrieAttnArgs A
       VecT kr[kB], vr[kB];
 #pragma unroll
       for (int u = 0; u < kB; ++u) {
-        kr[u] = *(const __attribute__((address_space(3))) VecT*)(kvl + js[u] * RB + 2 * d0);
-        vr[u] = *(const __attribute__((address_space(3))) VecT*)(kvl + CHB + js[u] * RB + 2 * d0);
+        kr[u] = *(const __attribute__((address_space(3))) VecT*)(kv + js[u] * RB + 2 * d0);
+        vr[u] = *(const __attribute__((address_space(3))) VecT*)(kv + CHB + js[u] * RB + 2 * d0);
       }
       float sc[kB];
 #pragma unroll
@@ -742,9 +793,46 @@ __global__ __launch_bounds__(64 * kWavesB) void node_merge_kernel(TrieAttnArgs A
       }
     }
   }
-  wait_vm(0);  // the group partials
+}
 
-  // Final: groups in order, then the node partial.
+// Final result of the wave's row e: the group partials combined in group
+// order, then the node partial (m, l, acc); bf16 store.
+template <int D, bool COH = false>
+__device__ __forceinline__ void merge_store(const TrieAttnArgs& A, int g, const RowRef& R, float m, float l,
+                                            const float (&acc)[D / 16]) {
+  constexpr int DN = D / 16;
+  typedef typename NodeVec<DN>::T VecT;
+  constexpr int NW = DN / 2;
+  const int lane = __lane_id();
+  const int d0 = DN * (lane & 15);
+  const int NG = A.NG;
+  float gm[kGroupTarget], gl[kGroupTarget];
+  f32x4 ga[kGroupTarget][DN / 4];
+  const size_t gbase = ((size_t)g * A.R + R.rr) * NG;
+  // Byte offsets of the partials fit 31 bits (checked by the host for COH).
+  const __amdgpu_buffer_rsrc_t rml = buffer_rsrc(A.gp_ml, 0x7fffffff);
+  const __amdgpu_buffer_rsrc_t racc = buffer_rsrc(A.gp_acc, 0x7fffffff);
+#pragma unroll
+  for (int qq = 0; qq < kGroupTarget; ++qq) {
+    if (qq < NG) {
+      if constexpr (COH) {
+        // sc1 (cache policy 16): the coherence of an agent-scope atomic load.
+        const f32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(rml, (int)((gbase + qq) * 8), 0, 16);
+        gm[qq] = ml.x;
+        gl[qq] = ml.y;
+#pragma unroll
+        for (int v = 0; v < DN / 4; ++v)
+          ga[qq][v] = __builtin_amdgcn_raw_buffer_load_b128(racc, (int)(((gbase + qq) * D + d0 + 4 * v) * 4), 0, 16);
+      } else {
+        const float2 ml = *reinterpret_cast<const float2*>(A.gp_ml + (gbase + qq) * 2);
+        gm[qq] = ml.x;
+        gl[qq] = ml.y;
+#pragma unroll
+        for (int v = 0; v < DN / 4; ++v)
+          ga[qq][v] = *reinterpret_cast<const f32x4*>(A.gp_acc + (gbase + qq) * D + d0 + 4 * v);
+      }
+    }
+  }
   float fm = kNegInf, fl = 0.f, facc[DN];
 #pragma unroll
   for (int i = 0; i < DN; ++i) facc[i] = 0.f;
@@ -752,19 +840,116 @@ __global__ __launch_bounds__(64 * kWavesB) void node_merge_kernel(TrieAttnArgs A
   for (int qq = 0; qq < kGroupTarget; ++qq)
     if (qq < NG) combine<DN>(fm, fl, facc, gm[qq], gl[qq], reinterpret_cast<const float*>(ga[qq]));
   combine<DN>(fm, fl, facc, m, l, acc);
-
-  if (!live) return;
+  if (!R.live) return;
   VecT ov;
 #pragma unroll
   for (int i = 0; i < NW; ++i) ov[i] = pack_bf16x2(facc[2 * i] / fl, facc[2 * i + 1] / fl);
-  *reinterpret_cast<VecT*>(A.out + hd * A.soh + (int64_t)mq * A.som + d0) = ov;
+  *reinterpret_cast<VecT*>(A.out + R.hd * A.soh + (int64_t)R.mq * A.som + d0) = ov;
+}
+
+// ------------------------------------------------------------------ kernel B
+// Workgroup (g, c8): rows r = 8 c8 + 4 w + e of kv head g (wave w, lane
+// 16 e + n holds head_dim [DN n, +DN) of row e): node fold, then merge.
+template <int D>
+__global__ __launch_bounds__(64 * kWavesB) void node_merge_kernel(TrieAttnArgs A) {
+  __shared__ __attribute__((aligned(16))) char kv[NodeLds<D>::BYTES];
+  const int lane = __lane_id();
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+  const int RC8 = (A.R + 7) / 8;
+  const int g = blockIdx.x / RC8;
+  const int c8 = blockIdx.x - g * RC8;
+  const RowRef R = row_ref(A, g, 8 * c8 + 4 * w + (lane >> 4), 8 * c8);
+  float m, l, acc[D / 16];
+  node_fold<D>(A, g, R, (lds_char*)kv, w, kWavesB, m, l, acc);
+  merge_store<D>(A, g, R, m, l, acc);
+}
+
+// ------------------------------------------------------------------ fused kernel
+// One launch: workgroup (g, rb, q) runs prompt_block, counts itself in
+// cnt[g][rb], folds the node slots of its share of the block's rows -- rows
+// q RPW .. q RPW + RPW - 1 of the block, 4 per wave -- and, once all NG groups
+// of the block are counted, merges those rows.  Every workgroup of the grid is
+// resident at once (the host launches this kernel only when the grid fits),
+// so the wait always ends; it is also bounded, and a bound reached raises a
+// flag the host can read.  The last workgroup of a block to finish its merge
+// resets the block's counters to zero.
+//
+// Visibility without cache-wide fences: every word that crosses workgroups
+// (group partials, counters) is written by an agent-scope atomic store or
+// read-modify-write and read by a load with the same coherence bit (sc1) as an
+// agent-scope atomic load, so no access depends on an L2 write-back or
+// invalidate.  Order: each wave waits for its own partial stores to complete
+// (vmcnt 0) before the workgroup barrier that precedes the counter increment;
+// the partial loads are issued only after the counter load that released the
+// wait has returned.  A release/acquire pair at agent scope (buffer_wbl2 and
+// buffer_inv of the whole L2) would order the same accesses at several
+// microseconds per workgroup.
+constexpr int kSpinLimit = 1 << 22;
+constexpr int kSyncWords = 4096;   // timeout flag + [HK][NRB][2] counters
+
+template <int D, int kRT>
+__global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
+  constexpr int LB = PromptLds<D, kRT>::BYTES > NodeLds<D>::BYTES ? PromptLds<D, kRT>::BYTES : NodeLds<D>::BYTES;
+  __shared__ __attribute__((aligned(16))) char lds[LB];
+  const int lane = __lane_id();
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = blockIdx.x % A.HK;
+  const int rest = blockIdx.x / A.HK;
+  const int rb = rest % A.NRB;
+  const int q = rest / A.NRB;
+  int* cnt = A.sync + 1 + 2 * (g * A.NRB + rb);
+
+  prompt_block<D, kRT, true>(A, lds, g, rb, q);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
+  lds_barrier();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  const int rows_blk = 32 * kRT;
+  const int rpw = 4 * ((rows_blk / 4 + A.NG - 1) / A.NG);   // rows merged per workgroup (multiple of 4)
+  const int r0 = rb * rows_blk + q * rpw;
+  const int rend = min(rb * rows_blk + min(rows_blk, (q + 1) * rpw), A.R);
+  bool waited = false;
+  for (int p0 = r0; p0 < rend; p0 += 4 * kWavesA) {
+    if (p0 != r0) lds_barrier();  // every wave is done with the previous pass's node chunk
+    const int rbase = p0 + 4 * w;
+    const int r = rbase + (lane >> 4);
+    RowRef Rl = row_ref(A, g, r < rend ? r : A.R, p0);   // rows of other shares shadow row p0
+    Rl.live = r < rend;
+    float m, l, acc[D / 16];
+    node_fold<D>(A, g, Rl, (lds_char*)lds, w, kWavesA, m, l, acc);
+    if (!waited) {
+      if (w == 0) {
+        int v = 0;
+        for (int it = 0; it < kSpinLimit; ++it) {
+          v = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (v >= A.NG) break;
+          __builtin_amdgcn_s_sleep(2);
+        }
+        if (v < A.NG && lane == 0) __hip_atomic_store(A.sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      }
+      lds_barrier();
+      waited = true;
+    }
+    if (rbase < rend) merge_store<D, true>(A, g, Rl, m, l, acc);
+  }
+  // Counters back to zero once every workgroup of the block is past its wait.
+  lds_barrier();
+  if (threadIdx.x == 0) {
+    const int d = __hip_atomic_fetch_add(cnt + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (d == A.NG - 1) {
+      __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(cnt + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 // ------------------------------------------------------------------ host side
 
 struct Plan {
   int GQA, R, RT, NRB, NG, S, prompt_wgs, node_wgs;
-  size_t off_gp_ml, off_gp_acc, total;
+  size_t off_gp_ml, off_gp_acc, off_sync, total;
 };
 
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -794,20 +979,53 @@ static int make_plan(int H, int HK, int M, int P, int NN, int D, int rows_per_wa
   pl->prompt_wgs = HK * pl->NRB * pl->NG;
   pl->node_wgs = HK * ((pl->R + 7) / 8);
   const size_t parts = (size_t)HK * pl->R * pl->NG;
+  // The synchronisation words sit at the start, at the same place for every
+  // shape, so a workspace shared by calls of different shapes never holds
+  // another call's partials where a call expects zero counters.
   size_t off = 0;
+  pl->off_sync = off;   off = align256(off + kSyncWords * sizeof(int));
   pl->off_gp_ml = off;  off = align256(off + parts * 2 * sizeof(float));
   pl->off_gp_acc = off; off = align256(off + parts * D * sizeof(float));
   pl->total = off;
   return RSPX_OK;
 }
 
-template <int D>
-static void launch_all(const TrieAttnArgs& a, const Plan& pl, hipStream_t s) {
-  if (pl.prompt_wgs > 0) {
-    if (pl.RT == 1) hipLaunchKernelGGL((prompt_kernel<D, 1>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);
-    else hipLaunchKernelGGL((prompt_kernel<D, 2>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);
+// Workgroups of fused_kernel<D, RT> the device holds at once (0 if unknown).
+template <int D, int RT>
+static int fused_capacity() {
+  static int cap[64];
+  static bool done[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!done[dev]) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fused_kernel<D, RT>, 64 * kWavesA, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      per_cu = cus = 0;
+    }
+    cap[dev] = per_cu * cus;
+    done[dev] = true;
   }
+  return cap[dev];
+}
+
+template <int D, int RT>
+static void launch_rt(const TrieAttnArgs& a, const Plan& pl, hipStream_t s, int mode) {
+  const bool fused = pl.NG > 0 && mode != 2 && 1 + 2 * pl.NRB * a.HK <= kSyncWords &&
+                     (size_t)a.HK * pl.R * pl.NG * D * sizeof(float) < (size_t(1) << 31) &&
+                     pl.prompt_wgs <= fused_capacity<D, RT>();
+  if (fused) {
+    hipLaunchKernelGGL((fused_kernel<D, RT>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);
+    return;
+  }
+  if (pl.prompt_wgs > 0) hipLaunchKernelGGL((prompt_kernel<D, RT>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);
   hipLaunchKernelGGL((node_merge_kernel<D>), dim3(pl.node_wgs), dim3(64 * kWavesB), 0, s, a);
+}
+
+template <int D>
+static void launch_all(const TrieAttnArgs& a, const Plan& pl, hipStream_t s, int mode) {
+  if (pl.RT == 1) launch_rt<D, 1>(a, pl, s, mode);
+  else launch_rt<D, 2>(a, pl, s, mode);
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -822,16 +1040,12 @@ extern "C" int64_t rspx_trie_attn_workspace_bytes(int H, int HK, int M, int P, i
   return (int64_t)pl.total;  // independent of NN and rows_per_wave
 }
 
-extern "C" int rspx_trie_attn(const void* q, int64_t sqh, int64_t sqm,
-                              const void* kp, int64_t skph, int64_t skpn,
-                              const void* vp, int64_t svph, int64_t svpn,
-                              const void* kn, int64_t sknh, int64_t sknn,
-                              const void* vn, int64_t svnh, int64_t svnn,
-                              const uint8_t* msk, int64_t smm, int64_t smn,
-                              void* out, int64_t soh, int64_t som,
-                              int H, int HK, int M, int P, int NN, int D, float sm_scale,
-                              void* workspace, int64_t workspace_bytes, int rows_per_wave,
-                              void* stream) {
+static int trie_attn_impl(const void* q, int64_t sqh, int64_t sqm, const void* kp, int64_t skph, int64_t skpn,
+                          const void* vp, int64_t svph, int64_t svpn, const void* kn, int64_t sknh, int64_t sknn,
+                          const void* vn, int64_t svnh, int64_t svnn, const uint8_t* msk, int64_t smm, int64_t smn,
+                          void* out, int64_t soh, int64_t som, int H, int HK, int M, int P, int NN, int D,
+                          float sm_scale, void* workspace, int64_t workspace_bytes, int rows_per_wave, void* stream,
+                          int mode) {
   Plan pl;
   int rc = make_plan(H, HK, M, P, NN, D, rows_per_wave, &pl);
   if (rc != RSPX_OK) return rc;
@@ -839,14 +1053,14 @@ extern "C" int rspx_trie_attn(const void* q, int64_t sqh, int64_t sqm,
   if (M == 0) return RSPX_OK;
   if (!q || !out || (P > 0 && (!kp || !vp)) || (NN > 0 && (!kn || !vn || !msk)))
     return RSPX_EINVAL;
-  if (pl.total > 0 && (!workspace || workspace_bytes < (int64_t)pl.total)) return RSPX_EWORKSPACE;
+  if (!workspace || workspace_bytes < (int64_t)pl.total) return RSPX_EWORKSPACE;
   const void* ptrs[] = {q, kp, vp, kn, vn, out, workspace};
   for (const void* p : ptrs)
     if (p && !aligned16(p)) return RSPX_EALIGN;
   const int64_t strides[] = {sqh, sqm, skph, skpn, svph, svpn, sknh, sknn, svnh, svnn, soh, som};
   for (int64_t s : strides)
     if (s % 8 != 0) return RSPX_EALIGN;
-  // Byte offsets inside one kv head's prompt K/V are 32-bit.
+  // Byte offsets inside one kv head's prompt and node K/V are 32-bit.
   if (P > 0 && ((int64_t)P * skpn * 2 >= (1ll << 31) || (int64_t)P * svpn * 2 >= (1ll << 31)))
     return RSPX_EUNSUPPORTED;
   if (NN > 0 && ((int64_t)NN * sknn * 2 >= (1ll << 31) || (int64_t)NN * svnn * 2 >= (1ll << 31)))
@@ -866,9 +1080,46 @@ extern "C" int rspx_trie_attn(const void* q, int64_t sqh, int64_t sqm,
   char* ws = static_cast<char*>(workspace);
   a.gp_ml = reinterpret_cast<float*>(ws + pl.off_gp_ml);
   a.gp_acc = reinterpret_cast<float*>(ws + pl.off_gp_acc);
+  a.sync = reinterpret_cast<int*>(ws + pl.off_sync);
 
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (D == 128) launch_all<128>(a, pl, s);
-  else launch_all<64>(a, pl, s);
+  if (D == 128) launch_all<128>(a, pl, s, mode);
+  else launch_all<64>(a, pl, s, mode);
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
+}
+
+extern "C" int rspx_trie_attn(const void* q, int64_t sqh, int64_t sqm, const void* kp, int64_t skph, int64_t skpn,
+                              const void* vp, int64_t svph, int64_t svpn, const void* kn, int64_t sknh, int64_t sknn,
+                              const void* vn, int64_t svnh, int64_t svnn, const uint8_t* msk, int64_t smm,
+                              int64_t smn, void* out, int64_t soh, int64_t som, int H, int HK, int M, int P, int NN,
+                              int D, float sm_scale, void* workspace, int64_t workspace_bytes, int rows_per_wave,
+                              void* stream) {
+  return trie_attn_impl(q, sqh, sqm, kp, skph, skpn, vp, svph, svpn, kn, sknh, sknn, vn, svnh, svnn, msk, smm, smn,
+                        out, soh, som, H, HK, M, P, NN, D, sm_scale, workspace, workspace_bytes, rows_per_wave,
+                        stream, 0);
+}
+
+extern "C" int rspx_trie_attn_launches(const void* q, int64_t sqh, int64_t sqm, const void* kp, int64_t skph,
+                                       int64_t skpn, const void* vp, int64_t svph, int64_t svpn, const void* kn,
+                                       int64_t sknh, int64_t sknn, const void* vn, int64_t svnh, int64_t svnn,
+                                       const uint8_t* msk, int64_t smm, int64_t smn, void* out, int64_t soh,
+                                       int64_t som, int H, int HK, int M, int P, int NN, int D, float sm_scale,
+                                       void* workspace, int64_t workspace_bytes, int rows_per_wave, int launches,
+                                       void* stream) {
+  if (launches != 1 && launches != 2) return RSPX_EINVAL;
+  return trie_attn_impl(q, sqh, sqm, kp, skph, skpn, vp, svph, svpn, kn, sknh, sknn, vn, svnh, svnn, msk, smm, smn,
+                        out, soh, som, H, HK, M, P, NN, D, sm_scale, workspace, workspace_bytes, rows_per_wave,
+                        stream, launches);
+}
+
+extern "C" int rspx_trie_attn_status(const void* workspace, int H, int HK, int M, int P, int D, void* stream) {
+  Plan pl;
+  if (make_plan(H, HK, M, P, 0, D, 1, &pl) != RSPX_OK || !workspace) return RSPX_EINVAL;
+  int v = 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (hipMemcpyAsync(&v, static_cast<const char*>(workspace) + pl.off_sync, sizeof(int), hipMemcpyDeviceToHost, s) !=
+          hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return RSPX_ELAUNCH;
+  return v ? 1 : 0;
 }

@@ -108,7 +108,7 @@ class Decoder:
                 raise RuntimeError("decoder workspace must be sized before graph capture")
             if ws is not None:
                 self._ws_retired.append(ws)
-            ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+            ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)
             self._ws[name] = ws
         return ws
 

@@ -21,11 +21,13 @@ from .. import _lib
 from ._tensor import as_kernel_input
 
 
-def trie_attn(q, kp, vp, kn, vn, msk, sm_scale=None, out=None, rows_per_wave: int = 0, workspace=None):
-    """Launch the kernel on the current stream.  ``rows_per_wave`` (0/1/2) only
-    changes the work split, never the result.  ``workspace``: a uint8 GPU tensor
-    of at least rspx_trie_attn_workspace_bytes bytes (default: a per-stream
-    scratch buffer)."""
+def trie_attn(q, kp, vp, kn, vn, msk, sm_scale=None, out=None, rows_per_wave: int = 0, workspace=None,
+              launches: int = 0):
+    """Launch the kernel on the current stream.  ``rows_per_wave`` (0/1/2) and
+    ``launches`` (0 = automatic, 1 = one kernel when it fits, 2 = two kernels)
+    only change the work split, never the result.  ``workspace``: a zero-filled
+    uint8 GPU tensor of at least rspx_trie_attn_workspace_bytes bytes (default:
+    a per-stream scratch buffer)."""
     H, M, D = q.shape
     HK, P, D2 = kp.shape
     NN = kn.shape[1]
@@ -54,7 +56,9 @@ def trie_attn(q, kp, vp, kn, vn, msk, sm_scale=None, out=None, rows_per_wave: in
     ws = workspace if workspace is not None else _lib.workspace(dev, need)
     if ws.numel() < need:
         raise ValueError("fused_attn_hyb: workspace too small")
-    rc = L.rspx_trie_attn(
+    fn = L.rspx_trie_attn if launches == 0 else L.rspx_trie_attn_launches
+    extra = () if launches == 0 else (int(launches),)
+    rc = fn(
         q.data_ptr(), q.stride(0), q.stride(1),
         kp.data_ptr(), kp.stride(0), kp.stride(1),
         vp.data_ptr(), vp.stride(0), vp.stride(1),
@@ -63,7 +67,7 @@ def trie_attn(q, kp, vp, kn, vn, msk, sm_scale=None, out=None, rows_per_wave: in
         msk.data_ptr(), msk.stride(0), msk.stride(1),
         out.data_ptr(), out.stride(0), out.stride(1),
         H, HK, M, P, NN, D, float(sm_scale),
-        ws.data_ptr(), ws.numel(), int(rows_per_wave),
+        ws.data_ptr(), ws.numel(), int(rows_per_wave), *extra,
         _lib.stream_ptr(dev))
     _lib.check("rspx_trie_attn", rc)
     return out
@@ -95,7 +99,7 @@ def make_launcher(q, kp, vp, kn, vn, msk, sm_scale=None, out=None, workspace=Non
     L = _lib.lib()
     need = L.rspx_trie_attn_workspace_bytes(H, HK, M, P, D)
     if workspace is None:
-        workspace = _lib.workspace(q.device, need)
+        workspace = _lib.workspace(q.device, need)   # zero-filled on allocation
     if workspace.numel() < need:
         raise ValueError("make_launcher: workspace too small")
     s = stream if stream is not None else _lib.stream_ptr(q.device)

@@ -199,3 +199,53 @@ def test_drop_in_signature_and_errors():
     # non-contiguous views are accepted (copied where the layout needs it)
     qt = args[0].transpose(0, 1).contiguous().transpose(0, 1)
     assert torch.equal(fused_attn_hyb(qt, *args[1:]), out)
+
+
+def _status(case, ws):
+    from respect_amd import _lib
+    H, M, D = case.q.shape
+    HK, P, _ = case.kp.shape
+    return _lib.lib().rspx_trie_attn_status(ws.data_ptr(), H, HK, M, P, D, _lib.stream_ptr(ws.device))
+
+
+@pytest.mark.parametrize("which", ["cfg1", "cfg2", "base37", "long", "gqa2", "d64"])
+def test_one_and_two_launches_equal(which):
+    """The one-kernel path (prompt groups, node fold and merge with workgroups
+    waiting on per-row-block counters) and the two-kernel path give the same
+    bits; the counters are back at zero after each call (repeat calls on one
+    workspace stay equal) and no wait ran out."""
+    from respect_amd import _lib
+    c = {"cfg1": gen.cfg1, "cfg2": gen.cfg2, "base37": lambda: gen.cfg2(seed=4, base=37),
+         "long": lambda: gen.attn_case(8, 32, 8, 128, 16384, 8, 32, 0, 32, 128, kv_scale=128 ** -0.5),
+         "gqa2": lambda: gen.attn_case(7, 16, 8, 128, 700, 3, 9, 0, 6, None),
+         "d64": lambda: gen.attn_case(7, 16, 2, 64, 3086, 3, 9, 0, 6, None)}[which]()
+    H, M, D = c.q.shape
+    HK, P, _ = c.kp.shape
+    need = _lib.lib().rspx_trie_attn_workspace_bytes(H, HK, M, P, D)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    two = _run(c, launches=2, workspace=ws)
+    ones = [_run(c, launches=1, workspace=ws) for _ in range(3)]
+    auto = _run(c, workspace=ws)
+    assert _status(c, ws) == 0
+    for o in ones + [auto]:
+        assert torch.equal(o, two)
+    for rpw in (1, 2):
+        assert torch.equal(_run(c, launches=1, rows_per_wave=rpw, workspace=ws), two)
+    assert _status(c, ws) == 0
+
+
+def test_one_launch_workspace_shared_by_shapes():
+    """One workspace used by calls of different shapes in turn (as the decoder's
+    verify and 1-token calls share one): the counters sit where no call writes
+    partials, so every call still equals its two-kernel result."""
+    from respect_amd import _lib
+    cases = [gen.cfg2(seed=9), gen.cfg1(), gen.attn_case(3, 32, 8, 128, 5000, 2, 4, 0, 1, None),
+             gen.cfg2(seed=9, base=100)]
+    need = max(_lib.lib().rspx_trie_attn_workspace_bytes(c.q.shape[0], c.kp.shape[0], c.q.shape[1],
+                                                         c.kp.shape[1], c.q.shape[2]) for c in cases)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    want = [_run(c, launches=2) for c in cases]
+    for _ in range(2):
+        for c, w in zip(cases, want):
+            assert torch.equal(_run(c, launches=1, workspace=ws), w)
+    assert _status(cases[0], ws) == 0
