@@ -22,6 +22,10 @@
  *   rspx_trie_mask      respect/decoding/verify.py:22-41 mask + dispatch.py:94-115 padding
  *   rspx_kv_compact     respect/decoding/kv_buffer.py:93 compact(cache, prompt_len, base, slots)
  *   rspx_argmax_rows    respect/decoding/acceptance.py:20 greedy_token(logits, offset, size)
+ *   rspx_square         respect/system/fused.py:126 _sq_k (the squares of rmsnorm, fused.py:176)
+ *   rspx_add_sq         respect/system/fused.py:185 add_sq(r, h)
+ *   rspx_norm_apply     respect/system/fused.py:148 _norm_apply_k (norm_from, fused.py:165)
+ *   rspx_rope_vision    respect/system/fused.py:97  rope_vision(x, cos, sin)
  */
 #ifndef RESPECT_AMD_H
 #define RESPECT_AMD_H
@@ -247,6 +251,33 @@ int rspx_kv_compact(const uint64_t* bases, int n_tensors, int HK, int D, int64_t
 int64_t rspx_argmax_workspace_bytes(int M, int V);
 int rspx_argmax_rows(const float* logits, int64_t sl, int M, int V, int off, int size, int64_t* out, void* workspace,
                      int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- Prefill / Flow element-wise
+ * The kernels the reference's Prefill and Flow patches use, at PyTorch's
+ * rounding points (every multiply and add a separate fp32 operation):
+ *
+ * rspx_square: q = float(x)^2.  x [rows, n] bf16 (row stride sx), q [rows, n]
+ *   fp32 (row stride sq).  Replaces _sq_k, respect/system/fused.py:126.
+ * rspx_add_sq: x = bf16(float(r) + float(h)), q = float(x)^2.  Replaces
+ *   add_sq(r, h), respect/system/fused.py:185 (bf16 inputs and output).
+ * rspx_norm_apply: y = bf16(float(w) * bf16(float(x) * rsqrt(var[row] + eps)))
+ *   with var [rows] fp32 (the mean of q, taken by the caller as the reference
+ *   takes it with PyTorch) and w [n].  rsqrt is a correctly rounded square
+ *   root and divide.  Replaces _norm_apply_k / norm_from(xs, sq, w, eps),
+ *   respect/system/fused.py:148-173.
+ * rspx_rope_vision: y = bf16(x * cos + rotate_half(x) * sin) in fp32 with one
+ *   final rounding; x [L, NH, D] bf16 (strides sxl, sxh), cos/sin [L, D] fp32
+ *   (row stride scl), y [L, NH, D] contiguous.  D % 16 == 0.  Replaces
+ *   rope_vision(x, cos, sin), respect/system/fused.py:97.
+ * n % 8 == 0; pointers and row strides 16-byte aligned.
+ */
+int rspx_square(const void* x, int64_t sx, float* q, int64_t sq, int rows, int n, void* stream);
+int rspx_add_sq(const void* r, int64_t sr, const void* h, int64_t sh, void* x, int64_t sx, float* q, int64_t sq,
+                int rows, int n, void* stream);
+int rspx_norm_apply(const void* x, int64_t sx, const float* var, const void* w, void* y, int64_t sy, int rows, int n,
+                    float eps, void* stream);
+int rspx_rope_vision(const void* x, int64_t sxl, int64_t sxh, const float* cos, const float* sin, int64_t scl,
+                     void* y, int L, int NH, int D, void* stream);
 
 #ifdef __cplusplus
 }

@@ -97,3 +97,78 @@ def rope_tables(positions, head_dim: int = 128, theta: float = 1.0e6, device=Non
     freqs = pos[:, None] * inv_freq[None, :]
     emb = torch.cat((freqs, freqs), dim=-1)
     return emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+
+
+# ------------------------------------------------------------------ Prefill / Flow
+# respect/system/fused.py:126-194 and :78-103: the kernels compute the squares,
+# the residual add and the normalisation at PyTorch's rounding points; the mean
+# of the squares is taken with PyTorch, as the reference does, so RMSNorm's
+# reduction order is PyTorch's.
+
+def _bf16_rows(t, name):
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name}: respect_amd builds the bf16 path only")
+    return as_kernel_input(t.reshape(-1, t.shape[-1]).contiguous(), name)
+
+
+def _square(xs):
+    M, N = xs.shape
+    sq = torch.empty((M, N), device=xs.device, dtype=torch.float32)
+    rc = _lib.lib().rspx_square(xs.data_ptr(), xs.stride(0), sq.data_ptr(), sq.stride(0), M, N,
+                                _lib.stream_ptr(xs.device))
+    _lib.check("rspx_square", rc)
+    return sq
+
+
+def add_sq(r, h):
+    """x = r + h (bf16, rounded once) and x.float() ** 2; both [rows, n]."""
+    if r.shape != h.shape:
+        raise ValueError("add_sq: r and h must have the same shape")
+    rs, hs = _bf16_rows(r, "r"), _bf16_rows(h, "h")
+    M, N = rs.shape
+    x = torch.empty((M, N), device=r.device, dtype=torch.bfloat16)
+    sq = torch.empty((M, N), device=r.device, dtype=torch.float32)
+    rc = _lib.lib().rspx_add_sq(rs.data_ptr(), rs.stride(0), hs.data_ptr(), hs.stride(0), x.data_ptr(), x.stride(0),
+                                sq.data_ptr(), sq.stride(0), M, N, _lib.stream_ptr(r.device))
+    _lib.check("rspx_add_sq", rc)
+    return x, sq
+
+
+def norm_from(xs, sq, w, eps):
+    """xs [M, N] bf16, sq = xs.float() ** 2.  The mean is taken by PyTorch, the rest by the kernel."""
+    M, N = xs.shape
+    if xs.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or sq.dtype != torch.float32:
+        raise TypeError("norm_from: respect_amd builds bf16 xs / w with fp32 squares only")
+    if not (sq.is_cuda and sq.device == xs.device) or tuple(sq.shape) != (M, N) or tuple(w.shape) != (N,):
+        raise ValueError("norm_from: sq must be [M, N] and w [N], on the device of xs")
+    var = sq.mean(-1).contiguous()
+    xs = as_kernel_input(xs.contiguous(), "xs")
+    w = as_kernel_input(w.contiguous(), "w")
+    y = torch.empty((M, N), device=xs.device, dtype=torch.bfloat16)
+    rc = _lib.lib().rspx_norm_apply(xs.data_ptr(), xs.stride(0), var.data_ptr(), w.data_ptr(), y.data_ptr(),
+                                    y.stride(0), M, N, float(eps), _lib.stream_ptr(xs.device))
+    _lib.check("rspx_norm_apply", rc)
+    return y
+
+
+def rmsnorm(x, w, eps):
+    """Prefill RMSNorm: squares in a kernel, mean by PyTorch, normalisation in a kernel."""
+    xs = _bf16_rows(x, "x")
+    return norm_from(xs, _square(xs), w, eps).reshape(x.shape)
+
+
+def rope_vision(x, cos, sin):
+    """One tensor of apply_rotary_pos_emb_vision: x [L, NH, D] bf16, cos/sin [L, D];
+    computed in float32, returned in bf16."""
+    if x.dtype != torch.bfloat16:
+        raise TypeError("rope_vision: respect_amd builds the bf16 path only")
+    L, NH, D = x.shape
+    x = as_kernel_input(x, "x")
+    if not (cos.is_cuda and sin.is_cuda and cos.device == x.device and sin.device == x.device):
+        raise RuntimeError("rope_vision: cos/sin must be GPU tensors on the device of x")
+    cos, sin = cos.float().reshape(L, D).contiguous(), sin.float().reshape(L, D).contiguous()
+    y = torch.empty((L, NH, D), device=x.device, dtype=torch.bfloat16)
+    rc = _lib.lib().rspx_rope_vision(x.data_ptr(), x.stride(0), x.stride(1), cos.data_ptr(), sin.data_ptr(),
+                                     cos.stride(0), y.data_ptr(), L, NH, D, _lib.stream_ptr(x.device))
+    _lib.check("rspx_rope_vision", rc)
+    return y

@@ -53,3 +53,46 @@ def test_silu_mul_vs_torch_and_limits():
     assert bf16.ulp_diff(ours, ref, 1e-30).max() <= 1.0
     z = N.silu_mul(np.array([0.0, 200.0, -200.0], np.float32), np.ones(3, np.float32))
     assert z[0] == 0 and z[1] == 200.0 and z[2] == 0
+
+
+def test_prefill_square_and_add_sq_bitwise_vs_torch():
+    rng = np.random.default_rng(5)
+    r = gen.bf16_normal(rng, (7, 256))
+    h = gen.bf16_normal(rng, (7, 256))
+    assert np.array_equal(N.square(r), (_t(r).float() ** 2).numpy())
+    x, q = N.add_sq(r, h)
+    xt = _t(r) + _t(h)                       # bf16 add on the CPU: fp32 add, one rounding
+    assert np.array_equal(x, xt.float().numpy())
+    assert np.array_equal(q, (xt.float() ** 2).numpy())
+
+
+def test_prefill_norm_apply_vs_torch_and_exact_rsqrt():
+    rng = np.random.default_rng(6)
+    x = gen.bf16_normal(rng, (16, 512))
+    w = bf16.round_bf16(1 + 0.02 * rng.standard_normal(512).astype(np.float32))
+    var = (x.astype(np.float32) ** 2).mean(-1).astype(np.float32)
+    ours = N.norm_apply(x, var, w, 1e-6)
+    xt = _t(x).float()
+    ref = (_t(w) * (xt * torch.rsqrt(torch.from_numpy(var)[:, None] + 1e-6)).to(torch.bfloat16)).float().numpy()
+    assert bf16.ulp_diff(ours, ref).max() <= 1.0
+    # var + eps = 4^k: rsqrt is exact, so y = bf16(w * bf16(x * 2^-k)) exactly
+    v = np.array([4.0, 0.25, 16.0, 1.0], np.float32)
+    xs = gen.bf16_normal(rng, (4, 64))
+    wn = bf16.round_bf16(np.linspace(0.5, 1.5, 64).astype(np.float32))
+    y = N.norm_apply(xs, v, wn, 0.0)
+    exact = bf16.round_bf16(wn * bf16.round_bf16(xs * (1.0 / np.sqrt(v))[:, None].astype(np.float32)))
+    assert np.array_equal(y, exact)
+
+
+def test_prefill_rope_vision_bitwise_vs_hf_formula():
+    rng = np.random.default_rng(7)
+    L, NH, D = 9, 3, 80
+    x = gen.bf16_normal(rng, (L, NH, D))
+    ang = rng.standard_normal((L, D)).astype(np.float32)
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    ours = N.rope_vision(x, cos, sin)
+    q = _t(x).float()
+    c, s = torch.from_numpy(cos)[:, None], torch.from_numpy(sin)[:, None]
+    rot = torch.cat((-q[..., D // 2:], q[..., :D // 2]), dim=-1)
+    ref = ((q * c) + (rot * s)).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(ours, ref)
