@@ -14,8 +14,10 @@ Test infrastructure only: it checks the wiring of the GPU decoder (which
 projection rows are q, k, v; where RoPE applies; which slots a row sees),
 not bits -- bitwise parity of the GPU path is against its own 1-token path.
 Pinned by: its pieces are oracle.norm (pinned against PyTorch) and exact
-float64 attention; tests/test_oracle_decoder.py checks it against a direct
-one-token computation on a one-layer model.
+float64 attention; tests/test_oracle_decoder.py checks, on tiny models, that
+its batched forward equals its own token-by-token forward, that the cache
+slot layout does not matter, and that with a single visible key the q/k
+weights cannot change the logits (the attention output is that key's value).
 """
 from __future__ import annotations
 
