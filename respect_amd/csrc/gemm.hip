@@ -11,8 +11,10 @@
 //   ((c0 + c1) + c2) + ..., then rounded once to the output type.
 // So a row's output bits do not depend on how many rows the call carries.
 //
-// Work split: workgroup = (64 output columns, chunk s, 64-row tile), 4 waves
-// of 16 columns each.  W -- the large operand, read exactly once -- goes
+// Work split: workgroup = (16 W output columns, chunk s, 64-row tile), W = 4
+// or 8 waves of 16 columns each (the host picks W per shape for speed; the
+// chunk count S comes from 64-column tiles whatever W is, so W never changes
+// a bit of the result).  W -- the large operand, read exactly once -- goes
 // straight from HBM into the MFMA A operand registers (lane (n16, g4) loads
 // W[col n16][k + 8 g4, +8): 16 contiguous bytes), double-buffered in rounds
 // of 8 k-blocks.  X (at most 64 rows) is shared by the 4 waves: each round of
@@ -30,8 +32,8 @@ namespace rspx {
 
 namespace gemm {
 
-constexpr int kCols = 64;      // output columns per workgroup (4 waves x 16)
-constexpr int kRows = 64;      // rows per workgroup (4 MFMA tiles)
+constexpr int kSplitCols = 64;  // column tile the chunk count S is derived from
+constexpr int kRows = 64;       // rows per workgroup (4 MFMA tiles)
 constexpr int kRoundKB = 8;    // k-blocks of 32 per round
 constexpr int kRoundK = 32 * kRoundKB;
 
@@ -57,9 +59,6 @@ struct Args {
 
 constexpr int kOOB = 0x7ffffff0;  // a buffer offset past any descriptor: loads return 0, touch nothing
 
-__device__ __forceinline__ void vm_wait16() {
-  __builtin_amdgcn_s_waitcnt((16 & 15) | ((16 >> 4) << 14) | 0x70 | 0xF00);  // vmcnt(16)
-}
 __device__ __forceinline__ void vm_wait0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 __device__ __forceinline__ void raw_barrier() {
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
@@ -84,17 +83,21 @@ __device__ __forceinline__ void round_compute(const lds_char_t* xb, const u32x4 
   }
 }
 
-// X chunks of round rr into LDS buffer xb: wave w issues row tile t = w,
-// k-blocks 0..7 (rows 16 t + n16, k [8 g4, +8) of the block).  W loads of
-// round rr into registers.  Rounds past the chunk and rows past M use
-// out-of-range offsets: zeros, no memory traffic.  Every wave issues exactly
-// 8 X chunks and 8 W loads per round on every path, so the waits below are
-// exact counts.
+// X chunks of round rr into LDS buffer xb: the 32 chunks (k-block kb, row
+// tile t) of a round are spread over the W waves, wave w taking row tile
+// t = w % 4 and k-blocks w / 4 + (W / 4) j (rows 16 t + n16, k [8 g4, +8) of
+// the block).  W loads of round rr into registers.  Rounds past the chunk and
+// rows past M use out-of-range offsets: zeros, no memory traffic.  Every wave
+// issues exactly 32 / W X chunks and 8 W loads per round on every path, so
+// the waits below are exact counts.
+template <int W>
 __device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t rx, int xoff, int rr, int nr, lds_char_t* xb, int w) {
   const bool live = rr < nr;
 #pragma unroll
-  for (int kb = 0; kb < kRoundKB; ++kb)
-    x_dma16(rx, live ? xoff + 2 * (rr * kRoundK + 32 * kb) : kOOB, xb + (kb * 4 + w) * 1024);
+  for (int j = 0; j < 32 / W; ++j) {
+    const int kb = (w >> 2) + (W / 4) * j;
+    x_dma16(rx, live ? xoff + 2 * (rr * kRoundK + 32 * kb) : kOOB, xb + (kb * 4 + (w & 3)) * 1024);
+  }
   asm volatile("" ::: "memory");
 }
 __device__ __forceinline__ void issue_w(__amdgpu_buffer_rsrc_t rw, int woff, int rr, int nr, u32x4 (&wf)[kRoundKB]) {
@@ -106,22 +109,23 @@ __device__ __forceinline__ void issue_w(__amdgpu_buffer_rsrc_t rw, int woff, int
   asm volatile("" ::: "memory");
 }
 
-// s_waitcnt vmcnt(n) for the counts the unrolled pipeline uses.
+// s_waitcnt vmcnt(n) for the counts the pipeline uses (multiples of 4, <= 32;
+// n is a compile-time constant wherever it is called, so one case remains).
+#define RSPX_VMW(v) __builtin_amdgcn_s_waitcnt(((v) & 15) | (((v) >> 4) << 14) | 0x70 | 0xF00)
 __device__ __forceinline__ void vm_wait_n(int n) {
   switch (n) {
-    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-    case 8: __builtin_amdgcn_s_waitcnt(8 | 0x70 | 0xF00); break;
-    case 16: __builtin_amdgcn_s_waitcnt((16 & 15) | ((16 >> 4) << 14) | 0x70 | 0xF00); break;
-    case 24: __builtin_amdgcn_s_waitcnt((24 & 15) | ((24 >> 4) << 14) | 0x70 | 0xF00); break;
-    default: __builtin_amdgcn_s_waitcnt((32 & 15) | ((32 >> 4) << 14) | 0x70 | 0xF00); break;
+    case 0: RSPX_VMW(0); break;
+    case 4: RSPX_VMW(4); break;
+    case 8: RSPX_VMW(8); break;
+    case 12: RSPX_VMW(12); break;
+    case 16: RSPX_VMW(16); break;
+    case 20: RSPX_VMW(20); break;
+    case 24: RSPX_VMW(24); break;
+    case 28: RSPX_VMW(28); break;
+    default: RSPX_VMW(32); break;
   }
 }
-__device__ __forceinline__ void vm_wait24() {
-  __builtin_amdgcn_s_waitcnt((24 & 15) | ((24 >> 4) << 14) | 0x70 | 0xF00);  // vmcnt(24)
-}
-__device__ __forceinline__ void vm_wait32() {
-  __builtin_amdgcn_s_waitcnt((32 & 15) | ((32 >> 4) << 14) | 0x70 | 0xF00);  // vmcnt(32)
-}
+#undef RSPX_VMW
 
 // Pipeline: W (the HBM stream) is requested 3 rounds ahead into a ring of 4
 // register buffers, X (L2-resident) 1 round ahead into 2 LDS buffers.  Round
@@ -129,8 +133,10 @@ __device__ __forceinline__ void vm_wait32() {
 // NR > 0: the NR rounds are unrolled at compile time, so every wait count is
 // exact and the compiler's own waits for the W registers never drain the
 // prefetch; NR == 0: a run-time loop (any round count, shallower prefetch).
-template <int MT, int NR>
-__global__ __launch_bounds__(256) void gemm_kernel(Args A) {
+template <int MT, int NR, int W>
+__global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
+  constexpr int kCols = 16 * W;
+  constexpr int XPW = 32 / W;                 // X chunks per wave per round
   __shared__ __attribute__((aligned(16))) char xs[2][kRoundKB * 4 * 1024];  // 2 x 32 KB
   constexpr int XB = kRoundKB * 4 * 1024;
   const int lane = __lane_id();
@@ -152,7 +158,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(Args A) {
   const int mrows = min(kRows, A.M - row0);
   const __amdgpu_buffer_rsrc_t rx =
       rsrc(A.x + (int64_t)row0 * A.sx + k0, 2 * ((int64_t)(mrows - 1) * A.sx + (A.K - k0)));
-  const int xoff = 2 * ((16 * w + n16) * (int)A.sx + 8 * g4);
+  const int xoff = 2 * ((16 * (w & 3) + n16) * (int)A.sx + 8 * g4);
   const __amdgpu_buffer_rsrc_t rw =
       rsrc(A.w + (int64_t)(has_cols ? col : 0) * A.sw + k0, has_cols ? 2 * (15 * A.sw + A.KC) : 0);
   const int woff = 2 * (n16 * (int)A.sw + 8 * g4);
@@ -167,16 +173,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(Args A) {
     // others and the counts below would be off).  Exact wait per round: the
     // loads issued after the later of X(r) and W(r).
     u32x4 wbuf[4][kRoundKB];
-    issue_x(rx, xoff, 0, nr, xl, w);
+    issue_x<W>(rx, xoff, 0, nr, xl, w);
     issue_w(rw, woff, 0, nr, wbuf[0]);
     if constexpr (NR > 1) issue_w(rw, woff, 1, nr, wbuf[1]);
     if constexpr (NR > 2) issue_w(rw, woff, 2, nr, wbuf[2]);
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      if (r + 1 < NR) issue_x(rx, xoff, r + 1, nr, xl + ((r + 1) & 1) * XB, w);
+      if (r + 1 < NR) issue_x<W>(rx, xoff, r + 1, nr, xl + ((r + 1) & 1) * XB, w);
       if (r + 3 < NR) issue_w(rw, woff, r + 3, nr, wbuf[(r + 3) & 3]);
-      const int younger = r == 0 ? 8 * ((1 < NR) + (2 < NR) + (1 < NR) + (3 < NR))
-                                 : 8 * ((r + 2 < NR) + (r + 1 < NR) + (r + 3 < NR));
+      const int younger = r == 0 ? 8 * ((1 < NR) + (2 < NR) + (3 < NR)) + XPW * (1 < NR)
+                                 : 8 * ((r + 2 < NR) + (r + 3 < NR)) + XPW * (r + 1 < NR);
       vm_wait_n(younger);
       raw_barrier();
       round_compute<MT>(xl + (r & 1) * XB, wbuf[r & 3], acc, lane);
@@ -184,19 +190,19 @@ __global__ __launch_bounds__(256) void gemm_kernel(Args A) {
     }
   } else {
     u32x4 wa[kRoundKB], wb[kRoundKB];
-    issue_x(rx, xoff, 0, nr, xl, w);
+    issue_x<W>(rx, xoff, 0, nr, xl, w);
     issue_w(rw, woff, 0, nr, wa);
     for (int r = 0; r < nr; r += 2) {
-      issue_x(rx, xoff, r + 1, nr, xl + XB, w);
+      issue_x<W>(rx, xoff, r + 1, nr, xl + XB, w);
       issue_w(rw, woff, r + 1, nr, wb);
-      vm_wait16();
+      vm_wait_n(8 + XPW);
       raw_barrier();
       round_compute<MT>(xl, wa, acc, lane);
       raw_barrier();
       if (r + 1 >= nr) break;
-      issue_x(rx, xoff, r + 2, nr, xl, w);
+      issue_x<W>(rx, xoff, r + 2, nr, xl, w);
       issue_w(rw, woff, r + 2, nr, wa);
-      vm_wait16();
+      vm_wait_n(8 + XPW);
       raw_barrier();
       round_compute<MT>(xl + XB, wb, acc, lane);
       raw_barrier();
@@ -247,7 +253,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* part, int S, i
 // until the grid has >= 256 workgroups per 64-row tile, at most 8, each chunk
 // a whole number of 256-wide rounds.
 static int linear_splits(int N, int K) {
-  const int nt = (N + gemm::kCols - 1) / gemm::kCols;
+  const int nt = (N + gemm::kSplitCols - 1) / gemm::kSplitCols;
   int S = 1;
   while (nt * S < 256 && S < 8 && K % (gemm::kRoundK * 2 * S) == 0) S *= 2;
   return S;
@@ -278,29 +284,38 @@ static int linear_launch(const void* x, int64_t sx, const void* w, int64_t sw, v
   a.out = out; a.so = so;
   a.part = part;
   a.M = M; a.N = N; a.K = K; a.S = S; a.KC = K / S; a.out_fp32 = out_fp32 ? 1 : 0; a.to_part = to_part;
-  const int NT = (N + gemm::kCols - 1) / gemm::kCols;
   const int MTILES = (M + gemm::kRows - 1) / gemm::kRows;
+  // 8 waves (128 columns) share each X round between twice the columns; worth
+  // it while the grid keeps >= 192 workgroups, and for the widest layers
+  // (the vocabulary head) only when the X block is large (many rows).
+  const int wg8 = (N + 127) / 128 * S;
+  const int waves = (wg8 >= 192 && (M >= 32 || wg8 < 1024)) ? 8 : 4;
+  const int NT = (N + 16 * waves - 1) / (16 * waves);
   const int64_t grid = (int64_t)NT * S * MTILES;
   if (grid > 0x7fffffff) return RSPX_EUNSUPPORTED;
   const int mt = (MTILES > 1 || M >= 64) ? 4 : (M + 15) / 16;  // row tiles per 64-row tile
   const int nr = a.KC / gemm::kRoundK;
-  const dim3 g((unsigned)grid), b(256);
-#define RSPX_GEMM_NR(MTV)                                                                         \
+  const dim3 g((unsigned)grid), b(64 * waves);
+#define RSPX_GEMM_NR(MTV, WV)                                                                     \
   switch (nr) {                                                                                  \
-    case 1: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 1>), g, b, 0, s, a); break;               \
-    case 2: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 2>), g, b, 0, s, a); break;               \
-    case 3: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 3>), g, b, 0, s, a); break;               \
-    case 4: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 4>), g, b, 0, s, a); break;               \
-    case 6: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 6>), g, b, 0, s, a); break;               \
-    case 8: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 8>), g, b, 0, s, a); break;               \
-    case 12: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 12>), g, b, 0, s, a); break;             \
-    case 16: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 16>), g, b, 0, s, a); break;             \
-    default: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 0>), g, b, 0, s, a); break;              \
+    case 1: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 1, WV>), g, b, 0, s, a); break;           \
+    case 2: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 2, WV>), g, b, 0, s, a); break;           \
+    case 3: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 3, WV>), g, b, 0, s, a); break;           \
+    case 4: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 4, WV>), g, b, 0, s, a); break;           \
+    case 6: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 6, WV>), g, b, 0, s, a); break;           \
+    case 8: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 8, WV>), g, b, 0, s, a); break;           \
+    case 12: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 12, WV>), g, b, 0, s, a); break;         \
+    case 16: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 16, WV>), g, b, 0, s, a); break;         \
+    default: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 0, WV>), g, b, 0, s, a); break;          \
   }
-  if (mt == 4) { RSPX_GEMM_NR(4) }
-  else if (mt == 3) { RSPX_GEMM_NR(3) }
-  else if (mt == 2) { RSPX_GEMM_NR(2) }
-  else { RSPX_GEMM_NR(1) }
+#define RSPX_GEMM_MT(WV)                 \
+  if (mt == 4) { RSPX_GEMM_NR(4, WV) }   \
+  else if (mt == 3) { RSPX_GEMM_NR(3, WV) } \
+  else if (mt == 2) { RSPX_GEMM_NR(2, WV) } \
+  else { RSPX_GEMM_NR(1, WV) }
+  if (waves == 8) { RSPX_GEMM_MT(8) }
+  else { RSPX_GEMM_MT(4) }
+#undef RSPX_GEMM_MT
 #undef RSPX_GEMM_NR
   if (S > 1 && !to_part) {
     const int64_t quads = (int64_t)M * N / 4;
