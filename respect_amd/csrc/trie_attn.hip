@@ -375,8 +375,9 @@ struct PromptLds {
 // memory.  Wave w: row half h = w / 4 (kRT tiles of 16 rows), key quarter
 // k = w % 4 (steps 4 i + k of the group).  ATOMIC: the partial is stored with
 // agent-scope atomic stores (write-through) for a merge inside the same launch.
-template <int D, int kRT, bool ATOMIC>
-__device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, int g, int rb, int q) {
+template <int D, int kRT, bool ATOMIC, class Hook>
+__device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, int g, int rb, int q,
+                                             const Hook& before_stores) {
   using G = StepGeom<D>;
   using L = PromptLds<D, kRT>;
   constexpr int DQ = G::DQ, DT = G::DT;
@@ -637,18 +638,29 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
   lds_barrier();
   // Every wave stores staged rows with 16-byte stores, 1 KB (RPI rows) per
   // instruction; ATOMIC: with the coherence of an agent-scope atomic store.
+  // The staged rows are read into registers first: `before_stores` may then
+  // issue direct-to-LDS loads into the first half of the ring (free from here
+  // on) without an LDS read of this function waiting for them.
   constexpr int RPI = 1024 / (4 * D);
   constexpr int NST = 32 * kRT / RPI;
+  static_assert(NST % kWavesA == 0, "every wave stores the same number of pieces");
+  constexpr int NSW = NST / kWavesA;
   const int c4 = lane % (D / 4);
+  f32x4 sv[NSW];
+#pragma unroll
+  for (int j = 0; j < NSW; ++j) {
+    const int rl = (w + kWavesA * j) * RPI + lane / (D / 4);
+    sv[j] = *(const __attribute__((address_space(3))) f32x4*)(stage + rl * RS + 4 * c4);
+  }
+  before_stores();
   const __amdgpu_buffer_rsrc_t racc = buffer_rsrc(A.gp_acc, 0x7fffffff);
-  for (int x = w; x < NST; x += kWavesA) {
-    const int rl = x * RPI + lane / (D / 4);
-    const int r = row0 + rl;
-    const f32x4 v = *(const __attribute__((address_space(3))) f32x4*)(stage + rl * RS + 4 * c4);
+#pragma unroll
+  for (int j = 0; j < NSW; ++j) {
+    const int r = row0 + (w + kWavesA * j) * RPI + lane / (D / 4);
     if (r < A.R) {
       const size_t off = (((size_t)g * A.R + r) * A.NG + q) * D + 4 * c4;
-      if constexpr (ATOMIC) __builtin_amdgcn_raw_buffer_store_b128(v, racc, (int)(off * 4), 0, 16);
-      else *reinterpret_cast<f32x4*>(A.gp_acc + off) = v;
+      if constexpr (ATOMIC) __builtin_amdgcn_raw_buffer_store_b128(sv[j], racc, (int)(off * 4), 0, 16);
+      else *reinterpret_cast<f32x4*>(A.gp_acc + off) = sv[j];
     }
   }
 }
@@ -658,7 +670,7 @@ __global__ __launch_bounds__(512) void prompt_kernel(TrieAttnArgs A) {
   __shared__ __attribute__((aligned(16))) char lds[PromptLds<D, kRT>::BYTES];
   const int g = blockIdx.x % A.HK;
   const int rest = blockIdx.x / A.HK;
-  prompt_block<D, kRT, false>(A, lds, g, rest % A.NRB, rest / A.NRB);
+  prompt_block<D, kRT, false>(A, lds, g, rest % A.NRB, rest / A.NRB, [] {});
 }
 
 // ------------------------------------------------------------------ node fold and merge
@@ -668,7 +680,16 @@ template <> struct NodeVec<4> { typedef u32x2 T; };
 
 constexpr int kChunk = 64;  // node slots staged in LDS at a time
 
-template <int D> struct NodeLds { static constexpr int BYTES = 2 * kChunk * 2 * D; };  // K rows, then V rows
+// Node LDS: the chunk's K as score fragments -- 1 KB per 16-slot tile kt and
+// 32-wide head_dim step i, lane (n16, g4)'s 16 bytes are K[16 kt + n16][32 i +
+// 8 g4, +8), read back with one ds_read_b128 -- then its V rows, then the fp32
+// scores (later p) of up to 4 kWavesA rows x kChunk slots.
+template <int D> struct NodeLds {
+  static constexpr int KBYTES = kChunk * 2 * D;
+  static constexpr int VBYTES = kChunk * 2 * D;
+  static constexpr int SROW = kChunk + 4;  // floats per score row
+  static constexpr int BYTES = KBYTES + VBYTES + 4 * kWavesA * SROW * 4;
+};
 
 // Where a row's result goes: row r of kv head g is query r / GQA of head
 // g GQA + r % GQA.  Rows past R shadow a valid row and are never stored.
@@ -685,20 +706,129 @@ __device__ __forceinline__ RowRef row_ref(const TrieAttnArgs& A, int g, int r, i
   return x;
 }
 
-// Node partial of one row per 16 lanes (lane 16 e + n holds head_dim
-// [DN n, +DN) of the wave's row e): the row's allowed node slots folded one
-// at a time in slot order, fp32 p (attention.py:52-67).  Every wave of the
-// workgroup (nw of them, this is wave w) calls it: 64-slot chunks of kv head
-// g's node K/V are copied into LDS `kv` by all of them; waves whose rows are
-// not live only help with the copies.  Ends with every vector load of the
-// calling wave complete.
+typedef __attribute__((address_space(3))) float lds_float;
+
+// Loads a caller may issue ahead of node_fold for the first chunk of its
+// first row pass (single-chunk tries only): the chunk's K/V in LDS, the score
+// fragment of the wave's task and its row's mask bytes.
+template <int D> struct NodePre {
+  bf16x8 qf[D / 32];
+  uint8_t mb[4];
+};
+
+// Chunk c0 of kv head g's node K (score fragments) and, if `withv`, V rows
+// into LDS `kv`: 1 KB pieces x = w, w + nw, ...  Slots past NN read zeros.
 template <int D>
-__device__ __forceinline__ void node_fold(const TrieAttnArgs& A, int g, const RowRef& R, lds_char* kv, int w, int nw,
+__device__ __forceinline__ void node_issue(const TrieAttnArgs& A, int g, int c0, lds_char* kv, int w, int nw,
+                                           bool withv) {
+  constexpr int DQ = D / 32, RB = 2 * D;
+  constexpr int KX = NodeLds<D>::KBYTES / 1024, VX = NodeLds<D>::VBYTES / 1024;
+  const int lane = __lane_id();
+  const int left = A.NN - c0 - 1;
+  const __amdgpu_buffer_rsrc_t rk =
+      buffer_rsrc(A.kn + g * A.sknh + (int64_t)c0 * A.sknn, 2 * ((int64_t)left * A.sknn + D));
+  const __amdgpu_buffer_rsrc_t rv =
+      buffer_rsrc(A.vn + g * A.svnh + (int64_t)c0 * A.svnn, 2 * ((int64_t)left * A.svnn + D));
+  const int nx = withv ? KX + VX : KX;
+  for (int x = w; x < nx; x += nw) {
+    if (x < KX) {
+      const int slot = 16 * (x / DQ) + (lane & 15);
+      bdma16(rk, 2 * (slot * (int)A.sknn + 32 * (x % DQ) + 8 * (lane >> 4)), kv + x * 1024);
+    } else {
+      const int byte = (x - KX) * 1024 + 16 * lane;
+      bdma16(rv, 2 * (byte / RB) * (int)A.svnn + byte % RB, kv + x * 1024);
+    }
+  }
+}
+
+// Score fragment of tile rt of the pass starting at row p0: lane (n16, g4)
+// holds head_dim [32 i + 8 g4, +8) of pass row 16 rt + n16 (rows at or past
+// rend shadow row p0).
+template <int D>
+__device__ __forceinline__ void node_q(const TrieAttnArgs& A, int g, int p0, int rend, int rt,
+                                       bf16x8 (&qf)[D / 32]) {
+  const int lane = __lane_id();
+  const int r = p0 + 16 * rt + (lane & 15);
+  const RowRef R = row_ref(A, g, r < rend ? r : p0, p0);
+  const uint16_t* qp = A.q + R.hd * A.sqh + (int64_t)R.mq * A.sqm + 8 * (lane >> 4);
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) qf[i] = *reinterpret_cast<const bf16x8*>(qp + 32 * i);
+}
+
+// Row R's mask bytes of chunk c0: lane (e, n) gets slots c0 + 16 b + n.
+__device__ __forceinline__ void node_mask(const TrieAttnArgs& A, const RowRef& R, int c0, uint8_t (&mb)[4]) {
+  const int n = __lane_id() & 15;
+  const uint8_t* mrow = A.msk + (int64_t)R.mq * A.smm;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int t = c0 + 16 * b + n;
+    mb[b] = (R.live && t < A.NN) ? mrow[(int64_t)t * A.smn] : (uint8_t)0;
+  }
+}
+
+// Scores q.k times A.c of the pass's rows and chunk c0's slots into S
+// ([row][SROW], fp32) with one 16x16x32 MFMA chain per task (row tile rt,
+// slot tile kt); waves take tasks w, w + nw, ...  With use_pre, `qpre` is the
+// fragment of task w.  Each score depends only on its row's q and its slot's
+// k: neither the tile nor the lane position changes its bits.
+template <int D>
+__device__ __forceinline__ void node_scores(const TrieAttnArgs& A, int g, int p0, int rend, int c0,
+                                            const lds_char* kv, lds_float* S, int w, int nw,
+                                            const bf16x8 (&qpre)[D / 32], bool use_pre) {
+  constexpr int DQ = D / 32;
+  const int lane = __lane_id();
+  const int nrt = (min(rend - p0, 4 * nw) + 15) / 16;
+  const int nkt = min(kChunk, A.NN - c0 + 15) / 16;
+  for (int t = w; t < 4 * nrt; t += nw) {
+    const int rt = t >> 2, kt = t & 3;
+    if (kt >= nkt) continue;
+    bf16x8 qf[DQ];
+    if (use_pre && t == w) {
+#pragma unroll
+      for (int i = 0; i < DQ; ++i) qf[i] = qpre[i];
+    } else {
+      node_q<D>(A, g, p0, rend, rt, qf);
+    }
+    f32x4 sv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) {
+      const bf16x8 a = *(const __attribute__((address_space(3))) bf16x8*)(kv + (kt * DQ + i) * 1024 + 16 * lane);
+      sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[i], sv, 0, 0, 0);
+    }
+    // Lane (n16, g4), element j: slot 16 kt + 4 g4 + j of pass row 16 rt + n16.
+    const f32x4 o = sv * A.c;
+    *(__attribute__((address_space(3))) f32x4*)(S + (16 * rt + (lane & 15)) * NodeLds<D>::SROW + 16 * kt +
+                                                4 * (lane >> 4)) = o;
+  }
+}
+
+__device__ __forceinline__ float max16(float x) {
+  x = fmaxf(x, dpp<0xB1>(x));
+  x = fmaxf(x, dpp<0x4E>(x));
+  x = fmaxf(x, dpp<0x141>(x));
+  x = fmaxf(x, dpp<0x140>(x));
+  return x;
+}
+
+// Node partial of one row per 16 lanes (lane 16 e + n holds head_dim
+// [DN n, +DN) of pass row 4 w + e, described by R) over the row's allowed node
+// slots (attention.py:52-67): m is the maximum score over every allowed slot,
+// p = exp2(score - m) in fp32, and l and acc are sums over the allowed slots
+// taken one at a time in slot order -- every bit depends only on the ordered
+// list of the row's allowed (k, v), not on where in the node area they sit.
+// Every wave of the workgroup (nw of them, this is wave w) calls it for the
+// pass of rows [p0, p0 + 4 nw) clipped to rend; waves whose rows are not live
+// help with the copies and score tiles.  With more than one chunk a first
+// pass over K finds m.  have_pre: chunk 0 (the only one) was issued by the
+// caller into `pre` and LDS (node_prefetch).  Ends with every
+// vector load of the calling wave complete.
+template <int D>
+__device__ __forceinline__ void node_fold(const TrieAttnArgs& A, int g, int p0, int rend, const RowRef& R,
+                                          lds_char* kv, int w, int nw, const NodePre<D>& pre, bool have_pre,
                                           float& m, float& l, float (&acc)[D / 16]) {
   constexpr int DN = D / 16;
   constexpr int RB = 2 * D;                          // bytes per node row
-  constexpr int CHB = kChunk * RB;                   // bytes of K (or V) per chunk
-  constexpr int kB = 8;                              // slots per fold batch
+  constexpr int kB = 8;                              // slots per accumulation batch
   typedef typename NodeVec<DN>::T VecT;
   constexpr int NW = DN / 2;                         // 32-bit words per lane vector
   const int lane = __lane_id();
@@ -710,35 +840,61 @@ __device__ __forceinline__ void node_fold(const TrieAttnArgs& A, int g, const Ro
 #pragma unroll
   for (int i = 0; i < DN; ++i) acc[i] = 0.f;
   if (NN == 0) return;
+  lds_float* S = (lds_float*)(kv + NodeLds<D>::KBYTES + NodeLds<D>::VBYTES);
+  lds_float* Srow = S + (4 * w + e) * NodeLds<D>::SROW;
+  const lds_char* vl = kv + NodeLds<D>::KBYTES;
+  const bool one = NN <= kChunk;
 
-  float qf[DN];
-  {
-    const VecT qv = *reinterpret_cast<const VecT*>(A.q + R.hd * A.sqh + (int64_t)R.mq * A.sqm + d0);
+  if (!one) {
+    for (int c0 = 0; c0 < NN; c0 += kChunk) {
+      if (c0 > 0) lds_barrier();  // every wave is done with the previous chunk's scores
+      node_issue<D>(A, g, c0, kv, w, nw, false);
+      uint8_t mb[4];
+      node_mask(A, R, c0, mb);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      lds_barrier();
+      node_scores<D>(A, g, p0, rend, c0, kv, S, w, nw, pre.qf, false);
+      lds_barrier();
+      float x = kNegInf;
 #pragma unroll
-    for (int i = 0; i < NW; ++i) { qf[2 * i] = bf16_lo(qv[i]); qf[2 * i + 1] = bf16_hi(qv[i]); }
+      for (int b = 0; b < 4; ++b)
+        if (mb[b]) x = fmaxf(x, Srow[16 * b + n]);
+      m = fmaxf(m, max16(x));
+    }
+    lds_barrier();
   }
-  const uint8_t* mrow = A.msk + (int64_t)R.mq * A.smm;
-  const uint16_t* knb = A.kn + g * A.sknh;
-  const uint16_t* vnb = A.vn + g * A.svnh;
 
   for (int c0 = 0; c0 < NN; c0 += kChunk) {
     if (c0 > 0) lds_barrier();  // every wave is done with the previous chunk
-    // Row e's mask bytes of the chunk: lane (e, n) tests slots c0 + 16 b + n.
+    const bool pf = have_pre && one;
     uint8_t mb[4];
+    if (pf) {
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int t = c0 + 16 * b + n;
-      mb[b] = (R.live && t < NN) ? mrow[(int64_t)t * A.smn] : (uint8_t)0;
+      for (int b = 0; b < 4; ++b) mb[b] = pre.mb[b];
+    } else {
+      node_issue<D>(A, g, c0, kv, w, nw, true);
+      node_mask(A, R, c0, mb);
     }
-    // The chunk's K and V rows into LDS: 1 KB pieces x = w, w + nw, ...
-    const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(knb + (int64_t)c0 * A.sknn, 2 * ((int64_t)(NN - c0 - 1) * A.sknn + D));
-    const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(vnb + (int64_t)c0 * A.svnn, 2 * ((int64_t)(NN - c0 - 1) * A.svnn + D));
-    for (int x = w; x < 2 * CHB / 1024; x += nw) {
-      const int byte = (x * 1024 + 16 * lane) % CHB;
-      const int slot = byte / RB, unit = (byte % RB) / 16;
-      if (x * 1024 < CHB) bdma16(rk, 2 * slot * (int)A.sknn + 16 * unit, kv + x * 1024);
-      else bdma16(rv, 2 * slot * (int)A.svnn + 16 * unit, kv + x * 1024);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of the chunk is in LDS
+    lds_barrier();                       // and every other wave's part
+    node_scores<D>(A, g, p0, rend, c0, kv, S, w, nw, pre.qf, pf);
+    lds_barrier();
+
+    float s4[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) s4[b] = Srow[16 * b + n];
+    if (one) {
+      float x = kNegInf;
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        if (mb[b]) x = fmaxf(x, s4[b]);
+      m = max16(x);
     }
+    // p of the row's allowed slots back into the row's scores (the row's
+    // lanes are the only readers, all in this wave).
+#pragma unroll
+    for (int b = 0; b < 4; ++b) Srow[16 * b + n] = mb[b] ? fexp2(s4[b] - m) : 0.f;
+
     uint64_t mm = 0;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -747,8 +903,6 @@ __device__ __forceinline__ void node_fold(const TrieAttnArgs& A, int g, const Ro
     }
     const int cnt = __builtin_popcountll(mm);
     const int cmax = max(max(__shfl(cnt, 0), __shfl(cnt, 16)), max(__shfl(cnt, 32), __shfl(cnt, 48)));
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of the chunk is in LDS
-    lds_barrier();                       // and every other wave's part
 
     for (int b0 = 0; b0 < cmax; b0 += kB) {
       int js[kB];
@@ -759,40 +913,40 @@ __device__ __forceinline__ void node_fold(const TrieAttnArgs& A, int g, const Ro
         js[u] = ok[u] ? __builtin_ctzll(mm) : 0;
         mm &= mm - 1;
       }
-      VecT kr[kB], vr[kB];
+      VecT vr[kB];
+      float pu[kB];
 #pragma unroll
       for (int u = 0; u < kB; ++u) {
-        kr[u] = *(const __attribute__((address_space(3))) VecT*)(kv + js[u] * RB + 2 * d0);
-        vr[u] = *(const __attribute__((address_space(3))) VecT*)(kv + CHB + js[u] * RB + 2 * d0);
-      }
-      float sc[kB];
-#pragma unroll
-      for (int u = 0; u < kB; ++u) {
-        float dot = 0.f;
-#pragma unroll
-        for (int i = 0; i < NW; ++i) {
-          dot = __builtin_fmaf(qf[2 * i], bf16_lo(kr[u][i]), dot);
-          dot = __builtin_fmaf(qf[2 * i + 1], bf16_hi(kr[u][i]), dot);
-        }
-        sc[u] = sum16(dot) * A.c;
+        vr[u] = *(const __attribute__((address_space(3))) VecT*)(vl + js[u] * RB + 2 * d0);
+        pu[u] = Srow[js[u]];
       }
 #pragma unroll
       for (int u = 0; u < kB; ++u) {
         if (ok[u]) {
-          const float mn = fmaxf(m, sc[u]);
-          const float a = fexp2(m - mn);
-          const float p = fexp2(sc[u] - mn);
-          l = __builtin_fmaf(l, a, p);
+          l += pu[u];
 #pragma unroll
           for (int i = 0; i < NW; ++i) {
-            acc[2 * i] = __builtin_fmaf(p, bf16_lo(vr[u][i]), acc[2 * i] * a);
-            acc[2 * i + 1] = __builtin_fmaf(p, bf16_hi(vr[u][i]), acc[2 * i + 1] * a);
+            acc[2 * i] = __builtin_fmaf(pu[u], bf16_lo(vr[u][i]), acc[2 * i]);
+            acc[2 * i + 1] = __builtin_fmaf(pu[u], bf16_hi(vr[u][i]), acc[2 * i + 1]);
           }
-          m = mn;
         }
       }
     }
   }
+}
+
+// Issues node_fold's chunk-0 loads for the first row pass [p0, rend) of a
+// workgroup of nw waves (call only when 0 < NN <= kChunk and p0 < rend).
+template <int D>
+__device__ __forceinline__ void node_prefetch(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv, int w,
+                                              int nw, NodePre<D>& pre) {
+  node_issue<D>(A, g, 0, kv, w, nw, true);
+  const int nrt = (min(rend - p0, 4 * nw) + 15) / 16;
+  if (w < 4 * nrt) node_q<D>(A, g, p0, rend, w >> 2, pre.qf);
+  const int r = p0 + 4 * w + (__lane_id() >> 4);
+  RowRef R = row_ref(A, g, r < rend ? r : A.R, p0);
+  R.live = r < rend;
+  node_mask(A, R, 0, pre.mb);
 }
 
 // Final result of the wave's row e: the group partials combined in group
@@ -860,7 +1014,8 @@ __global__ __launch_bounds__(64 * kWavesB) void node_merge_kernel(TrieAttnArgs A
   const int c8 = blockIdx.x - g * RC8;
   const RowRef R = row_ref(A, g, 8 * c8 + 4 * w + (lane >> 4), 8 * c8);
   float m, l, acc[D / 16];
-  node_fold<D>(A, g, R, (lds_char*)kv, w, kWavesB, m, l, acc);
+  NodePre<D> none;
+  node_fold<D>(A, g, 8 * c8, min(8 * c8 + 8, A.R), R, (lds_char*)kv, w, kWavesB, none, false, m, l, acc);
   merge_store<D>(A, g, R, m, l, acc);
 }
 
@@ -890,6 +1045,7 @@ constexpr int kSyncWords = 4096;   // timeout flag + [HK][NRB][2] counters
 template <int D, int kRT>
 __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   constexpr int LB = PromptLds<D, kRT>::BYTES > NodeLds<D>::BYTES ? PromptLds<D, kRT>::BYTES : NodeLds<D>::BYTES;
+  static_assert(NodeLds<D>::BYTES <= PromptLds<D, kRT>::RINGBYTES / 2, "node chunk prefetched into the ring's first half");
   __shared__ __attribute__((aligned(16))) char lds[LB];
   const int lane = __lane_id();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -898,17 +1054,23 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   const int rb = rest % A.NRB;
   const int q = rest / A.NRB;
   int* cnt = A.sync + 1 + 2 * (g * A.NRB + rb);
+  const int rows_blk = 32 * kRT;
+  const int rpw = 4 * ((rows_blk / 4 + A.NG - 1) / A.NG);   // rows merged per workgroup (multiple of 4)
+  const int r0 = rb * rows_blk + q * rpw;
+  const int rend = min(rb * rows_blk + min(rows_blk, (q + 1) * rpw), A.R);
 
-  prompt_block<D, kRT, true>(A, lds, g, rb, q);
+  // A single-chunk trie's node K/V, score fragment and mask bytes are loaded
+  // while the group partial is being stored.
+  const bool pf = A.NN > 0 && A.NN <= kChunk && r0 < rend;
+  NodePre<D> pre;
+  prompt_block<D, kRT, true>(A, lds, g, rb, q, [&] {
+    if (pf) node_prefetch<D>(A, g, r0, rend, (lds_char*)lds, w, kWavesA, pre);
+  });
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
   lds_barrier();
   if (threadIdx.x == 0) __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  const int rows_blk = 32 * kRT;
-  const int rpw = 4 * ((rows_blk / 4 + A.NG - 1) / A.NG);   // rows merged per workgroup (multiple of 4)
-  const int r0 = rb * rows_blk + q * rpw;
-  const int rend = min(rb * rows_blk + min(rows_blk, (q + 1) * rpw), A.R);
   bool waited = false;
   for (int p0 = r0; p0 < rend; p0 += 4 * kWavesA) {
     if (p0 != r0) lds_barrier();  // every wave is done with the previous pass's node chunk
@@ -917,7 +1079,7 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
     RowRef Rl = row_ref(A, g, r < rend ? r : A.R, p0);   // rows of other shares shadow row p0
     Rl.live = r < rend;
     float m, l, acc[D / 16];
-    node_fold<D>(A, g, Rl, (lds_char*)lds, w, kWavesA, m, l, acc);
+    node_fold<D>(A, g, p0, rend, Rl, (lds_char*)lds, w, kWavesA, pre, pf && p0 == r0, m, l, acc);
     if (!waited) {
       if (w == 0) {
         int v = 0;
