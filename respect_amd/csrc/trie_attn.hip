@@ -61,7 +61,7 @@ constexpr int kGroupTarget = 8;  // maximum number of key groups per kv head
 constexpr float kLazyTau = 8.f;  // log2 headroom before the reference max moves
 constexpr int kMaxNodeSlots = 4096;
 constexpr int kWavesA = 8;       // waves per prompt workgroup
-constexpr int kWavesB = 2;       // waves per merge workgroup
+constexpr int kWavesB = 8;       // waves per merge workgroup (one row each)
 
 struct TrieAttnArgs {
   const uint16_t* q;  int64_t sqh, sqm;
@@ -298,75 +298,13 @@ __device__ __forceinline__ void issue_round(const uint16_t* kpg, const uint16_t*
 }
 
 // ------------------------------------------------------------------ kernel A
-// Workgroup (g, rb, q): kv head g, rows [32 kRT rb, +32 kRT), key group q =
-// steps [q S, q S + S).  Wave w: row half h = w / 4 (kRT tiles of 16 rows),
-// key quarter k = w % 4 (steps 4 i + k of the group).
-// Quarter partials in LDS: region i holds acc[t][j] as [t][j][lane] f32x4
-// (ring) and (m, l) of rows 16 t + n16 (Q area).
-template <int D, int kRT>
-__device__ __forceinline__ void quarter_put(lds_char* ring, lds_char* qreg, int region,
-                                            const f32x4 (&acc)[kRT][D / 16], const float (&mref)[kRT],
-                                            const float (&lrow)[kRT], int lane) {
-  constexpr int DT = D / 16, REG = kRT * DT * 1024, REGML = kRT * 16 * 8;
-  const int n16 = lane & 15, g4 = lane >> 4;
-#pragma unroll
-  for (int t = 0; t < kRT; ++t) {
-#pragma unroll
-    for (int j = 0; j < DT; ++j)
-      *(__attribute__((address_space(3))) f32x4*)(ring + region * REG + (t * DT + j) * 1024 + 16 * lane) = acc[t][j];
-    if (g4 == 0) {
-      __attribute__((address_space(3))) float* ml =
-          (__attribute__((address_space(3))) float*)(qreg + region * REGML) + 2 * (16 * t + n16);
-      ml[0] = mref[t];
-      ml[1] = lrow[t];
-    }
-  }
-}
-
-// state (mref, lrow, acc) <- state (+) the partial in `region`: combine() per
-// row, the row factors moved from the score layout (row n16) to the
-// accumulator layout (rows 4 g4 + e) by a lane shuffle.
-template <int D, int kRT>
-__device__ __forceinline__ void quarter_take(const lds_char* ring, const lds_char* qreg, int region,
-                                             f32x4 (&acc)[kRT][D / 16], float (&mref)[kRT], float (&lrow)[kRT],
-                                             int lane) {
-  constexpr int DT = D / 16, REG = kRT * DT * 1024, REGML = kRT * 16 * 8;
-  const int n16 = lane & 15, g4 = lane >> 4;
-#pragma unroll
-  for (int t = 0; t < kRT; ++t) {
-    const __attribute__((address_space(3))) float* ml =
-        (const __attribute__((address_space(3))) float*)(qreg + region * REGML) + 2 * (16 * t + n16);
-    const float m2 = ml[0], l2 = ml[1];
-    float a = 1.f, b = 0.f;
-    if (m2 != kNegInf) {
-      const float mn = fmaxf(mref[t], m2);
-      a = fexp2(mref[t] - mn);
-      b = fexp2(m2 - mn);
-      lrow[t] = __builtin_fmaf(l2, b, lrow[t] * a);
-      mref[t] = mn;
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float ae = shfl_idx(a, 4 * g4 + e), be = shfl_idx(b, 4 * g4 + e);
-#pragma unroll
-      for (int j = 0; j < DT; ++j) {
-        const f32x4 a2 =
-            *(const __attribute__((address_space(3))) f32x4*)(ring + region * REG + (t * DT + j) * 1024 + 16 * lane);
-        acc[t][j][e] = __builtin_fmaf(a2[e], be, acc[t][j][e] * ae);
-      }
-    }
-  }
-}
-
+// LDS of a prompt workgroup: the K/V ring, then the Q fragments.
 template <int D, int kRT>
 struct PromptLds {
   using G = StepGeom<D>;
   static constexpr int QBYTES = 2 * kRT * G::DQ * 1024;
   static constexpr int RINGBYTES = G::RING * G::ROUND;
   static constexpr int BYTES = RINGBYTES + QBYTES;
-  static_assert(4 * kRT * G::DT * 1024 <= RINGBYTES / 2, "quarter accumulators use half the ring");
-  static_assert(4 * kRT * 16 * 8 <= QBYTES, "quarter (m, l) reuse the Q area");
-  static_assert(32 * kRT * (D + 4) * 4 <= RINGBYTES / 2, "the staged group partial uses the other half");
   static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
@@ -593,74 +531,100 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
     }
   }
 
-  // Quarter partials combined as ((q0 (+) q1) (+) (q2 (+) q3)) through LDS
-  // (the ring is free once every wave is past its last step): stage 1 waves
-  // k = 1, 3 hand their partial to k = 0, 2; stage 2 wave k = 2 hands to
-  // k = 0, which stores the group partial of its row half.  A partial is
-  // acc[t][j] as [t][j][lane] f32x4 plus (m, l) of rows 16 t + n16.
-  lds_barrier();
-  if (has_rows && (k & 1)) quarter_put<D, kRT>(ring, qreg, 2 * h + (k >> 1), acc, mref, lrow, lane);
-  lds_barrier();
-  if (has_rows && !(k & 1)) quarter_take<D, kRT>(ring, qreg, 2 * h + (k >> 1), acc, mref, lrow, lane);
-  lds_barrier();
-  if (has_rows && k == 2) quarter_put<D, kRT>(ring, qreg, 2 * h, acc, mref, lrow, lane);
-  lds_barrier();
+  // Quarter partials combined in one step (the ring and the Q area are free
+  // once every wave is past its last step).  Each wave writes (m, l) of its
+  // rows, then scales its accumulators by s_k = exp2(m_k - M), M the row's
+  // maximum over the four quarters k (s_k = 0 for an empty quarter), and
+  // writes them row-major into the ring; every wave then sums a share of the
+  // block's rows over the quarters as (q0 + q1) + (q2 + q3) and stores it, with
+  // l = (l0 s0 + l1 s1) + (l2 s2 + l3 s3) beside M.
   typedef __attribute__((address_space(3))) float lds_float;
-  constexpr int RS = D + 4;  // staged row stride in floats: a write's 4 row groups land on different banks
-  lds_float* stage = (lds_float*)(ring + RINGBYTES / 2);
-  if (has_rows && k == 0) {
-    quarter_take<D, kRT>(ring, qreg, 2 * h, acc, mref, lrow, lane);
-    // Group partial of the wave's rows: (m, l) of rows 16 t + n16 from lanes
-    // g4 == 0 straight out; acc (rows 16 t + 4 g4 + e, head_dim 16 j + n16)
-    // staged row-major in the second half of the ring.
+  typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+  typedef __attribute__((address_space(3))) f32x2 lds_f32x2;
+  constexpr int BR = 32 * kRT;  // rows of the block
+  static_assert(4 * BR * D * 4 <= RINGBYTES, "the four scaled quarters fit the ring");
+  static_assert(8 * kRT * 16 * 8 <= L::QBYTES, "quarter (m, l) fit the Q area");
+  lds_float* qml = (lds_float*)qreg;    // [h][k][t][16 rows] (m, l)
+  lds_float* qacc = (lds_float*)ring;   // [k][BR rows][D], 16-column blocks swizzled by row
+  lds_barrier();
+  if (g4 == 0) {
 #pragma unroll
-    for (int t = 0; t < kRT; ++t) {
-      if (g4 == 0) {
-        const int r = trow + 16 * t + n16;
-        if (r < A.R) {
-          float* ml = A.gp_ml + (((size_t)g * A.R + r) * A.NG + q) * 2;
-          if constexpr (ATOMIC) {
-            __hip_atomic_store(ml, mref[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(ml + 1, lrow[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          } else {
-            ml[0] = mref[t];
-            ml[1] = lrow[t];
-          }
-        }
-      }
+    for (int t = 0; t < kRT; ++t)
+      *(lds_f32x2*)(qml + (((4 * h + k) * kRT + t) * 16 + n16) * 2) = f32x2{mref[t], lrow[t]};
+  }
+  lds_barrier();
+  float Mr[kRT], Lr[kRT];
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
+  for (int t = 0; t < kRT; ++t) {
+    float mk[4], lk[4], sk[4];
 #pragma unroll
-        for (int j = 0; j < DT; ++j)
-          stage[(16 * kRT * h + 16 * t + 4 * g4 + e) * RS + 16 * j + n16] = acc[t][j][e];
+    for (int kk = 0; kk < 4; ++kk) {
+      const f32x2 v = *(const lds_f32x2*)(qml + (((4 * h + kk) * kRT + t) * 16 + n16) * 2);
+      mk[kk] = v.x;
+      lk[kk] = v.y;
+    }
+    const float M = fmaxf(fmaxf(mk[0], mk[1]), fmaxf(mk[2], mk[3]));
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) sk[kk] = mk[kk] == kNegInf ? 0.f : fexp2(mk[kk] - M);
+    Mr[t] = M;
+    Lr[t] = (lk[0] * sk[0] + lk[1] * sk[1]) + (lk[2] * sk[2] + lk[3] * sk[3]);
+    const float own = k == 0 ? sk[0] : k == 1 ? sk[1] : k == 2 ? sk[2] : sk[3];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float se = shfl_idx(own, 4 * g4 + e);   // factor of row 16 t + 4 g4 + e
+      const int row = 16 * kRT * h + 16 * t + 4 * g4 + e;
+      lds_float* dst = qacc + (k * BR + row) * D;
+#pragma unroll
+      for (int j = 0; j < DT; ++j) dst[(16 * j + n16) ^ (16 * g4)] = acc[t][j][e] * se;
     }
   }
   lds_barrier();
-  // Every wave stores staged rows with 16-byte stores, 1 KB (RPI rows) per
-  // instruction; ATOMIC: with the coherence of an agent-scope atomic store.
-  // The staged rows are read into registers first: `before_stores` may then
-  // issue direct-to-LDS loads into the first half of the ring (free from here
-  // on) without an LDS read of this function waiting for them.
+  // Group partial: rows RPI x + lane / (D / 4), columns [4 c4, +4): 1 KB per
+  // store instruction; ATOMIC: with the coherence of an agent-scope atomic store.
   constexpr int RPI = 1024 / (4 * D);
-  constexpr int NST = 32 * kRT / RPI;
+  constexpr int NST = BR / RPI;
   static_assert(NST % kWavesA == 0, "every wave stores the same number of pieces");
   constexpr int NSW = NST / kWavesA;
   const int c4 = lane % (D / 4);
   f32x4 sv[NSW];
 #pragma unroll
-  for (int j = 0; j < NSW; ++j) {
-    const int rl = (w + kWavesA * j) * RPI + lane / (D / 4);
-    sv[j] = *(const __attribute__((address_space(3))) f32x4*)(stage + rl * RS + 4 * c4);
+  for (int jj = 0; jj < NSW; ++jj) {
+    const int rl = (w + kWavesA * jj) * RPI + lane / (D / 4);
+    const lds_float* src = qacc + rl * D + ((4 * c4) ^ (16 * ((rl >> 2) & 3)));
+    const f32x4 a0 = *(const lds_f32x4*)(src);
+    const f32x4 a1 = *(const lds_f32x4*)(src + BR * D);
+    const f32x4 a2 = *(const lds_f32x4*)(src + 2 * BR * D);
+    const f32x4 a3 = *(const lds_f32x4*)(src + 3 * BR * D);
+    sv[jj] = (a0 + a1) + (a2 + a3);
   }
+  if (has_rows && k == 0 && g4 == 0) {
+#pragma unroll
+    for (int t = 0; t < kRT; ++t) {
+      const int r = trow + 16 * t + n16;
+      if (r < A.R) {
+        float* ml = A.gp_ml + (((size_t)g * A.R + r) * A.NG + q) * 2;
+        if constexpr (ATOMIC) {
+          __hip_atomic_store(ml, Mr[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(ml + 1, Lr[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          ml[0] = Mr[t];
+          ml[1] = Lr[t];
+        }
+      }
+    }
+  }
+  // Every wave's ring reads are complete: `before_stores` may issue
+  // direct-to-LDS loads into the ring.
+  lds_barrier();
   before_stores();
   const __amdgpu_buffer_rsrc_t racc = buffer_rsrc(A.gp_acc, 0x7fffffff);
 #pragma unroll
-  for (int j = 0; j < NSW; ++j) {
-    const int r = row0 + (w + kWavesA * j) * RPI + lane / (D / 4);
+  for (int jj = 0; jj < NSW; ++jj) {
+    const int r = row0 + (w + kWavesA * jj) * RPI + lane / (D / 4);
     if (r < A.R) {
       const size_t off = (((size_t)g * A.R + r) * A.NG + q) * D + 4 * c4;
-      if constexpr (ATOMIC) __builtin_amdgcn_raw_buffer_store_b128(sv[j], racc, (int)(off * 4), 0, 16);
-      else *reinterpret_cast<f32x4*>(A.gp_acc + off) = sv[j];
+      if constexpr (ATOMIC) __builtin_amdgcn_raw_buffer_store_b128(sv[jj], racc, (int)(off * 4), 0, 16);
+      else *reinterpret_cast<f32x4*>(A.gp_acc + off) = sv[jj];
     }
   }
 }
@@ -683,12 +647,13 @@ constexpr int kChunk = 64;  // node slots staged in LDS at a time
 // Node LDS: the chunk's K as score fragments -- 1 KB per 16-slot tile kt and
 // 32-wide head_dim step i, lane (n16, g4)'s 16 bytes are K[16 kt + n16][32 i +
 // 8 g4, +8), read back with one ds_read_b128 -- then its V rows, then the fp32
-// scores (later p) of up to 4 kWavesA rows x kChunk slots.
+// scores of up to kMaxNodeRows rows x kChunk slots.
+constexpr int kMaxNodeRows = 64;  // a workgroup's node rows: at most one prompt row block
 template <int D> struct NodeLds {
   static constexpr int KBYTES = kChunk * 2 * D;
   static constexpr int VBYTES = kChunk * 2 * D;
   static constexpr int SROW = kChunk + 4;  // floats per score row
-  static constexpr int BYTES = KBYTES + VBYTES + 4 * kWavesA * SROW * 4;
+  static constexpr int BYTES = KBYTES + VBYTES + kMaxNodeRows * SROW * 4;
 };
 
 // Where a row's result goes: row r of kv head g is query r / GQA of head
@@ -708,12 +673,12 @@ __device__ __forceinline__ RowRef row_ref(const TrieAttnArgs& A, int g, int r, i
 
 typedef __attribute__((address_space(3))) float lds_float;
 
-// Loads a caller may issue ahead of node_fold for the first chunk of its
-// first row pass (single-chunk tries only): the chunk's K/V in LDS, the score
-// fragment of the wave's task and its row's mask bytes.
-template <int D> struct NodePre {
+// Loads a caller may issue ahead of node_rows for a single-chunk trie: the
+// chunk's K/V in LDS, the score fragment of the wave's first task and the mask
+// bytes of the wave's rows.
+template <int D, int MAXR> struct NodePre {
   bf16x8 qf[D / 32];
-  uint8_t mb[4];
+  uint8_t mb[MAXR];
 };
 
 // Chunk c0 of kv head g's node K (score fragments) and, if `withv`, V rows
@@ -741,8 +706,8 @@ __device__ __forceinline__ void node_issue(const TrieAttnArgs& A, int g, int c0,
   }
 }
 
-// Score fragment of tile rt of the pass starting at row p0: lane (n16, g4)
-// holds head_dim [32 i + 8 g4, +8) of pass row 16 rt + n16 (rows at or past
+// Score fragment of row tile rt of the rows starting at p0: lane (n16, g4)
+// holds head_dim [32 i + 8 g4, +8) of row p0 + 16 rt + n16 (rows at or past
 // rend shadow row p0).
 template <int D>
 __device__ __forceinline__ void node_q(const TrieAttnArgs& A, int g, int p0, int rend, int rt,
@@ -755,29 +720,25 @@ __device__ __forceinline__ void node_q(const TrieAttnArgs& A, int g, int p0, int
   for (int i = 0; i < D / 32; ++i) qf[i] = *reinterpret_cast<const bf16x8*>(qp + 32 * i);
 }
 
-// Row R's mask bytes of chunk c0: lane (e, n) gets slots c0 + 16 b + n.
-__device__ __forceinline__ void node_mask(const TrieAttnArgs& A, const RowRef& R, int c0, uint8_t (&mb)[4]) {
-  const int n = __lane_id() & 15;
-  const uint8_t* mrow = A.msk + (int64_t)R.mq * A.smm;
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const int t = c0 + 16 * b + n;
-    mb[b] = (R.live && t < A.NN) ? mrow[(int64_t)t * A.smn] : (uint8_t)0;
-  }
+// Mask byte of row r (below R) for slot c0 + lane; 0 past NN.
+__device__ __forceinline__ uint8_t node_mask(const TrieAttnArgs& A, int r, int c0) {
+  const int t = c0 + __lane_id();
+  return t < A.NN ? A.msk[(int64_t)(r / A.GQA) * A.smm + (int64_t)t * A.smn] : (uint8_t)0;
 }
 
-// Scores q.k times A.c of the pass's rows and chunk c0's slots into S
-// ([row][SROW], fp32) with one 16x16x32 MFMA chain per task (row tile rt,
-// slot tile kt); waves take tasks w, w + nw, ...  With use_pre, `qpre` is the
-// fragment of task w.  Each score depends only on its row's q and its slot's
-// k: neither the tile nor the lane position changes its bits.
+// Scores q.k times A.c of rows [p0, rend) (at most kMaxNodeRows) and chunk
+// c0's slots into S ([row - p0][SROW], fp32) with one 16x16x32 MFMA chain per
+// task (row tile rt, slot tile kt); waves take tasks w, w + nw, ...  With
+// use_pre, `qpre` is the fragment of task w.  Each score depends only on its
+// row's q and its slot's k: neither the tile nor the lane position changes
+// its bits.
 template <int D>
 __device__ __forceinline__ void node_scores(const TrieAttnArgs& A, int g, int p0, int rend, int c0,
                                             const lds_char* kv, lds_float* S, int w, int nw,
                                             const bf16x8 (&qpre)[D / 32], bool use_pre) {
   constexpr int DQ = D / 32;
   const int lane = __lane_id();
-  const int nrt = (min(rend - p0, 4 * nw) + 15) / 16;
+  const int nrt = (rend - p0 + 15) / 16;
   const int nkt = min(kChunk, A.NN - c0 + 15) / 16;
   for (int t = w; t < 4 * nrt; t += nw) {
     const int rt = t >> 2, kt = t & 3;
@@ -795,71 +756,91 @@ __device__ __forceinline__ void node_scores(const TrieAttnArgs& A, int g, int p0
       const bf16x8 a = *(const __attribute__((address_space(3))) bf16x8*)(kv + (kt * DQ + i) * 1024 + 16 * lane);
       sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[i], sv, 0, 0, 0);
     }
-    // Lane (n16, g4), element j: slot 16 kt + 4 g4 + j of pass row 16 rt + n16.
+    // Lane (n16, g4), element j: slot 16 kt + 4 g4 + j of row p0 + 16 rt + n16.
     const f32x4 o = sv * A.c;
     *(__attribute__((address_space(3))) f32x4*)(S + (16 * rt + (lane & 15)) * NodeLds<D>::SROW + 16 * kt +
                                                 4 * (lane >> 4)) = o;
   }
 }
 
-__device__ __forceinline__ float max16(float x) {
+__device__ __forceinline__ float max64(float x) {
   x = fmaxf(x, dpp<0xB1>(x));
   x = fmaxf(x, dpp<0x4E>(x));
   x = fmaxf(x, dpp<0x141>(x));
   x = fmaxf(x, dpp<0x140>(x));
-  return x;
+  return rows4_max(x);
 }
 
-// Node partial of one row per 16 lanes (lane 16 e + n holds head_dim
-// [DN n, +DN) of pass row 4 w + e, described by R) over the row's allowed node
-// slots (attention.py:52-67): m is the maximum score over every allowed slot,
-// p = exp2(score - m) in fp32, and l and acc are sums over the allowed slots
-// taken one at a time in slot order -- every bit depends only on the ordered
-// list of the row's allowed (k, v), not on where in the node area they sit.
-// Every wave of the workgroup (nw of them, this is wave w) calls it for the
-// pass of rows [p0, p0 + 4 nw) clipped to rend; waves whose rows are not live
-// help with the copies and score tiles.  With more than one chunk a first
-// pass over K finds m.  have_pre: chunk 0 (the only one) was issued by the
-// caller into `pre` and LDS (node_prefetch).  Ends with every
-// vector load of the calling wave complete.
-template <int D>
-__device__ __forceinline__ void node_fold(const TrieAttnArgs& A, int g, int p0, int rend, const RowRef& R,
-                                          lds_char* kv, int w, int nw, const NodePre<D>& pre, bool have_pre,
-                                          float& m, float& l, float (&acc)[D / 16]) {
-  constexpr int DN = D / 16;
+// Node lane vector: head_dim [DL l, +DL) of a row held by lane l.
+template <int DL> struct NodeLane;
+template <> struct NodeLane<2> {
+  typedef uint32_t T;
+  static __device__ __forceinline__ float at(T v, int k) { return k == 0 ? bf16_lo(v) : bf16_hi(v); }
+};
+template <> struct NodeLane<1> {
+  typedef uint16_t T;
+  static __device__ __forceinline__ float at(T v, int) { return __uint_as_float((uint32_t)v << 16); }
+};
+
+// Node partials of the wave's rows p0 + w + nw i (i < MAXR), one row at a time
+// over the whole wave: lane l holds head_dim [DL l, +DL), DL = D / 64.
+template <int D, int MAXR> struct NodePart {
+  float m[MAXR], l[MAXR], acc[MAXR][D / 64];
+};
+
+// Node partials of rows [p0, rend) of kv head g (at most kMaxNodeRows) over
+// each row's allowed node slots (attention.py:52-67): m is the maximum score
+// over every allowed slot, p = exp2(score - m) in fp32, and l and acc are sums
+// over the allowed slots taken one at a time in slot order -- every bit
+// depends only on the ordered list of the row's allowed (k, v), not on where
+// in the node area they sit.  Every wave of the workgroup (nw of them, this is
+// wave w) calls it; wave w owns rows p0 + w + nw i.  With more than one chunk
+// a first pass over K finds m.  have_pre: the single chunk was issued by the
+// caller into LDS and `pre` (node_prefetch), and the caller has since waited
+// for them (vmcnt 0) and passed a workgroup barrier.  Ends with every vector
+// load of the calling wave complete.
+template <int D, int MAXR>
+__device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv, int w,
+                                          int nw, const NodePre<D, MAXR>& pre, bool have_pre,
+                                          NodePart<D, MAXR>& np) {
+  constexpr int DL = D / 64;
   constexpr int RB = 2 * D;                          // bytes per node row
   constexpr int kB = 8;                              // slots per accumulation batch
-  typedef typename NodeVec<DN>::T VecT;
-  constexpr int NW = DN / 2;                         // 32-bit words per lane vector
+  typedef NodeLane<DL> NL;
+  typedef typename NL::T LaneT;
   const int lane = __lane_id();
-  const int e = lane >> 4, n = lane & 15;
-  const int d0 = DN * n;
   const int NN = A.NN;
-  m = kNegInf;
-  l = 0.f;
+  const int mine = (rend - p0 - w + nw - 1) / nw;   // rows of this wave
 #pragma unroll
-  for (int i = 0; i < DN; ++i) acc[i] = 0.f;
+  for (int i = 0; i < MAXR; ++i) {
+    np.m[i] = kNegInf;
+    np.l[i] = 0.f;
+#pragma unroll
+    for (int k = 0; k < DL; ++k) np.acc[i][k] = 0.f;
+  }
   if (NN == 0) return;
   lds_float* S = (lds_float*)(kv + NodeLds<D>::KBYTES + NodeLds<D>::VBYTES);
-  lds_float* Srow = S + (4 * w + e) * NodeLds<D>::SROW;
-  const lds_char* vl = kv + NodeLds<D>::KBYTES;
+  const lds_char* vl = kv + NodeLds<D>::KBYTES + DL * 2 * lane;
   const bool one = NN <= kChunk;
 
   if (!one) {
     for (int c0 = 0; c0 < NN; c0 += kChunk) {
       if (c0 > 0) lds_barrier();  // every wave is done with the previous chunk's scores
       node_issue<D>(A, g, c0, kv, w, nw, false);
-      uint8_t mb[4];
-      node_mask(A, R, c0, mb);
+      uint8_t mb[MAXR];
+#pragma unroll
+      for (int i = 0; i < MAXR; ++i) mb[i] = i < mine ? node_mask(A, p0 + w + nw * i, c0) : (uint8_t)0;
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
       lds_barrier();
       node_scores<D>(A, g, p0, rend, c0, kv, S, w, nw, pre.qf, false);
       lds_barrier();
-      float x = kNegInf;
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
-        if (mb[b]) x = fmaxf(x, Srow[16 * b + n]);
-      m = fmaxf(m, max16(x));
+      for (int i = 0; i < MAXR; ++i) {
+        if (i < mine) {
+          const float s = S[(w + nw * i) * NodeLds<D>::SROW + lane];
+          np.m[i] = fmaxf(np.m[i], max64(mb[i] ? s : kNegInf));
+        }
+      }
     }
     lds_barrier();
   }
@@ -867,167 +848,160 @@ __device__ __forceinline__ void node_fold(const TrieAttnArgs& A, int g, int p0, 
   for (int c0 = 0; c0 < NN; c0 += kChunk) {
     if (c0 > 0) lds_barrier();  // every wave is done with the previous chunk
     const bool pf = have_pre && one;
-    uint8_t mb[4];
+    uint8_t mb[MAXR];
     if (pf) {
+      // The caller waited for its loads (vmcnt 0) before a workgroup barrier.
+      // No wait here: a store or atomic it issued since may still be in flight.
 #pragma unroll
-      for (int b = 0; b < 4; ++b) mb[b] = pre.mb[b];
+      for (int i = 0; i < MAXR; ++i) mb[i] = pre.mb[i];
     } else {
       node_issue<D>(A, g, c0, kv, w, nw, true);
-      node_mask(A, R, c0, mb);
+#pragma unroll
+      for (int i = 0; i < MAXR; ++i) mb[i] = i < mine ? node_mask(A, p0 + w + nw * i, c0) : (uint8_t)0;
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of the chunk is in LDS
+      lds_barrier();                       // and every other wave's part
     }
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of the chunk is in LDS
-    lds_barrier();                       // and every other wave's part
     node_scores<D>(A, g, p0, rend, c0, kv, S, w, nw, pre.qf, pf);
     lds_barrier();
 
-    float s4[4];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) s4[b] = Srow[16 * b + n];
-    if (one) {
-      float x = kNegInf;
+    for (int i = 0; i < MAXR; ++i) {
+      if (i >= mine) continue;
+      const float s = S[(w + nw * i) * NodeLds<D>::SROW + lane];
+      const bool ok = mb[i] != 0;
+      if (one) np.m[i] = max64(ok ? s : kNegInf);
+      const float p = ok ? fexp2(s - np.m[i]) : 0.f;
+      uint64_t mm = __builtin_amdgcn_ballot_w64(ok);  // wave-uniform: the row's allowed slots
+      float l = np.l[i];
+      float acc[DL];
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
-        if (mb[b]) x = fmaxf(x, s4[b]);
-      m = max16(x);
-    }
-    // p of the row's allowed slots back into the row's scores (the row's
-    // lanes are the only readers, all in this wave).
+      for (int k = 0; k < DL; ++k) acc[k] = np.acc[i][k];
+      while (mm != 0) {
+        int js[kB];
+        bool on[kB];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) Srow[16 * b + n] = mb[b] ? fexp2(s4[b] - m) : 0.f;
-
-    uint64_t mm = 0;
+        for (int u = 0; u < kB; ++u) {
+          on[u] = mm != 0;
+          js[u] = on[u] ? __builtin_ctzll(mm) : 0;
+          mm &= mm - 1;
+        }
+        LaneT vr[kB];
+        float pu[kB];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const uint64_t bits = __builtin_amdgcn_ballot_w64(mb[b] != 0);
-      mm |= ((bits >> (16 * e)) & 0xffffull) << (16 * b);
-    }
-    const int cnt = __builtin_popcountll(mm);
-    const int cmax = max(max(__shfl(cnt, 0), __shfl(cnt, 16)), max(__shfl(cnt, 32), __shfl(cnt, 48)));
-
-    for (int b0 = 0; b0 < cmax; b0 += kB) {
-      int js[kB];
-      bool ok[kB];
+        for (int u = 0; u < kB; ++u) {
+          vr[u] = *(const __attribute__((address_space(3))) LaneT*)(vl + js[u] * RB);
+          pu[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), js[u]));
+        }
 #pragma unroll
-      for (int u = 0; u < kB; ++u) {
-        ok[u] = mm != 0;
-        js[u] = ok[u] ? __builtin_ctzll(mm) : 0;
-        mm &= mm - 1;
-      }
-      VecT vr[kB];
-      float pu[kB];
+        for (int u = 0; u < kB; ++u) {
+          if (on[u]) {
+            l += pu[u];
 #pragma unroll
-      for (int u = 0; u < kB; ++u) {
-        vr[u] = *(const __attribute__((address_space(3))) VecT*)(vl + js[u] * RB + 2 * d0);
-        pu[u] = Srow[js[u]];
-      }
-#pragma unroll
-      for (int u = 0; u < kB; ++u) {
-        if (ok[u]) {
-          l += pu[u];
-#pragma unroll
-          for (int i = 0; i < NW; ++i) {
-            acc[2 * i] = __builtin_fmaf(pu[u], bf16_lo(vr[u][i]), acc[2 * i]);
-            acc[2 * i + 1] = __builtin_fmaf(pu[u], bf16_hi(vr[u][i]), acc[2 * i + 1]);
+            for (int k = 0; k < DL; ++k) acc[k] = __builtin_fmaf(pu[u], NL::at(vr[u], k), acc[k]);
           }
         }
       }
+      np.l[i] = l;
+#pragma unroll
+      for (int k = 0; k < DL; ++k) np.acc[i][k] = acc[k];
     }
   }
 }
 
-// Issues node_fold's chunk-0 loads for the first row pass [p0, rend) of a
-// workgroup of nw waves (call only when 0 < NN <= kChunk and p0 < rend).
-template <int D>
+// Issues node_rows' loads for a single-chunk trie (0 < NN <= kChunk, p0 < rend).
+template <int D, int MAXR>
 __device__ __forceinline__ void node_prefetch(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv, int w,
-                                              int nw, NodePre<D>& pre) {
+                                              int nw, NodePre<D, MAXR>& pre) {
   node_issue<D>(A, g, 0, kv, w, nw, true);
-  const int nrt = (min(rend - p0, 4 * nw) + 15) / 16;
-  if (w < 4 * nrt) node_q<D>(A, g, p0, rend, w >> 2, pre.qf);
-  const int r = p0 + 4 * w + (__lane_id() >> 4);
-  RowRef R = row_ref(A, g, r < rend ? r : A.R, p0);
-  R.live = r < rend;
-  node_mask(A, R, 0, pre.mb);
+  if (w < 4 * ((rend - p0 + 15) / 16)) node_q<D>(A, g, p0, rend, w >> 2, pre.qf);
+  const int mine = (rend - p0 - w + nw - 1) / nw;
+#pragma unroll
+  for (int i = 0; i < MAXR; ++i) pre.mb[i] = i < mine ? node_mask(A, p0 + w + nw * i, 0) : (uint8_t)0;
 }
 
-// Final result of the wave's row e: the group partials combined in group
-// order, then the node partial (m, l, acc); bf16 store.
+// Final result of row r of kv head g, one row over the wave (lane l: head_dim
+// [DL l, +DL)): the group partials combined in group order, then the node
+// partial (m, l, acc); bf16 store.
 template <int D, bool COH = false>
-__device__ __forceinline__ void merge_store(const TrieAttnArgs& A, int g, const RowRef& R, float m, float l,
-                                            const float (&acc)[D / 16]) {
-  constexpr int DN = D / 16;
-  typedef typename NodeVec<DN>::T VecT;
-  constexpr int NW = DN / 2;
+__device__ __forceinline__ void merge_row(const TrieAttnArgs& A, int g, int r, float m, float l,
+                                          const float (&acc)[D / 64]) {
+  constexpr int DL = D / 64;
   const int lane = __lane_id();
-  const int d0 = DN * (lane & 15);
+  const RowRef R = row_ref(A, g, r, r);
   const int NG = A.NG;
-  float gm[kGroupTarget], gl[kGroupTarget];
-  f32x4 ga[kGroupTarget][DN / 4];
-  const size_t gbase = ((size_t)g * A.R + R.rr) * NG;
+  float gm[kGroupTarget], gl[kGroupTarget], ga[kGroupTarget][DL];
+  const size_t gbase = ((size_t)g * A.R + r) * NG;
   // Byte offsets of the partials fit 31 bits (checked by the host for COH).
   const __amdgpu_buffer_rsrc_t rml = buffer_rsrc(A.gp_ml, 0x7fffffff);
   const __amdgpu_buffer_rsrc_t racc = buffer_rsrc(A.gp_acc, 0x7fffffff);
 #pragma unroll
   for (int qq = 0; qq < kGroupTarget; ++qq) {
     if (qq < NG) {
+      const size_t ao = (gbase + qq) * D + DL * lane;
       if constexpr (COH) {
         // sc1 (cache policy 16): the coherence of an agent-scope atomic load.
         const f32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(rml, (int)((gbase + qq) * 8), 0, 16);
         gm[qq] = ml.x;
         gl[qq] = ml.y;
-#pragma unroll
-        for (int v = 0; v < DN / 4; ++v)
-          ga[qq][v] = __builtin_amdgcn_raw_buffer_load_b128(racc, (int)(((gbase + qq) * D + d0 + 4 * v) * 4), 0, 16);
+        if constexpr (DL == 2) {
+          const f32x2 a = __builtin_amdgcn_raw_buffer_load_b64(racc, (int)(ao * 4), 0, 16);
+          ga[qq][0] = a.x;
+          ga[qq][1] = a.y;
+        } else {
+          ga[qq][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(racc, (int)(ao * 4), 0, 16));
+        }
       } else {
         const float2 ml = *reinterpret_cast<const float2*>(A.gp_ml + (gbase + qq) * 2);
         gm[qq] = ml.x;
         gl[qq] = ml.y;
 #pragma unroll
-        for (int v = 0; v < DN / 4; ++v)
-          ga[qq][v] = *reinterpret_cast<const f32x4*>(A.gp_acc + (gbase + qq) * D + d0 + 4 * v);
+        for (int k = 0; k < DL; ++k) ga[qq][k] = A.gp_acc[ao + k];
       }
     }
   }
-  float fm = kNegInf, fl = 0.f, facc[DN];
+  float fm = kNegInf, fl = 0.f, facc[DL];
 #pragma unroll
-  for (int i = 0; i < DN; ++i) facc[i] = 0.f;
+  for (int k = 0; k < DL; ++k) facc[k] = 0.f;
 #pragma unroll
   for (int qq = 0; qq < kGroupTarget; ++qq)
-    if (qq < NG) combine<DN>(fm, fl, facc, gm[qq], gl[qq], reinterpret_cast<const float*>(ga[qq]));
-  combine<DN>(fm, fl, facc, m, l, acc);
-  if (!R.live) return;
-  VecT ov;
-#pragma unroll
-  for (int i = 0; i < NW; ++i) ov[i] = pack_bf16x2(facc[2 * i] / fl, facc[2 * i + 1] / fl);
-  *reinterpret_cast<VecT*>(A.out + R.hd * A.soh + (int64_t)R.mq * A.som + d0) = ov;
+    if (qq < NG) combine<DL>(fm, fl, facc, gm[qq], gl[qq], ga[qq]);
+  combine<DL>(fm, fl, facc, m, l, acc);
+  uint16_t* o = A.out + R.hd * A.soh + (int64_t)R.mq * A.som + DL * lane;
+  if constexpr (DL == 2) *reinterpret_cast<uint32_t*>(o) = pack_bf16x2(facc[0] / fl, facc[1] / fl);
+  else *o = f32_to_bf16_rne(facc[0] / fl);
 }
 
 // ------------------------------------------------------------------ kernel B
-// Workgroup (g, c8): rows r = 8 c8 + 4 w + e of kv head g (wave w, lane
-// 16 e + n holds head_dim [DN n, +DN) of row e): node fold, then merge.
+// Workgroup (g, c8): rows [8 c8, 8 c8 + 8) of kv head g, rows 8 c8 + w + nw i
+// on wave w: node partials, then merge.
 template <int D>
 __global__ __launch_bounds__(64 * kWavesB) void node_merge_kernel(TrieAttnArgs A) {
+  constexpr int MAXR = 8 / kWavesB;
   __shared__ __attribute__((aligned(16))) char kv[NodeLds<D>::BYTES];
-  const int lane = __lane_id();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int RC8 = (A.R + 7) / 8;
   const int g = blockIdx.x / RC8;
-  const int c8 = blockIdx.x - g * RC8;
-  const RowRef R = row_ref(A, g, 8 * c8 + 4 * w + (lane >> 4), 8 * c8);
-  float m, l, acc[D / 16];
-  NodePre<D> none;
-  node_fold<D>(A, g, 8 * c8, min(8 * c8 + 8, A.R), R, (lds_char*)kv, w, kWavesB, none, false, m, l, acc);
-  merge_store<D>(A, g, R, m, l, acc);
+  const int p0 = 8 * (blockIdx.x - g * RC8);
+  const int rend = min(p0 + 8, A.R);
+  NodePre<D, MAXR> none;
+  NodePart<D, MAXR> np;
+  node_rows<D, MAXR>(A, g, p0, rend, (lds_char*)kv, w, kWavesB, none, false, np);
+#pragma unroll
+  for (int i = 0; i < MAXR; ++i) {
+    const int r = p0 + w + kWavesB * i;
+    if (r < rend) merge_row<D>(A, g, r, np.m[i], np.l[i], np.acc[i]);
+  }
 }
 
 // ------------------------------------------------------------------ fused kernel
 // One launch: workgroup (g, rb, q) runs prompt_block, counts itself in
-// cnt[g][rb], folds the node slots of its share of the block's rows -- rows
-// q RPW .. q RPW + RPW - 1 of the block, 4 per wave -- and, once all NG groups
-// of the block are counted, merges those rows.  Every workgroup of the grid is
-// resident at once (the host launches this kernel only when the grid fits),
-// so the wait always ends; it is also bounded, and a bound reached raises a
-// flag the host can read.  The last workgroup of a block to finish its merge
-// resets the block's counters to zero.
+// cnt[g][rb], computes the node partials of its share of the block's rows --
+// rows q RPW .. q RPW + RPW - 1 of the block, row r0 + w + 8 i on wave w --
+// and, once all NG groups of the block are counted, merges those rows.  Every
+// workgroup of the grid is resident at once (the host launches this kernel
+// only when the grid fits), so the wait always ends; it is also bounded, and a
+// bound reached raises a flag the host can read.  The last workgroup of a
+// block to finish its merge resets the block's counters to zero.
 //
 // Visibility without cache-wide fences: every word that crosses workgroups
 // (group partials, counters) is written by an agent-scope atomic store or
@@ -1046,6 +1020,8 @@ template <int D, int kRT>
 __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   constexpr int LB = PromptLds<D, kRT>::BYTES > NodeLds<D>::BYTES ? PromptLds<D, kRT>::BYTES : NodeLds<D>::BYTES;
   static_assert(NodeLds<D>::BYTES <= PromptLds<D, kRT>::RINGBYTES / 2, "node chunk prefetched into the ring's first half");
+  constexpr int MAXR = 32 * kRT / kWavesA;   // node rows per wave
+  static_assert(32 * kRT <= kMaxNodeRows, "a row block fits the node score area");
   __shared__ __attribute__((aligned(16))) char lds[LB];
   const int lane = __lane_id();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1062,39 +1038,34 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   // A single-chunk trie's node K/V, score fragment and mask bytes are loaded
   // while the group partial is being stored.
   const bool pf = A.NN > 0 && A.NN <= kChunk && r0 < rend;
-  NodePre<D> pre;
+  NodePre<D, MAXR> pre;
   prompt_block<D, kRT, true>(A, lds, g, rb, q, [&] {
-    if (pf) node_prefetch<D>(A, g, r0, rend, (lds_char*)lds, w, kWavesA, pre);
+    if (pf) node_prefetch<D, MAXR>(A, g, r0, rend, (lds_char*)lds, w, kWavesA, pre);
   });
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
   lds_barrier();
   if (threadIdx.x == 0) __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  bool waited = false;
-  for (int p0 = r0; p0 < rend; p0 += 4 * kWavesA) {
-    if (p0 != r0) lds_barrier();  // every wave is done with the previous pass's node chunk
-    const int rbase = p0 + 4 * w;
-    const int r = rbase + (lane >> 4);
-    RowRef Rl = row_ref(A, g, r < rend ? r : A.R, p0);   // rows of other shares shadow row p0
-    Rl.live = r < rend;
-    float m, l, acc[D / 16];
-    node_fold<D>(A, g, p0, rend, Rl, (lds_char*)lds, w, kWavesA, pre, pf && p0 == r0, m, l, acc);
-    if (!waited) {
-      if (w == 0) {
-        int v = 0;
-        for (int it = 0; it < kSpinLimit; ++it) {
-          v = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          if (v >= A.NG) break;
-          __builtin_amdgcn_s_sleep(2);
-        }
-        if (v < A.NG && lane == 0) __hip_atomic_store(A.sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  if (r0 < rend) {
+    NodePart<D, MAXR> np;
+    node_rows<D, MAXR>(A, g, r0, rend, (lds_char*)lds, w, kWavesA, pre, pf, np);
+    if (w == 0) {
+      int v = 0;
+      for (int it = 0; it < kSpinLimit; ++it) {
+        v = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (v >= A.NG) break;
+        __builtin_amdgcn_s_sleep(2);
       }
-      lds_barrier();
-      waited = true;
+      if (v < A.NG && lane == 0) __hip_atomic_store(A.sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     }
-    if (rbase < rend) merge_store<D, true>(A, g, Rl, m, l, acc);
+    lds_barrier();
+#pragma unroll
+    for (int i = 0; i < MAXR; ++i) {
+      const int r = r0 + w + kWavesA * i;
+      if (r < rend) merge_row<D, true>(A, g, r, np.m[i], np.l[i], np.acc[i]);
+    }
   }
   // Counters back to zero once every workgroup of the block is past its wait.
   lds_barrier();
