@@ -61,7 +61,6 @@ constexpr int kGroupTarget = 8;  // maximum number of key groups per kv head
 constexpr float kLazyTau = 8.f;  // log2 headroom before the reference max moves
 constexpr int kMaxNodeSlots = 4096;
 constexpr int kWavesA = 8;       // waves per prompt workgroup
-constexpr int kWavesB = 8;       // waves per merge workgroup (one row each)
 
 struct TrieAttnArgs {
   const uint16_t* q;  int64_t sqh, sqm;
@@ -71,7 +70,7 @@ struct TrieAttnArgs {
   const uint16_t* vn; int64_t svnh, svnn;
   const uint8_t* msk; int64_t smm, smn;
   uint16_t* out;      int64_t soh, som;
-  int HK, GQA, M, P, NN;
+  int HK, GQS, M, P, NN;   // GQS = log2(query heads per kv head)
   int R, NRB, NG, S;  // rows per kv head, row blocks, groups, steps per group
   float c;            // sm_scale * log2(e)
   float* gp_ml;       // [HK][R][NG][2]  group partial (m, l)
@@ -344,8 +343,8 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
     const int T = c / DQ, i = c - T * DQ;
     const int r = row0 + 16 * T + n16;
     const int rc = r < A.R ? r : 0;
-    const int mq = rc / A.GQA, jh = rc - mq * A.GQA;
-    dma16(A.q + (int64_t)(g * A.GQA + jh) * A.sqh + (int64_t)mq * A.sqm + 32 * i + 8 * g4, qreg + c * 1024);
+    const int mq = rc >> A.GQS, jh = rc & ((1 << A.GQS) - 1);
+    dma16(A.q + (int64_t)((g << A.GQS) + jh) * A.sqh + (int64_t)mq * A.sqm + 32 * i + 8 * g4, qreg + c * 1024);
   }
 
   // This wave's chunks of a round: c = w + 8 j, step-in-round c / CH, chunk
@@ -647,14 +646,18 @@ constexpr int kChunk = 64;  // node slots staged in LDS at a time
 // Node LDS: the chunk's K as score fragments -- 1 KB per 16-slot tile kt and
 // 32-wide head_dim step i, lane (n16, g4)'s 16 bytes are K[16 kt + n16][32 i +
 // 8 g4, +8), read back with one ds_read_b128 -- then its V rows, then the fp32
-// scores of up to kMaxNodeRows rows x kChunk slots.
+// scores of up to kMaxNodeRows rows x kChunk slots, then the node partials of
+// those rows.
 constexpr int kMaxNodeRows = 64;  // a workgroup's node rows: at most one prompt row block
 template <int D> struct NodeLds {
   static constexpr int KBYTES = kChunk * 2 * D;
   static constexpr int VBYTES = kChunk * 2 * D;
   static constexpr int SROW = kChunk + 4;  // floats per score row
-  static constexpr int BYTES = KBYTES + VBYTES + kMaxNodeRows * SROW * 4;
+  static constexpr int NPOFF = KBYTES + VBYTES + kMaxNodeRows * SROW * 4;
+  static constexpr int NPROW = D + 4;      // node partial of a row: m, l, pad, pad, acc[D]
+  static constexpr int BYTES = NPOFF + kMaxNodeRows * NPROW * 4;
 };
+constexpr int kMaxRounds = kMaxNodeRows / kWavesA;  // node rows per wave
 
 // Where a row's result goes: row r of kv head g is query r / GQA of head
 // g GQA + r % GQA.  Rows past R shadow a valid row and are never stored.
@@ -666,8 +669,8 @@ __device__ __forceinline__ RowRef row_ref(const TrieAttnArgs& A, int g, int r, i
   RowRef x;
   x.live = r < A.R;
   x.rr = x.live ? r : fallback;
-  x.mq = x.rr / A.GQA;
-  x.hd = g * A.GQA + (x.rr - x.mq * A.GQA);
+  x.mq = x.rr >> A.GQS;
+  x.hd = (g << A.GQS) + (x.rr & ((1 << A.GQS) - 1));
   return x;
 }
 
@@ -676,10 +679,14 @@ typedef __attribute__((address_space(3))) float lds_float;
 // Loads a caller may issue ahead of node_rows for a single-chunk trie: the
 // chunk's K/V in LDS, the score fragment of the wave's first task and the mask
 // bytes of the wave's rows.
-template <int D, int MAXR> struct NodePre {
+template <int D> struct NodePre {
   bf16x8 qf[D / 32];
-  uint8_t mb[MAXR];
+  uint64_t mb;   // byte i: the mask byte of round i
 };
+static_assert(kMaxRounds <= 8, "mask bytes of every round in one 64-bit word");
+
+// Mask bytes of the wave's rounds for chunk c0, byte i for row p0 + w + 8 i.
+__device__ __forceinline__ uint64_t node_masks(const TrieAttnArgs& A, int p0, int nrd, int w, int c0);
 
 // Chunk c0 of kv head g's node K (score fragments) and, if `withv`, V rows
 // into LDS `kv`: 1 KB pieces x = w, w + nw, ...  Slots past NN read zeros.
@@ -723,7 +730,15 @@ __device__ __forceinline__ void node_q(const TrieAttnArgs& A, int g, int p0, int
 // Mask byte of row r (below R) for slot c0 + lane; 0 past NN.
 __device__ __forceinline__ uint8_t node_mask(const TrieAttnArgs& A, int r, int c0) {
   const int t = c0 + __lane_id();
-  return t < A.NN ? A.msk[(int64_t)(r / A.GQA) * A.smm + (int64_t)t * A.smn] : (uint8_t)0;
+  return t < A.NN ? A.msk[(int64_t)(r >> A.GQS) * A.smm + (int64_t)t * A.smn] : (uint8_t)0;
+}
+
+__device__ __forceinline__ uint64_t node_masks(const TrieAttnArgs& A, int p0, int nrd, int w, int c0) {
+  uint64_t mb = 0;
+#pragma unroll
+  for (int i = 0; i < kMaxRounds; ++i)
+    if (i < nrd) mb |= (uint64_t)node_mask(A, p0 + w + kWavesA * i, c0) << (8 * i);
+  return mb;
 }
 
 // Scores q.k times A.c of rows [p0, rend) (at most kMaxNodeRows) and chunk
@@ -782,27 +797,23 @@ template <> struct NodeLane<1> {
   static __device__ __forceinline__ float at(T v, int) { return __uint_as_float((uint32_t)v << 16); }
 };
 
-// Node partials of the wave's rows p0 + w + nw i (i < MAXR), one row at a time
-// over the whole wave: lane l holds head_dim [DL l, +DL), DL = D / 64.
-template <int D, int MAXR> struct NodePart {
-  float m[MAXR], l[MAXR], acc[MAXR][D / 64];
-};
-
 // Node partials of rows [p0, rend) of kv head g (at most kMaxNodeRows) over
 // each row's allowed node slots (attention.py:52-67): m is the maximum score
 // over every allowed slot, p = exp2(score - m) in fp32, and l and acc are sums
 // over the allowed slots taken one at a time in slot order -- every bit
 // depends only on the ordered list of the row's allowed (k, v), not on where
-// in the node area they sit.  Every wave of the workgroup (nw of them, this is
-// wave w) calls it; wave w owns rows p0 + w + nw i.  With more than one chunk
-// a first pass over K finds m.  have_pre: the single chunk was issued by the
-// caller into LDS and `pre` (node_prefetch), and the caller has since waited
-// for them (vmcnt 0) and passed a workgroup barrier.  Ends with every vector
-// load of the calling wave complete.
-template <int D, int MAXR>
+// in the node area they sit.  Every wave of the workgroup (kWavesA of them,
+// this is wave w) calls it; row p0 + w + 8 i is wave w's round i, and its
+// partial (m, l, acc) is left in the node-partial area of LDS (row i * 8 + w)
+// for the same wave to read.  With more than one chunk a first pass over K
+// finds m.  have_pre: the single chunk was issued by the caller into LDS and
+// `pre` (node_prefetch), and the caller has since waited for them (vmcnt 0)
+// and passed a workgroup barrier.  Does nothing when NN = 0.  Ends with every
+// vector load of the calling wave complete.
+template <int D>
 __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv, int w,
-                                          int nw, const NodePre<D, MAXR>& pre, bool have_pre,
-                                          NodePart<D, MAXR>& np) {
+                                          const NodePre<D>& pre, bool have_pre) {
+  constexpr int nw = kWavesA;
   constexpr int DL = D / 64;
   constexpr int RB = 2 * D;                          // bytes per node row
   constexpr int kB = 8;                              // slots per accumulation batch
@@ -810,16 +821,10 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
   typedef typename NL::T LaneT;
   const int lane = __lane_id();
   const int NN = A.NN;
-  const int mine = (rend - p0 - w + nw - 1) / nw;   // rows of this wave
-#pragma unroll
-  for (int i = 0; i < MAXR; ++i) {
-    np.m[i] = kNegInf;
-    np.l[i] = 0.f;
-#pragma unroll
-    for (int k = 0; k < DL; ++k) np.acc[i][k] = 0.f;
-  }
   if (NN == 0) return;
+  const int nrd = (rend - p0 - w + nw - 1) / nw;     // rounds of this wave
   lds_float* S = (lds_float*)(kv + NodeLds<D>::KBYTES + NodeLds<D>::VBYTES);
+  lds_float* NP = (lds_float*)(kv + NodeLds<D>::NPOFF);
   const lds_char* vl = kv + NodeLds<D>::KBYTES + DL * 2 * lane;
   const bool one = NN <= kChunk;
 
@@ -827,18 +832,19 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
     for (int c0 = 0; c0 < NN; c0 += kChunk) {
       if (c0 > 0) lds_barrier();  // every wave is done with the previous chunk's scores
       node_issue<D>(A, g, c0, kv, w, nw, false);
-      uint8_t mb[MAXR];
-#pragma unroll
-      for (int i = 0; i < MAXR; ++i) mb[i] = i < mine ? node_mask(A, p0 + w + nw * i, c0) : (uint8_t)0;
+      const uint64_t mb = node_masks(A, p0, nrd, w, c0);
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
       lds_barrier();
       node_scores<D>(A, g, p0, rend, c0, kv, S, w, nw, pre.qf, false);
       lds_barrier();
-#pragma unroll
-      for (int i = 0; i < MAXR; ++i) {
-        if (i < mine) {
-          const float s = S[(w + nw * i) * NodeLds<D>::SROW + lane];
-          np.m[i] = fmaxf(np.m[i], max64(mb[i] ? s : kNegInf));
+#pragma unroll 1
+      for (int i = 0; i < kMaxRounds; ++i) {
+        if (i < nrd) {
+          const int row = w + nw * i;
+          const bool ok = ((mb >> (8 * i)) & 0xff) != 0;
+          const float x = max64(ok ? S[row * NodeLds<D>::SROW + lane] : kNegInf);
+          lds_float* np = NP + row * NodeLds<D>::NPROW;
+          if (lane == 0) np[0] = c0 == 0 ? x : fmaxf(np[0], x);
         }
       }
     }
@@ -848,34 +854,37 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
   for (int c0 = 0; c0 < NN; c0 += kChunk) {
     if (c0 > 0) lds_barrier();  // every wave is done with the previous chunk
     const bool pf = have_pre && one;
-    uint8_t mb[MAXR];
+    uint64_t mb;
     if (pf) {
       // The caller waited for its loads (vmcnt 0) before a workgroup barrier.
       // No wait here: a store or atomic it issued since may still be in flight.
-#pragma unroll
-      for (int i = 0; i < MAXR; ++i) mb[i] = pre.mb[i];
+      mb = pre.mb;
     } else {
       node_issue<D>(A, g, c0, kv, w, nw, true);
-#pragma unroll
-      for (int i = 0; i < MAXR; ++i) mb[i] = i < mine ? node_mask(A, p0 + w + nw * i, c0) : (uint8_t)0;
+      mb = node_masks(A, p0, nrd, w, c0);
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of the chunk is in LDS
       lds_barrier();                       // and every other wave's part
     }
     node_scores<D>(A, g, p0, rend, c0, kv, S, w, nw, pre.qf, pf);
     lds_barrier();
 
-#pragma unroll
-    for (int i = 0; i < MAXR; ++i) {
-      if (i >= mine) continue;
-      const float s = S[(w + nw * i) * NodeLds<D>::SROW + lane];
-      const bool ok = mb[i] != 0;
-      if (one) np.m[i] = max64(ok ? s : kNegInf);
-      const float p = ok ? fexp2(s - np.m[i]) : 0.f;
+#pragma unroll 1
+    for (int i = 0; i < nrd; ++i) {
+      const int row = w + nw * i;
+      const bool ok = ((mb >> (8 * i)) & 0xff) != 0;
+      const float s = S[row * NodeLds<D>::SROW + lane];
+      lds_float* np = NP + row * NodeLds<D>::NPROW;
+      const float m = one ? max64(ok ? s : kNegInf) : np[0];
+      const float p = ok ? fexp2(s - m) : 0.f;
       uint64_t mm = __builtin_amdgcn_ballot_w64(ok);  // wave-uniform: the row's allowed slots
-      float l = np.l[i];
-      float acc[DL];
+      float l = 0.f, acc[DL];
 #pragma unroll
-      for (int k = 0; k < DL; ++k) acc[k] = np.acc[i][k];
+      for (int k = 0; k < DL; ++k) acc[k] = 0.f;
+      if (c0 > 0) {
+        l = np[1];
+#pragma unroll
+        for (int k = 0; k < DL; ++k) acc[k] = np[4 + DL * lane + k];
+      }
       while (mm != 0) {
         int js[kB];
         bool on[kB];
@@ -901,22 +910,24 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
           }
         }
       }
-      np.l[i] = l;
+      if (lane == 0) {
+        np[0] = m;
+        np[1] = l;
+      }
 #pragma unroll
-      for (int k = 0; k < DL; ++k) np.acc[i][k] = acc[k];
+      for (int k = 0; k < DL; ++k) np[4 + DL * lane + k] = acc[k];
     }
   }
 }
 
 // Issues node_rows' loads for a single-chunk trie (0 < NN <= kChunk, p0 < rend).
-template <int D, int MAXR>
+template <int D>
 __device__ __forceinline__ void node_prefetch(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv, int w,
-                                              int nw, NodePre<D, MAXR>& pre) {
+                                              NodePre<D>& pre) {
+  constexpr int nw = kWavesA;
   node_issue<D>(A, g, 0, kv, w, nw, true);
   if (w < 4 * ((rend - p0 + 15) / 16)) node_q<D>(A, g, p0, rend, w >> 2, pre.qf);
-  const int mine = (rend - p0 - w + nw - 1) / nw;
-#pragma unroll
-  for (int i = 0; i < MAXR; ++i) pre.mb[i] = i < mine ? node_mask(A, p0 + w + nw * i, 0) : (uint8_t)0;
+  pre.mb = node_masks(A, p0, (rend - p0 - w + nw - 1) / nw, w, 0);
 }
 
 // Final result of row r of kv head g, one row over the wave (lane l: head_dim
@@ -971,26 +982,46 @@ __device__ __forceinline__ void merge_row(const TrieAttnArgs& A, int g, int r, f
   else *o = f32_to_bf16_rne(facc[0] / fl);
 }
 
+// The node partial of wave w's round i, left in LDS by node_rows (empty when
+// there are no node slots), merged into row p0 + w + 8 i.
+template <int D, bool COH>
+__device__ __forceinline__ void merge_rounds(const TrieAttnArgs& A, int g, int p0, int rend, const lds_char* kv,
+                                             int w) {
+  constexpr int DL = D / 64;
+  const int lane = __lane_id();
+  const int nrd = (rend - p0 - w + kWavesA - 1) / kWavesA;
+  const lds_float* NP = (const lds_float*)(kv + NodeLds<D>::NPOFF);
+#pragma unroll 1
+  for (int i = 0; i < nrd; ++i) {
+    const int row = w + kWavesA * i;
+    float m = kNegInf, l = 0.f, acc[DL];
+#pragma unroll
+    for (int k = 0; k < DL; ++k) acc[k] = 0.f;
+    if (A.NN > 0) {
+      const lds_float* np = NP + row * NodeLds<D>::NPROW;
+      m = np[0];
+      l = np[1];
+#pragma unroll
+      for (int k = 0; k < DL; ++k) acc[k] = np[4 + DL * lane + k];
+    }
+    merge_row<D, COH>(A, g, p0 + row, m, l, acc);
+  }
+}
+
 // ------------------------------------------------------------------ kernel B
-// Workgroup (g, c8): rows [8 c8, 8 c8 + 8) of kv head g, rows 8 c8 + w + nw i
-// on wave w: node partials, then merge.
+// Workgroup (g, c8): rows [8 c8, 8 c8 + 8) of kv head g, row 8 c8 + w on
+// wave w: node partial, then merge.
 template <int D>
-__global__ __launch_bounds__(64 * kWavesB) void node_merge_kernel(TrieAttnArgs A) {
-  constexpr int MAXR = 8 / kWavesB;
+__global__ __launch_bounds__(64 * kWavesA) void node_merge_kernel(TrieAttnArgs A) {
   __shared__ __attribute__((aligned(16))) char kv[NodeLds<D>::BYTES];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int RC8 = (A.R + 7) / 8;
   const int g = blockIdx.x / RC8;
   const int p0 = 8 * (blockIdx.x - g * RC8);
   const int rend = min(p0 + 8, A.R);
-  NodePre<D, MAXR> none;
-  NodePart<D, MAXR> np;
-  node_rows<D, MAXR>(A, g, p0, rend, (lds_char*)kv, w, kWavesB, none, false, np);
-#pragma unroll
-  for (int i = 0; i < MAXR; ++i) {
-    const int r = p0 + w + kWavesB * i;
-    if (r < rend) merge_row<D>(A, g, r, np.m[i], np.l[i], np.acc[i]);
-  }
+  NodePre<D> none;
+  node_rows<D>(A, g, p0, rend, (lds_char*)kv, w, none, false);
+  merge_rounds<D, false>(A, g, p0, rend, (const lds_char*)kv, w);
 }
 
 // ------------------------------------------------------------------ fused kernel
@@ -1019,9 +1050,8 @@ constexpr int kSyncWords = 4096;   // timeout flag + [HK][NRB][2] counters
 template <int D, int kRT>
 __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   constexpr int LB = PromptLds<D, kRT>::BYTES > NodeLds<D>::BYTES ? PromptLds<D, kRT>::BYTES : NodeLds<D>::BYTES;
-  static_assert(NodeLds<D>::BYTES <= PromptLds<D, kRT>::RINGBYTES / 2, "node chunk prefetched into the ring's first half");
-  constexpr int MAXR = 32 * kRT / kWavesA;   // node rows per wave
-  static_assert(32 * kRT <= kMaxNodeRows, "a row block fits the node score area");
+  static_assert(NodeLds<D>::BYTES <= PromptLds<D, kRT>::RINGBYTES, "node LDS inside the ring");
+  static_assert(32 * kRT <= kMaxNodeRows, "a row block fits the node areas");
   __shared__ __attribute__((aligned(16))) char lds[LB];
   const int lane = __lane_id();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1038,9 +1068,9 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   // A single-chunk trie's node K/V, score fragment and mask bytes are loaded
   // while the group partial is being stored.
   const bool pf = A.NN > 0 && A.NN <= kChunk && r0 < rend;
-  NodePre<D, MAXR> pre;
+  NodePre<D> pre;
   prompt_block<D, kRT, true>(A, lds, g, rb, q, [&] {
-    if (pf) node_prefetch<D, MAXR>(A, g, r0, rend, (lds_char*)lds, w, kWavesA, pre);
+    if (pf) node_prefetch<D>(A, g, r0, rend, (lds_char*)lds, w, pre);
   });
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
@@ -1048,8 +1078,7 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   if (threadIdx.x == 0) __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   if (r0 < rend) {
-    NodePart<D, MAXR> np;
-    node_rows<D, MAXR>(A, g, r0, rend, (lds_char*)lds, w, kWavesA, pre, pf, np);
+    node_rows<D>(A, g, r0, rend, (lds_char*)lds, w, pre, pf);
     if (w == 0) {
       int v = 0;
       for (int it = 0; it < kSpinLimit; ++it) {
@@ -1061,11 +1090,7 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     }
     lds_barrier();
-#pragma unroll
-    for (int i = 0; i < MAXR; ++i) {
-      const int r = r0 + w + kWavesA * i;
-      if (r < rend) merge_row<D, true>(A, g, r, np.m[i], np.l[i], np.acc[i]);
-    }
+    merge_rounds<D, true>(A, g, r0, rend, (const lds_char*)lds, w);
   }
   // Counters back to zero once every workgroup of the block is past its wait.
   lds_barrier();
@@ -1152,7 +1177,7 @@ static void launch_rt(const TrieAttnArgs& a, const Plan& pl, hipStream_t s, int 
     return;
   }
   if (pl.prompt_wgs > 0) hipLaunchKernelGGL((prompt_kernel<D, RT>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);
-  hipLaunchKernelGGL((node_merge_kernel<D>), dim3(pl.node_wgs), dim3(64 * kWavesB), 0, s, a);
+  hipLaunchKernelGGL((node_merge_kernel<D>), dim3(pl.node_wgs), dim3(64 * kWavesA), 0, s, a);
 }
 
 template <int D>
@@ -1207,7 +1232,7 @@ static int trie_attn_impl(const void* q, int64_t sqh, int64_t sqm, const void* k
   a.vn = static_cast<const uint16_t*>(vn); a.svnh = svnh; a.svnn = svnn;
   a.msk = msk; a.smm = smm; a.smn = smn;
   a.out = static_cast<uint16_t*>(out); a.soh = soh; a.som = som;
-  a.HK = HK; a.GQA = pl.GQA; a.M = M; a.P = P; a.NN = NN;
+  a.HK = HK; a.GQS = __builtin_ctz(pl.GQA); a.M = M; a.P = P; a.NN = NN;
   a.R = pl.R; a.NRB = pl.NRB; a.NG = pl.NG; a.S = pl.S;
   a.c = (float)((double)sm_scale * 1.4426950408889634);
   char* ws = static_cast<char*>(workspace);
