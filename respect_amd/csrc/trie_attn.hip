@@ -168,77 +168,23 @@ __device__ __forceinline__ int vswz(int key) {
   return 2 * ((key / (16 / U)) % (U / 2));
 }
 
-__device__ __forceinline__ void wait_vm(int n) {
-  // s_waitcnt vmcnt(n); the count must be an immediate, hence the switch.
+// s_waitcnt vmcnt(v) for an immediate v.
 #define RSPX_VM(v) __builtin_amdgcn_s_waitcnt(((v) & 15) | (((v) >> 4) << 14) | 0x70 | 0xF00)
-  switch (n) {
-    case 0: RSPX_VM(0); break;
-    case 1: RSPX_VM(1); break;
-    case 2: RSPX_VM(2); break;
-    case 3: RSPX_VM(3); break;
-    case 4: RSPX_VM(4); break;
-    case 5: RSPX_VM(5); break;
-    case 6: RSPX_VM(6); break;
-    case 7: RSPX_VM(7); break;
-    case 8: RSPX_VM(8); break;
-    case 9: RSPX_VM(9); break;
-    case 10: RSPX_VM(10); break;
-    case 11: RSPX_VM(11); break;
-    case 12: RSPX_VM(12); break;
-    case 13: RSPX_VM(13); break;
-    case 14: RSPX_VM(14); break;
-    case 15: RSPX_VM(15); break;
-    case 16: RSPX_VM(16); break;
-    case 17: RSPX_VM(17); break;
-    case 18: RSPX_VM(18); break;
-    case 19: RSPX_VM(19); break;
-    case 20: RSPX_VM(20); break;
-    case 21: RSPX_VM(21); break;
-    case 22: RSPX_VM(22); break;
-    case 23: RSPX_VM(23); break;
-    case 24: RSPX_VM(24); break;
-    case 25: RSPX_VM(25); break;
-    case 26: RSPX_VM(26); break;
-    case 27: RSPX_VM(27); break;
-    case 28: RSPX_VM(28); break;
-    case 29: RSPX_VM(29); break;
-    case 30: RSPX_VM(30); break;
-    case 31: RSPX_VM(31); break;
-    case 32: RSPX_VM(32); break;
-    case 33: RSPX_VM(33); break;
-    case 34: RSPX_VM(34); break;
-    case 35: RSPX_VM(35); break;
-    case 36: RSPX_VM(36); break;
-    case 37: RSPX_VM(37); break;
-    case 38: RSPX_VM(38); break;
-    case 39: RSPX_VM(39); break;
-    case 40: RSPX_VM(40); break;
-    case 41: RSPX_VM(41); break;
-    case 42: RSPX_VM(42); break;
-    case 43: RSPX_VM(43); break;
-    case 44: RSPX_VM(44); break;
-    case 45: RSPX_VM(45); break;
-    case 46: RSPX_VM(46); break;
-    case 47: RSPX_VM(47); break;
-    case 48: RSPX_VM(48); break;
-    case 49: RSPX_VM(49); break;
-    case 50: RSPX_VM(50); break;
-    case 51: RSPX_VM(51); break;
-    case 52: RSPX_VM(52); break;
-    case 53: RSPX_VM(53); break;
-    case 54: RSPX_VM(54); break;
-    case 55: RSPX_VM(55); break;
-    case 56: RSPX_VM(56); break;
-    case 57: RSPX_VM(57); break;
-    case 58: RSPX_VM(58); break;
-    case 59: RSPX_VM(59); break;
-    case 60: RSPX_VM(60); break;
-    case 61: RSPX_VM(61); break;
-    case 62: RSPX_VM(62); break;
-    case 63: RSPX_VM(63); break;
-    default: RSPX_VM(0); break;
+
+// Waits until at most `younger` rounds of OWN loads each (younger < RING) are
+// still in flight: vmcnt(OWN younger), the count as an immediate.
+template <int OWN, int RING>
+__device__ __forceinline__ void wait_rounds(int younger) {
+  static_assert(OWN * (RING - 1) < 64, "vmcnt range");
+  if constexpr (RING > 1) {
+    if (younger >= RING - 1) {
+      RSPX_VM(OWN * (RING - 1));
+      return;
+    }
+    wait_rounds<OWN, RING - 1>(younger);
+  } else {
+    RSPX_VM(0);
   }
-#undef RSPX_VM
 }
 
 // Direct-to-LDS loads: lane l's bytes land at dst + 16 l.  Non-template
@@ -273,26 +219,24 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// This wave's chunks of one round (4 steps from step `sfirst`) into the ring
-// slot at `dst`: chunk c = w + 8 j is chunk c % CH of step-in-round c / CH.
-// voff[t] is the lane's byte offset of chunk (w + 8 t) % CH relative to the
-// step's first key.  The descriptors cover keys [ks, P) of the kv head, so
-// keys past P (and whole steps past P) read zeros without touching memory.
+// This wave's chunks of one round (4 steps from step `sfirst` of the group)
+// into the ring slot at `dst`: chunk c = w + 8 j is chunk c % CH of
+// step-in-round c / CH.  voff[t] is the lane's byte offset of chunk
+// (w + 8 t) % CH relative to its step's first key; kstep / vstep are the bytes
+// per step.  The descriptors rk / rv start at the group's first key and end at
+// key P of the kv head, so keys past P (and whole steps past P) read zeros
+// without touching memory.
 template <int D, int NV>
-__device__ __forceinline__ void issue_round(const uint16_t* kpg, const uint16_t* vpg, int64_t skpn, int64_t svpn,
-                                            int P, int sfirst, const int (&voff)[NV], lds_char* dst, int w) {
+__device__ __forceinline__ void issue_round(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, int kstep,
+                                            int vstep, int sfirst, const int (&voff)[NV], lds_char* dst, int w) {
   using G = StepGeom<D>;
 #pragma unroll
   for (int j = 0; j < G::OWN; ++j) {
     const int c = w + kWavesA * j;
     const int sr = c / G::CH, cc = c % G::CH;
-    const int ks = (sfirst + sr) * kStep;
-    if (cc < G::KCH)
-      bdma16(buffer_rsrc(kpg + (int64_t)ks * skpn, 2 * ((int64_t)(P - ks - 1) * skpn + D)), voff[j % NV],
-             dst + sr * G::SLOT + cc * 1024);
-    else
-      bdma16(buffer_rsrc(vpg + (int64_t)ks * svpn, 2 * ((int64_t)(P - ks - 1) * svpn + D)), voff[j % NV],
-             dst + sr * G::SLOT + cc * 1024);
+    const int st = sfirst + sr;
+    if (cc < G::KCH) bdma16(rk, voff[j % NV] + st * kstep, dst + sr * G::SLOT + cc * 1024);
+    else bdma16(rv, voff[j % NV] + st * vstep, dst + sr * G::SLOT + cc * 1024);
   }
 }
 
@@ -405,14 +349,18 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
     for (int j = 0; j < DT; ++j) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
+  const int ks0 = s0 * kStep;   // the group's first key
+  const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kpg + (int64_t)ks0 * A.skpn, 2 * ((int64_t)(P - ks0 - 1) * A.skpn + D));
+  const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(vpg + (int64_t)ks0 * A.svpn, 2 * ((int64_t)(P - ks0 - 1) * A.svpn + D));
+  const int kstep = 2 * kStep * (int)A.skpn, vstep = 2 * kStep * (int)A.svpn;
   const int pro = min(nr, G::RING);
-  for (int rr = 0; rr < pro; ++rr) issue_round<D>(kpg, vpg, A.skpn, A.svpn, P, s0 + kQuarters * rr, voff, ring + (rr % G::RING) * G::ROUND, w);
+  for (int rr = 0; rr < pro; ++rr)
+    issue_round<D>(rk, rv, kstep, vstep, kQuarters * rr, voff, ring + (rr % G::RING) * G::ROUND, w);
 
   bf16x8 qop[kRT][DQ];
   for (int r = 0; r < nr; ++r) {
     // Own chunks of round r (and the Q chunks, issued first) have landed.
-    const int issued = min(nr, G::RING + r);
-    wait_vm(G::OWN * (issued - r - 1));
+    wait_rounds<G::OWN, G::RING>(min(nr - 1 - r, G::RING - 1));
     lds_barrier();   // every wave's chunks of round r are in LDS
     if (r == 0 && has_rows) {
 #pragma unroll
@@ -525,7 +473,7 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
     // Round r is consumed by every wave: its ring slot takes round r + RING.
     if (r + G::RING < nr) {
       lds_barrier();
-      issue_round<D>(kpg, vpg, A.skpn, A.svpn, P, s0 + kQuarters * (r + G::RING), voff,
+      issue_round<D>(rk, rv, kstep, vstep, kQuarters * (r + G::RING), voff,
                      ring + (r % G::RING) * G::ROUND, w);
     }
   }
