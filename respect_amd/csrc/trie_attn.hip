@@ -62,14 +62,16 @@ constexpr float kLazyTau = 8.f;  // log2 headroom before the reference max moves
 constexpr int kMaxNodeSlots = 4096;
 constexpr int kWavesA = 8;       // waves per prompt workgroup
 
+// Strides are in elements; the host checks that every element offset of a
+// tensor fits 30 bits, so offsets (and byte offsets) are 32-bit arithmetic.
 struct TrieAttnArgs {
-  const uint16_t* q;  int64_t sqh, sqm;
-  const uint16_t* kp; int64_t skph, skpn;
-  const uint16_t* vp; int64_t svph, svpn;
-  const uint16_t* kn; int64_t sknh, sknn;
-  const uint16_t* vn; int64_t svnh, svnn;
-  const uint8_t* msk; int64_t smm, smn;
-  uint16_t* out;      int64_t soh, som;
+  const uint16_t* q;  int sqh, sqm;
+  const uint16_t* kp; int skph, skpn;
+  const uint16_t* vp; int svph, svpn;
+  const uint16_t* kn; int sknh, sknn;
+  const uint16_t* vn; int svnh, svnn;
+  const uint8_t* msk; int smm, smn;
+  uint16_t* out;      int soh, som;
   int HK, GQS, M, P, NN;   // GQS = log2(query heads per kv head)
   int R, NRB, NG, S;  // rows per kv head, row blocks, groups, steps per group
   float c;            // sm_scale * log2(e)
@@ -288,7 +290,7 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
     const int r = row0 + 16 * T + n16;
     const int rc = r < A.R ? r : 0;
     const int mq = rc >> A.GQS, jh = rc & ((1 << A.GQS) - 1);
-    dma16(A.q + (int64_t)((g << A.GQS) + jh) * A.sqh + (int64_t)mq * A.sqm + 32 * i + 8 * g4, qreg + c * 1024);
+    dma16(A.q + (((g << A.GQS) + jh) * A.sqh + mq * A.sqm + 32 * i + 8 * g4), qreg + c * 1024);
   }
 
   // This wave's chunks of a round: c = w + 8 j, step-in-round c / CH, chunk
@@ -302,11 +304,11 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
     if (cc < G::KCH) {
       const int key = G::KPV * cc + lane / G::U;
       const int b = (lane % G::U) ^ kswz<D>(key);
-      voff[t] = 2 * key * (int)A.skpn + 16 * b;
+      voff[t] = 2 * key * A.skpn + 16 * b;
     } else {
       const int key = G::KPV * (cc - G::KCH) + lane / G::U;
       const int b = (lane % G::U) ^ vswz<D>(key);
-      voff[t] = 2 * key * (int)A.svpn + 16 * b;
+      voff[t] = 2 * key * A.svpn + 16 * b;
     }
   }
   const uint16_t* kpg = A.kp + g * A.skph;
@@ -350,9 +352,9 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
   }
 
   const int ks0 = s0 * kStep;   // the group's first key
-  const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kpg + (int64_t)ks0 * A.skpn, 2 * ((int64_t)(P - ks0 - 1) * A.skpn + D));
-  const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(vpg + (int64_t)ks0 * A.svpn, 2 * ((int64_t)(P - ks0 - 1) * A.svpn + D));
-  const int kstep = 2 * kStep * (int)A.skpn, vstep = 2 * kStep * (int)A.svpn;
+  const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kpg + ks0 * A.skpn, 2 * ((P - ks0 - 1) * A.skpn + D));
+  const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(vpg + ks0 * A.svpn, 2 * ((P - ks0 - 1) * A.svpn + D));
+  const int kstep = 2 * kStep * A.skpn, vstep = 2 * kStep * A.svpn;
   const int pro = min(nr, G::RING);
   for (int rr = 0; rr < pro; ++rr)
     issue_round<D>(rk, rv, kstep, vstep, kQuarters * rr, voff, ring + (rr % G::RING) * G::ROUND, w);
@@ -646,17 +648,17 @@ __device__ __forceinline__ void node_issue(const TrieAttnArgs& A, int g, int c0,
   const int lane = __lane_id();
   const int left = A.NN - c0 - 1;
   const __amdgpu_buffer_rsrc_t rk =
-      buffer_rsrc(A.kn + g * A.sknh + (int64_t)c0 * A.sknn, 2 * ((int64_t)left * A.sknn + D));
+      buffer_rsrc(A.kn + (g * A.sknh + c0 * A.sknn), 2 * (left * A.sknn + D));
   const __amdgpu_buffer_rsrc_t rv =
-      buffer_rsrc(A.vn + g * A.svnh + (int64_t)c0 * A.svnn, 2 * ((int64_t)left * A.svnn + D));
+      buffer_rsrc(A.vn + (g * A.svnh + c0 * A.svnn), 2 * (left * A.svnn + D));
   const int nx = withv ? KX + VX : KX;
   for (int x = w; x < nx; x += nw) {
     if (x < KX) {
       const int slot = 16 * (x / DQ) + (lane & 15);
-      bdma16(rk, 2 * (slot * (int)A.sknn + 32 * (x % DQ) + 8 * (lane >> 4)), kv + x * 1024);
+      bdma16(rk, 2 * (slot * A.sknn + 32 * (x % DQ) + 8 * (lane >> 4)), kv + x * 1024);
     } else {
       const int byte = (x - KX) * 1024 + 16 * lane;
-      bdma16(rv, 2 * (byte / RB) * (int)A.svnn + byte % RB, kv + x * 1024);
+      bdma16(rv, 2 * (byte / RB) * A.svnn + byte % RB, kv + x * 1024);
     }
   }
 }
@@ -670,7 +672,7 @@ __device__ __forceinline__ void node_q(const TrieAttnArgs& A, int g, int p0, int
   const int lane = __lane_id();
   const int r = p0 + 16 * rt + (lane & 15);
   const RowRef R = row_ref(A, g, r < rend ? r : p0, p0);
-  const uint16_t* qp = A.q + R.hd * A.sqh + (int64_t)R.mq * A.sqm + 8 * (lane >> 4);
+  const uint16_t* qp = A.q + (R.hd * A.sqh + R.mq * A.sqm + 8 * (lane >> 4));
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) qf[i] = *reinterpret_cast<const bf16x8*>(qp + 32 * i);
 }
@@ -678,7 +680,7 @@ __device__ __forceinline__ void node_q(const TrieAttnArgs& A, int g, int p0, int
 // Mask byte of row r (below R) for slot c0 + lane; 0 past NN.
 __device__ __forceinline__ uint8_t node_mask(const TrieAttnArgs& A, int r, int c0) {
   const int t = c0 + __lane_id();
-  return t < A.NN ? A.msk[(int64_t)(r >> A.GQS) * A.smm + (int64_t)t * A.smn] : (uint8_t)0;
+  return t < A.NN ? A.msk[(r >> A.GQS) * A.smm + t * A.smn] : (uint8_t)0;
 }
 
 __device__ __forceinline__ uint64_t node_masks(const TrieAttnArgs& A, int p0, int nrd, int w, int c0) {
@@ -925,7 +927,7 @@ __device__ __forceinline__ void merge_row(const TrieAttnArgs& A, int g, int r, f
   for (int qq = 0; qq < kGroupTarget; ++qq)
     if (qq < NG) combine<DL>(fm, fl, facc, gm[qq], gl[qq], ga[qq]);
   combine<DL>(fm, fl, facc, m, l, acc);
-  uint16_t* o = A.out + R.hd * A.soh + (int64_t)R.mq * A.som + DL * lane;
+  uint16_t* o = A.out + (R.hd * A.soh + R.mq * A.som + DL * lane);
   if constexpr (DL == 2) *reinterpret_cast<uint32_t*>(o) = pack_bf16x2(facc[0] / fl, facc[1] / fl);
   else *o = f32_to_bf16_rne(facc[0] / fl);
 }
@@ -1164,22 +1166,31 @@ static int trie_attn_impl(const void* q, int64_t sqh, int64_t sqm, const void* k
   for (const void* p : ptrs)
     if (p && !aligned16(p)) return RSPX_EALIGN;
   const int64_t strides[] = {sqh, sqm, skph, skpn, svph, svpn, sknh, sknn, svnh, svnn, soh, som};
-  for (int64_t s : strides)
+  for (int64_t s : strides) {
+    if (s < 0) return RSPX_EINVAL;
     if (s % 8 != 0) return RSPX_EALIGN;
-  // Byte offsets inside one kv head's prompt and node K/V are 32-bit.
-  if (P > 0 && ((int64_t)P * skpn * 2 >= (1ll << 31) || (int64_t)P * svpn * 2 >= (1ll << 31)))
-    return RSPX_EUNSUPPORTED;
-  if (NN > 0 && ((int64_t)NN * sknn * 2 >= (1ll << 31) || (int64_t)NN * svnn * 2 >= (1ll << 31)))
+  }
+  if (smm < 0 || smn < 0) return RSPX_EINVAL;
+  // The kernels address every tensor with 32-bit offsets: the largest element
+  // offset of each must stay below 2^30 (byte offsets below 2^31).
+  const int64_t lim = int64_t(1) << 30;
+  auto span = [](int64_t n0, int64_t s0, int64_t n1, int64_t s1, int64_t last) {
+    return (n0 > 0 ? (n0 - 1) * s0 : 0) + (n1 > 0 ? (n1 - 1) * s1 : 0) + last;
+  };
+  if (span(H, sqh, M, sqm, D) >= lim || span(H, soh, M, som, D) >= lim) return RSPX_EUNSUPPORTED;
+  if (P > 0 && (span(HK, skph, P, skpn, D) >= lim || span(HK, svph, P, svpn, D) >= lim)) return RSPX_EUNSUPPORTED;
+  if (NN > 0 && (span(HK, sknh, NN, sknn, D) >= lim || span(HK, svnh, NN, svnn, D) >= lim ||
+                 span(M, smm, NN, smn, 1) >= lim))
     return RSPX_EUNSUPPORTED;
 
   TrieAttnArgs a;
-  a.q = static_cast<const uint16_t*>(q);   a.sqh = sqh;   a.sqm = sqm;
-  a.kp = static_cast<const uint16_t*>(kp); a.skph = skph; a.skpn = skpn;
-  a.vp = static_cast<const uint16_t*>(vp); a.svph = svph; a.svpn = svpn;
-  a.kn = static_cast<const uint16_t*>(kn); a.sknh = sknh; a.sknn = sknn;
-  a.vn = static_cast<const uint16_t*>(vn); a.svnh = svnh; a.svnn = svnn;
-  a.msk = msk; a.smm = smm; a.smn = smn;
-  a.out = static_cast<uint16_t*>(out); a.soh = soh; a.som = som;
+  a.q = static_cast<const uint16_t*>(q);   a.sqh = (int)sqh;   a.sqm = (int)sqm;
+  a.kp = static_cast<const uint16_t*>(kp); a.skph = (int)skph; a.skpn = (int)skpn;
+  a.vp = static_cast<const uint16_t*>(vp); a.svph = (int)svph; a.svpn = (int)svpn;
+  a.kn = static_cast<const uint16_t*>(kn); a.sknh = (int)sknh; a.sknn = (int)sknn;
+  a.vn = static_cast<const uint16_t*>(vn); a.svnh = (int)svnh; a.svnn = (int)svnn;
+  a.msk = msk; a.smm = (int)smm; a.smn = (int)smn;
+  a.out = static_cast<uint16_t*>(out); a.soh = (int)soh; a.som = (int)som;
   a.HK = HK; a.GQS = __builtin_ctz(pl.GQA); a.M = M; a.P = P; a.NN = NN;
   a.R = pl.R; a.NRB = pl.NRB; a.NG = pl.NG; a.S = pl.S;
   a.c = (float)((double)sm_scale * 1.4426950408889634);
