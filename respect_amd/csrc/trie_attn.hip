@@ -436,11 +436,7 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
         lrow[t] = lrow[t] * alpha;
         mref[t] = mn;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float ae = shfl_idx(alpha, 4 * g4 + e);
-#pragma unroll
-          for (int j = 0; j < DT; ++j) acc[t][j][e] = acc[t][j][e] * ae;
-        }
+        for (int j = 0; j < DT; ++j) acc[t][j] = acc[t][j] * alpha;
       }
     }
 #pragma unroll
@@ -458,10 +454,11 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
       pop[t] = __builtin_bit_cast(bf16x8, pw);
     }
 
-    // O += bf16(P) V.  A operand: lane (n16, g4) holds row n16's p at k-slots
-    // 8 g4 + i <-> keys 4 g4 + i (i < 4) and 12 + 4 g4 + i.  B operand of
-    // head_dim tile j: V[key(k-slot)][16 j + n16], two transposing reads.
-    // Output lane: rows 4 g4 + e, head_dim 16 j + n16.
+    // O^T += V^T bf16(P)^T.  B operand: lane (n16, g4) holds row n16's p at
+    // k-slots 8 g4 + i <-> keys 4 g4 + i (i < 4) and 12 + 4 g4 + i.  A operand
+    // of head_dim tile j: V[key(k-slot)][16 j + n16], two transposing reads.
+    // Output lane: row n16, head_dim 16 j + 4 g4 + e -- each lane holds four
+    // consecutive head_dim columns of the row whose softmax state it keeps.
 #pragma unroll
     for (int j = 0; j < DT; ++j) {
       const s16x4 lo = lds_read_tr(slot + trv[0][j]);
@@ -469,7 +466,7 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
       const bf16x8 vop = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
       for (int t = 0; t < kRT; ++t)
-        acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop[t], vop, acc[t][j], 0, 0, 0);
+        acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[t], acc[t][j], 0, 0, 0);
     }
     }
     // Round r is consumed by every wave: its ring slot takes round r + RING.
@@ -494,7 +491,7 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
   static_assert(4 * BR * D * 4 <= RINGBYTES, "the four scaled quarters fit the ring");
   static_assert(8 * kRT * 16 * 8 <= L::QBYTES, "quarter (m, l) fit the Q area");
   lds_float* qml = (lds_float*)qreg;    // [h][k][t][16 rows] (m, l)
-  lds_float* qacc = (lds_float*)ring;   // [k][BR rows][D], 16-column blocks swizzled by row
+  lds_float* qacc = (lds_float*)ring;   // [k][BR rows][D], 16-byte units swizzled by row
   lds_barrier();
   if (g4 == 0) {
 #pragma unroll
@@ -518,14 +515,12 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
     Mr[t] = M;
     Lr[t] = (lk[0] * sk[0] + lk[1] * sk[1]) + (lk[2] * sk[2] + lk[3] * sk[3]);
     const float own = k == 0 ? sk[0] : k == 1 ? sk[1] : k == 2 ? sk[2] : sk[3];
+    // Row 16 t + n16 of this half, 16-byte units 4 j + g4, unit index XOR (row & 7).
+    const int row = 16 * kRT * h + 16 * t + n16;
+    lds_float* dst = qacc + (k * BR + row) * D;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float se = shfl_idx(own, 4 * g4 + e);   // factor of row 16 t + 4 g4 + e
-      const int row = 16 * kRT * h + 16 * t + 4 * g4 + e;
-      lds_float* dst = qacc + (k * BR + row) * D;
-#pragma unroll
-      for (int j = 0; j < DT; ++j) dst[(16 * j + n16) ^ (16 * g4)] = acc[t][j][e] * se;
-    }
+    for (int j = 0; j < DT; ++j)
+      *(lds_f32x4*)(dst + 4 * ((4 * j + g4) ^ (row & 7))) = acc[t][j] * own;
   }
   lds_barrier();
   // Group partial: rows RPI x + lane / (D / 4), columns [4 c4, +4): 1 KB per
@@ -539,7 +534,7 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
 #pragma unroll
   for (int jj = 0; jj < NSW; ++jj) {
     const int rl = (w + kWavesA * jj) * RPI + lane / (D / 4);
-    const lds_float* src = qacc + rl * D + ((4 * c4) ^ (16 * ((rl >> 2) & 3)));
+    const lds_float* src = qacc + rl * D + 4 * (c4 ^ (rl & 7));
     const f32x4 a0 = *(const lds_f32x4*)(src);
     const f32x4 a1 = *(const lds_f32x4*)(src + BR * D);
     const f32x4 a2 = *(const lds_f32x4*)(src + 2 * BR * D);
