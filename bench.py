@@ -388,6 +388,42 @@ def bench_decoder(args) -> dict:
             "launch": "HIP graphs (one captured forward per node-segment width), both paths"}
 
 
+# Trie shapes of the invariance sweep: (nodes, sequences, length, shared prefix lo, hi);
+# depth <= 32, node counts exact.
+SWEEP_TRIES = ((1, 1, 1, 0, 0), (8, 2, 5, 2, 2), (32, 2, 20, 8, 8), (64, 4, 24, 0, 16), (128, 5, 32, 8, 8))
+SWEEP_PROMPTS = (1024, 3072, 8192, 16384)
+
+
+def bench_sweep(args) -> dict:
+    """µs per call and fraction of HBM peak of the 8B-shape attention over prompt lengths and
+    trie sizes (rotating input sets beyond the last-level cache, as the headline line)."""
+    from respect_amd.kernels.attention import make_launcher
+    from respect_amd.workloads import AttnWorkload, merged_trie
+
+    points = []
+    for P in SWEEP_PROMPTS:
+        for (n, seqs, length, lo, hi) in SWEEP_TRIES:
+            per_set = 4 * 8 * 128 * P
+            sets = int(min(64, max(2, -(-300_000_000 // per_set))))
+            tree = merged_trie(7, seqs, length, lo, hi, n)
+            wl = AttnWorkload(P=P, tree=tree, sets=sets, seed=P + n)
+            launchers, keep = [], []
+            for (q, kp, vp, kn, vn) in wl.sets:
+                launch, out = make_launcher(q, kp, vp, kn, vn, wl.msk, wl.sm_scale)
+                launchers.append(launch)
+                keep.append(out)
+            ms = time_launches(launchers, 100, 10)
+            gbs = wl.algorithmic_bytes() / (ms * 1e-3) / 1e9
+            pt = {"prompt_len": P, "nodes": n, "us": round(ms * 1e3, 2), "GBps": round(gbs, 1),
+                  "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
+            if n >= 16:
+                pt["mfma_frac_of_peak"] = round(wl.flops() / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)
+            points.append(pt)
+            del wl, launchers, keep
+    return {"workload": "8B-shape attention (32 q / 8 kv heads, head_dim 128), prompt lengths x trie sizes",
+            "points": points}
+
+
 def bench_copy(args) -> dict:
     """Device-to-device copy of a 1 GiB bf16 buffer (torch's copy kernel): the
     measured HBM ceiling the kernels above are compared with, and the known-size
@@ -441,6 +477,8 @@ def main() -> int:
         _log("timing RMSNorm + q/k norm+RoPE and SwiGLU")
         res["extra"] = {"norm_rope": bench_norm_rope(args), "swiglu": bench_swiglu(args),
                         "copy": bench_copy(args)}
+        _log("timing the attention sweep (prompt lengths x trie sizes)")
+        res["extra"]["attn_sweep"] = bench_sweep(args)
     if not args.no_decoder:
         dec = bench_decoder(args)
         res["committed_tok_s"] = dec["committed_tok_s"]

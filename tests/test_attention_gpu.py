@@ -113,6 +113,28 @@ def test_committed_offset_rows_equal_paths(base):
         assert torch.equal(one[:, 0], full[:, int(i)]), f"node {i}"
 
 
+# (nodes, sequences, length, shared prefix lo, hi): depth <= 32, exact node counts.
+SWEEP_TRIES = ((1, 1, 1, 0, 0), (8, 2, 5, 2, 2), (32, 2, 20, 8, 8), (64, 4, 24, 0, 16), (128, 5, 32, 8, 8))
+
+
+@pytest.mark.parametrize("P", [1024, 3072, 8192, 16384])
+@pytest.mark.parametrize("tri", SWEEP_TRIES, ids=lambda t: f"n{t[0]}")
+def test_invariance_sweep(P, tri):
+    """8B shape over prompt lengths x trie sizes, the trie placed after a random number of
+    committed slots (node-segment tile edges fall mid-trie): sampled rows (always the
+    deepest) equal their 1-token path calls bitwise."""
+    n, seqs, length, lo, hi = tri
+    rng = np.random.default_rng(P + n)
+    base = int(rng.integers(0, 48))
+    c = gen.attn_case(P + n, 32, 8, 128, P, seqs, length, lo, hi, n, kv_scale=128 ** -0.5, base=base)
+    full = _run(c)
+    depth = np.array([nd.depth for nd in c.tree.nodes])
+    picks = {int(np.argmax(depth))} | {int(i) for i in rng.choice(n, min(n, 4), replace=False)}
+    for i in sorted(picks):
+        one = _run(gen.path_case(c, i))
+        assert torch.equal(one[:, 0], full[:, i]), f"P={P} n={n} base={base} node {i}"
+
+
 def test_slot_layout_invariance_reference_shapes():
     """tests/test_kernel_invariance.py:30-54 of the reference: 26 node values in slots
     0-25 vs 0-17 + 200-207, H=32, HK=8, D=128, NP=300, NN=224, 64 query rows."""
