@@ -180,6 +180,19 @@ int64_t rspx_linear_workspace_bytes(int M, int N, int K);
 int rspx_linear(const void* x, int64_t sx, const void* w, int64_t sw, void* out, int64_t so, int M, int N, int K,
                 int out_fp32, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Gate/up projection with SwiGLU in its epilogue: w holds the gate and up
+ * rows interleaved (row 2i = gate row i, row 2i + 1 = up row i, N = 2F), and
+ * out[m][i] (F columns, row stride so >= F) = bf16(bf16(silu(g)) * u) of the
+ * bf16 g = (x.w^T)[m][2i], u = (x.w^T)[m][2i + 1] -- bit for bit rspx_linear
+ * followed by rspx_silu_mul on the de-interleaved halves.  Needs a single
+ * K chunk (rspx_linear_splits(N, K) == 1; RSPX_EUNSUPPORTED otherwise) and
+ * N % 32 == 0.  No counterpart in the reference: it fuses linear
+ * (respect/kernels/gemm.py:30) with silu_mul (respect/system/fused.py:116)
+ * for the decoder step.
+ */
+int rspx_linear_silu(const void* x, int64_t sx, const void* w, int64_t sw, void* out, int64_t so, int M, int N, int K,
+                     void* stream);
+
 /* The same product, left as its fp32 chunk partials part[S][M][N] (S =
  * rspx_linear_splits(N, K), also when S == 1) for a consumer that adds them
  * in chunk order and rounds -- rspx_add_rmsnorm_partials,

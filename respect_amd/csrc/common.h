@@ -38,6 +38,10 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
 // Round a float to the nearest-even bf16 value, kept in fp32.
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16_rne(f)); }
 
+// SwiGLU's silu in fp32: g / (1 + exp(-g)) with the accurate library
+// exponential and an IEEE divide; g -> -inf gives g / inf = -0, as PyTorch does.
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+
 // 2^x on the hardware transcendental unit (v_exp_f32).  -inf -> 0.
 __device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -55,6 +55,7 @@ struct Args {
   float* part;                    // [S][M][N] fp32 (S > 1)
   int M, N, K, S, KC, out_fp32;
   int to_part;                    // write chunk partials even when S == 1
+  int silu;                       // S == 1: columns (2i, 2i + 1) are (gate_i, up_i); out[m][i] = SwiGLU
 };
 
 constexpr int kOOB = 0x7ffffff0;  // a buffer offset past any descriptor: loads return 0, touch nothing
@@ -221,6 +222,14 @@ __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
       *reinterpret_cast<f32x4*>(A.part + ((size_t)s * A.M + m) * A.N + n) = acc[t];
     } else if (A.out_fp32) {
       *reinterpret_cast<f32x4*>(static_cast<float*>(A.out) + (int64_t)m * A.so + n) = acc[t];
+    } else if (A.silu) {
+      // The bf16 gate/up values rspx_linear would store, then rspx_silu_mul's
+      // arithmetic: bf16(bf16(silu(g)) * u) for columns n / 2 and n / 2 + 1.
+      const uint32_t p0 = pack_bf16x2(acc[t][0], acc[t][1]);
+      const uint32_t p1 = pack_bf16x2(acc[t][2], acc[t][3]);
+      const float a0 = round_bf16(silu_f32(bf16_lo(p0))), a1 = round_bf16(silu_f32(bf16_lo(p1)));
+      *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(A.out) + (int64_t)m * A.so + n / 2) =
+          pack_bf16x2(a0 * bf16_hi(p0), a1 * bf16_hi(p1));
     } else {
       u32x2 o;
       o[0] = pack_bf16x2(acc[t][0], acc[t][1]);
@@ -276,7 +285,7 @@ extern "C" int64_t rspx_linear_workspace_bytes(int M, int N, int K) {
 
 namespace rspx {
 static int linear_launch(const void* x, int64_t sx, const void* w, int64_t sw, void* out, int64_t so, int M, int N,
-                         int K, int out_fp32, float* part, int to_part, hipStream_t s) {
+                         int K, int out_fp32, float* part, int to_part, hipStream_t s, int silu = 0) {
   const int S = linear_splits(N, K);
   gemm::Args a;
   a.x = static_cast<const uint16_t*>(x); a.sx = sx;
@@ -284,6 +293,7 @@ static int linear_launch(const void* x, int64_t sx, const void* w, int64_t sw, v
   a.out = out; a.so = so;
   a.part = part;
   a.M = M; a.N = N; a.K = K; a.S = S; a.KC = K / S; a.out_fp32 = out_fp32 ? 1 : 0; a.to_part = to_part;
+  a.silu = silu;
   const int MTILES = (M + gemm::kRows - 1) / gemm::kRows;
   // 8 waves (128 columns) share each X round between twice the columns; worth
   // it while the grid keeps >= 192 workgroups, and for the widest layers
@@ -351,6 +361,16 @@ extern "C" int rspx_linear(const void* x, int64_t sx, const void* w, int64_t sw,
     return RSPX_EWORKSPACE;
   return linear_launch(x, sx, w, sw, out, so, M, N, K, out_fp32, static_cast<float*>(workspace), 0,
                        static_cast<hipStream_t>(stream));
+}
+
+extern "C" int rspx_linear_silu(const void* x, int64_t sx, const void* w, int64_t sw, void* out, int64_t so, int M,
+                                int N, int K, void* stream) {
+  int rc = linear_check(x, sx, w, sw, M, N, K);
+  if (rc != RSPX_OK || M == 0) return rc;
+  if (!out || N % 32 != 0 || so < N / 2) return RSPX_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(out) & 15u) || so % 8) return RSPX_EALIGN;
+  if (linear_splits(N, K) != 1) return RSPX_EUNSUPPORTED;
+  return linear_launch(x, sx, w, sw, out, so, M, N, K, 0, nullptr, 0, static_cast<hipStream_t>(stream), 1);
 }
 
 extern "C" int rspx_linear_partials(const void* x, int64_t sx, const void* w, int64_t sw, float* part, int M, int N,

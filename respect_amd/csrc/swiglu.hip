@@ -14,10 +14,6 @@
 
 namespace rspx {
 
-// exp(-g) through the accurate library exponential; the divide is IEEE.
-// g -> -inf gives g / inf = -0, as PyTorch does.
-__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
-
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* g, int64_t sg, const uint16_t* u,
                                                        int64_t su, uint16_t* y, int64_t sy, int rows, int vcols) {
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;

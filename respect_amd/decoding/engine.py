@@ -13,7 +13,7 @@ Every arithmetic step goes through librespect_amd:
       a = attention(q; prompt K/V, node K/V, mask)   rspx_trie_attn
       h = a . Wo^T                                   rspx_linear_partials
       x, y = x + h, rmsnorm(x + h)                   rspx_add_rmsnorm_partials
-      g|u = y . Wgu^T ; m = silu(g) * u              rspx_linear, rspx_silu_mul
+      g|u = y . Wgu^T ; m = silu(g) * u              rspx_linear_silu (or rspx_linear, rspx_silu_mul)
       h = m . Wd^T ; x, y = x + h, rmsnorm(x + h)    rspx_linear_partials, rspx_add_rmsnorm_partials
 
 A projection feeding an epilogue is left as its fp32 K-chunk partials and
@@ -78,8 +78,20 @@ class Layer:
         self.k_norm = norm_w(D)
         self.wo = w(H, cfg.heads * D)
         self.post_norm = norm_w(H)
-        self.wgu = w(2 * F, H)                      # [gate | up] rows
+        wgu = w(2 * F, H)                           # [gate | up] rows
         self.wd = w(H, F)
+        # With one K chunk the gate/up product carries SwiGLU in its epilogue
+        # (rspx_linear_silu), which wants the rows interleaved: 2i gate i, 2i + 1 up i.
+        self.gu_fused = _lib.lib().rspx_linear_splits(2 * F, H) == 1
+        self._wgu = wgu.view(2, F, H).transpose(0, 1).reshape(2 * F, H).contiguous() if self.gu_fused else wgu
+
+    @property
+    def wgu(self) -> torch.Tensor:
+        """Gate/up weight as [gate | up] rows (a copy when stored interleaved)."""
+        if not self.gu_fused:
+            return self._wgu
+        F2, H = self._wgu.shape
+        return self._wgu.view(F2 // 2, 2, H).transpose(0, 1).reshape(F2, H)
 
 
 class Decoder:
@@ -170,10 +182,15 @@ class Decoder:
             _lib.check("rspx_add_rmsnorm_partials", L.rspx_add_rmsnorm_partials(
                 x.data_ptr(), Hd, hp, S, lay.post_norm.data_ptr(), x.data_ptr(), Hd, y.data_ptr(), Hd,
                 T, Hd, cfg.eps, s))
-            gu = self._linear(y, lay.wgu)
             F = cfg.ffn
-            _lib.check("rspx_silu_mul", L.rspx_silu_mul(gu.data_ptr(), gu.stride(0), gu.data_ptr() + 2 * F,
-                                                        gu.stride(0), mlp.data_ptr(), F, T, F, s))
+            if lay.gu_fused:
+                _lib.check("rspx_linear_silu", L.rspx_linear_silu(
+                    y.data_ptr(), y.stride(0), lay._wgu.data_ptr(), lay._wgu.stride(0), mlp.data_ptr(),
+                    mlp.stride(0), T, 2 * F, Hd, s))
+            else:
+                gu = self._linear(y, lay.wgu)
+                _lib.check("rspx_silu_mul", L.rspx_silu_mul(gu.data_ptr(), gu.stride(0), gu.data_ptr() + 2 * F,
+                                                            gu.stride(0), mlp.data_ptr(), F, T, F, s))
             hp, S = self._partials(mlp, lay.wd)
             nxt = self.layers[li + 1].in_norm if li + 1 < len(self.layers) else self.final_norm
             _lib.check("rspx_add_rmsnorm_partials", L.rspx_add_rmsnorm_partials(

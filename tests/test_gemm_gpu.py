@@ -145,3 +145,45 @@ def test_partials_consumers_equal_linear_then_op():
     for a, b in zip(*outs):
         assert torch.equal(a, b)
     assert torch.equal(outs[0][2][:, 3:3 + T].transpose(0, 1), qkv[:, (HQ + HK) * D:].view(T, HK, D))
+
+
+@pytest.mark.parametrize("M", [1, 7, 64, 130])
+def test_linear_silu_equals_linear_then_silu_mul(M):
+    """rspx_linear_silu on interleaved gate/up rows is bit for bit rspx_linear followed by
+    rspx_silu_mul on the [gate | up] layout, and leaves each row independent of M."""
+    from respect_amd import _lib
+    from respect_amd.kernels.gemm import linear
+    from respect_amd.system.fused import silu_mul
+    F, K = 8192, 256
+    print(f"[linear_silu] M={M} F={F} K={K}", flush=True)
+    L = _lib.lib()
+    assert L.rspx_linear_splits(2 * F, K) == 1
+    x, w = _xw(M + 11, M, 2 * F, K)
+    xd, wd = _dev(x), _dev(w)
+    wil = wd.view(2, F, K).transpose(0, 1).reshape(2 * F, K).contiguous()
+    gu = linear(xd, wd)
+    ref = silu_mul(gu[:, :F], gu[:, F:])
+    out = torch.empty((M, F), dtype=torch.bfloat16, device="cuda")
+    rc = L.rspx_linear_silu(xd.data_ptr(), K, wil.data_ptr(), K, out.data_ptr(), F, M, 2 * F, K,
+                            _lib.stream_ptr(xd.device))
+    _lib.check("rspx_linear_silu", rc)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    one = torch.empty((1, F), dtype=torch.bfloat16, device="cuda")
+    _lib.check("rspx_linear_silu", L.rspx_linear_silu(xd[M - 1:].data_ptr(), K, wil.data_ptr(), K, one.data_ptr(), F,
+                                                       1, 2 * F, K, _lib.stream_ptr(xd.device)))
+    torch.cuda.synchronize()
+    assert torch.equal(one[0], out[M - 1])
+
+
+def test_linear_silu_rejects_split_k():
+    from respect_amd import _lib
+    L = _lib.lib()
+    N, K = 1024, 4096                      # several K chunks
+    assert L.rspx_linear_splits(N, K) > 1
+    x = torch.zeros((4, K), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros((N, K), dtype=torch.bfloat16, device="cuda")
+    out = torch.empty((4, N // 2), dtype=torch.bfloat16, device="cuda")
+    rc = L.rspx_linear_silu(x.data_ptr(), K, w.data_ptr(), K, out.data_ptr(), N // 2, 4, N, K,
+                            _lib.stream_ptr(x.device))
+    assert rc == -2   # RSPX_EUNSUPPORTED
