@@ -588,19 +588,25 @@ template <> struct NodeVec<4> { typedef u32x2 T; };
 
 constexpr int kChunk = 64;  // node slots staged in LDS at a time
 
-// Node LDS: the chunk's K as score fragments -- 1 KB per 16-slot tile kt and
-// 32-wide head_dim step i, lane (n16, g4)'s 16 bytes are K[16 kt + n16][32 i +
-// 8 g4, +8), read back with one ds_read_b128 -- then its V rows, then the fp32
-// scores of up to kMaxNodeRows rows x kChunk slots, then the node partials of
-// those rows.
+// Node LDS: kResident buffers of a chunk's K as score fragments -- 1 KB per
+// 16-slot tile kt and 32-wide head_dim step i, lane (n16, g4)'s 16 bytes are
+// K[16 kt + n16][32 i + 8 g4, +8), read back with one ds_read_b128 -- then as
+// many of V rows, then the fp32 scores of up to kMaxNodeRows rows x kChunk
+// slots, then the node partials of those rows.  Streaming uses buffer 0; a
+// prefetched segment of up to kResident chunks sits in buffers 0, 1, ...
 constexpr int kMaxNodeRows = 64;  // a workgroup's node rows: at most one prompt row block
+constexpr int kResident = 2;  // node chunks a prefetching caller keeps in LDS at once
 template <int D> struct NodeLds {
-  static constexpr int KBYTES = kChunk * 2 * D;
-  static constexpr int VBYTES = kChunk * 2 * D;
+  static constexpr int KBYTES = kChunk * 2 * D;   // one chunk's K
+  static constexpr int VBYTES = kChunk * 2 * D;   // one chunk's V
+  static constexpr int VOFF = kResident * KBYTES;
+  static constexpr int SOFF = VOFF + kResident * VBYTES;
   static constexpr int SROW = kChunk + 4;  // floats per score row
-  static constexpr int NPOFF = KBYTES + VBYTES + kMaxNodeRows * SROW * 4;
+  static constexpr int NPOFF = SOFF + kMaxNodeRows * SROW * 4;
   static constexpr int NPROW = D + 4;      // node partial of a row: m, l, pad, pad, acc[D]
   static constexpr int BYTES = NPOFF + kMaxNodeRows * NPROW * 4;
+  static __device__ __forceinline__ lds_char* kbuf(lds_char* kv, int b) { return kv + b * KBYTES; }
+  static __device__ __forceinline__ lds_char* vbuf(lds_char* kv, int b) { return kv + VOFF + b * VBYTES; }
 };
 constexpr int kMaxRounds = kMaxNodeRows / kWavesA;  // node rows per wave
 
@@ -621,12 +627,17 @@ __device__ __forceinline__ RowRef row_ref(const TrieAttnArgs& A, int g, int r, i
 
 typedef __attribute__((address_space(3))) float lds_float;
 
-// Loads a caller may issue ahead of node_rows for a single-chunk trie: the
-// chunk's K/V in LDS, the score fragment of the wave's first task and the mask
-// bytes of the wave's rows.
+// Loads a caller may issue ahead of node_rows for a node segment of at most
+// kResident chunks: every chunk's K/V in LDS, the score fragment of the wave's
+// first task and the mask bytes of the wave's rows.
 template <int D> struct NodePre {
   bf16x8 qf[D / 32];
-  uint64_t mb;   // byte i: the mask byte of round i
+  uint64_t mb[kResident];   // chunk c, byte i: the mask byte of round i
+  // mb[b] for a run-time b, kept in registers (selects, no indexed access).
+  __device__ __forceinline__ uint64_t mask(int b) const {
+    static_assert(kResident == 2, "one select");
+    return b == 0 ? mb[0] : mb[1];
+  }
 };
 static_assert(kMaxRounds <= 8, "mask bytes of every round in one 64-bit word");
 
@@ -634,10 +645,10 @@ static_assert(kMaxRounds <= 8, "mask bytes of every round in one 64-bit word");
 __device__ __forceinline__ uint64_t node_masks(const TrieAttnArgs& A, int p0, int nrd, int w, int c0);
 
 // Chunk c0 of kv head g's node K (score fragments) and, if `withv`, V rows
-// into LDS `kv`: 1 KB pieces x = w, w + nw, ...  Slots past NN read zeros.
+// into LDS buffer b: 1 KB pieces x = w, w + nw, ...  Slots past NN read zeros.
 template <int D>
-__device__ __forceinline__ void node_issue(const TrieAttnArgs& A, int g, int c0, lds_char* kv, int w, int nw,
-                                           bool withv) {
+__device__ __forceinline__ void node_issue(const TrieAttnArgs& A, int g, int c0, lds_char* kv, int b, int w,
+                                           int nw, bool withv) {
   constexpr int DQ = D / 32, RB = 2 * D;
   constexpr int KX = NodeLds<D>::KBYTES / 1024, VX = NodeLds<D>::VBYTES / 1024;
   const int lane = __lane_id();
@@ -650,10 +661,10 @@ __device__ __forceinline__ void node_issue(const TrieAttnArgs& A, int g, int c0,
   for (int x = w; x < nx; x += nw) {
     if (x < KX) {
       const int slot = 16 * (x / DQ) + (lane & 15);
-      bdma16(rk, 2 * (slot * A.sknn + 32 * (x % DQ) + 8 * (lane >> 4)), kv + x * 1024);
+      bdma16(rk, 2 * (slot * A.sknn + 32 * (x % DQ) + 8 * (lane >> 4)), NodeLds<D>::kbuf(kv, b) + x * 1024);
     } else {
       const int byte = (x - KX) * 1024 + 16 * lane;
-      bdma16(rv, 2 * (byte / RB) * A.svnn + byte % RB, kv + x * 1024);
+      bdma16(rv, 2 * (byte / RB) * A.svnn + byte % RB, NodeLds<D>::vbuf(kv, b) + (x - KX) * 1024);
     }
   }
 }
@@ -751,9 +762,10 @@ template <> struct NodeLane<1> {
 // this is wave w) calls it; row p0 + w + 8 i is wave w's round i, and its
 // partial (m, l, acc) is left in the node-partial area of LDS (row i * 8 + w)
 // for the same wave to read.  With more than one chunk a first pass over K
-// finds m.  have_pre: the single chunk was issued by the caller into LDS and
-// `pre` (node_prefetch), and the caller has since waited for them (vmcnt 0)
-// and passed a workgroup barrier.  Does nothing when NN = 0.  Ends with every
+// finds m.  have_pre: the caller issued a segment of at most kResident chunks
+// (chunk c into buffer c) and `pre` (node_prefetch), has since waited for them
+// (vmcnt 0) and passed a workgroup barrier; otherwise chunks stream through
+// buffer 0.  Does nothing when NN = 0.  Ends with every
 // vector load of the calling wave complete.
 template <int D>
 __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv, int w,
@@ -768,19 +780,25 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
   const int NN = A.NN;
   if (NN == 0) return;
   const int nrd = (rend - p0 - w + nw - 1) / nw;     // rounds of this wave
-  lds_float* S = (lds_float*)(kv + NodeLds<D>::KBYTES + NodeLds<D>::VBYTES);
+  lds_float* S = (lds_float*)(kv + NodeLds<D>::SOFF);
   lds_float* NP = (lds_float*)(kv + NodeLds<D>::NPOFF);
-  const lds_char* vl = kv + NodeLds<D>::KBYTES + DL * 2 * lane;
   const bool one = NN <= kChunk;
+  const bool res = have_pre && NN <= kResident * kChunk;  // every chunk already in buffer c
 
   if (!one) {
     for (int c0 = 0; c0 < NN; c0 += kChunk) {
       if (c0 > 0) lds_barrier();  // every wave is done with the previous chunk's scores
-      node_issue<D>(A, g, c0, kv, w, nw, false);
-      const uint64_t mb = node_masks(A, p0, nrd, w, c0);
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-      lds_barrier();
-      node_scores<D>(A, g, p0, rend, c0, kv, S, w, nw, pre.qf, false);
+      const int b = res ? c0 / kChunk : 0;
+      uint64_t mb;
+      if (res) {
+        mb = pre.mask(b);
+      } else {
+        node_issue<D>(A, g, c0, kv, 0, w, nw, false);
+        mb = node_masks(A, p0, nrd, w, c0);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        lds_barrier();
+      }
+      node_scores<D>(A, g, p0, rend, c0, NodeLds<D>::kbuf(kv, b), S, w, nw, pre.qf, res);
       lds_barrier();
 #pragma unroll 1
       for (int i = 0; i < kMaxRounds; ++i) {
@@ -798,20 +816,21 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
 
   for (int c0 = 0; c0 < NN; c0 += kChunk) {
     if (c0 > 0) lds_barrier();  // every wave is done with the previous chunk
-    const bool pf = have_pre && one;
+    const int b = res ? c0 / kChunk : 0;
     uint64_t mb;
-    if (pf) {
+    if (res) {
       // The caller waited for its loads (vmcnt 0) before a workgroup barrier.
       // No wait here: a store or atomic it issued since may still be in flight.
-      mb = pre.mb;
+      mb = pre.mask(b);
     } else {
-      node_issue<D>(A, g, c0, kv, w, nw, true);
+      node_issue<D>(A, g, c0, kv, 0, w, nw, true);
       mb = node_masks(A, p0, nrd, w, c0);
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of the chunk is in LDS
       lds_barrier();                       // and every other wave's part
     }
-    node_scores<D>(A, g, p0, rend, c0, kv, S, w, nw, pre.qf, pf);
+    node_scores<D>(A, g, p0, rend, c0, NodeLds<D>::kbuf(kv, b), S, w, nw, pre.qf, res);
     lds_barrier();
+    const lds_char* vl = NodeLds<D>::vbuf(kv, b) + DL * 2 * lane;
 
 #pragma unroll 1
     for (int i = 0; i < nrd; ++i) {
@@ -865,14 +884,22 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
   }
 }
 
-// Issues node_rows' loads for a single-chunk trie (0 < NN <= kChunk, p0 < rend).
+// Issues node_rows' loads for a segment of at most kResident chunks
+// (0 < NN <= kResident kChunk, p0 < rend): chunk c into buffer c.
 template <int D>
 __device__ __forceinline__ void node_prefetch(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv, int w,
                                               NodePre<D>& pre) {
   constexpr int nw = kWavesA;
-  node_issue<D>(A, g, 0, kv, w, nw, true);
+  const int nrd = (rend - p0 - w + nw - 1) / nw;
+#pragma unroll
+  for (int b = 0; b < kResident; ++b) {
+    pre.mb[b] = 0;
+    if (b * kChunk < A.NN) {
+      node_issue<D>(A, g, b * kChunk, kv, b, w, nw, true);
+      pre.mb[b] = node_masks(A, p0, nrd, w, b * kChunk);
+    }
+  }
   if (w < 4 * ((rend - p0 + 15) / 16)) node_q<D>(A, g, p0, rend, w >> 2, pre.qf);
-  pre.mb = node_masks(A, p0, (rend - p0 - w + nw - 1) / nw, w, 0);
 }
 
 // Final result of row r of kv head g, one row over the wave (lane l: head_dim
@@ -1010,9 +1037,9 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   const int r0 = rb * rows_blk + q * rpw;
   const int rend = min(rb * rows_blk + min(rows_blk, (q + 1) * rpw), A.R);
 
-  // A single-chunk trie's node K/V, score fragment and mask bytes are loaded
-  // while the group partial is being stored.
-  const bool pf = A.NN > 0 && A.NN <= kChunk && r0 < rend;
+  // A node segment of at most kResident chunks (K/V, score fragment, mask
+  // bytes) is loaded while the group partial is being stored.
+  const bool pf = A.NN > 0 && A.NN <= kResident * kChunk && r0 < rend;
   NodePre<D> pre;
   prompt_block<D, kRT, true>(A, lds, g, rb, q, [&] {
     if (pf) node_prefetch<D>(A, g, r0, rend, (lds_char*)lds, w, pre);
