@@ -285,6 +285,60 @@ def bench_swiglu(args) -> dict:
             "hbm_frac_of_peak": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def bench_prefill(args) -> dict:
+    """Prefill / Flow element-wise kernels on [4096, 4096] bf16 rows (rotating sets beyond the
+    MALL): add_sq, square, norm_apply (the kernel halves of rmsnorm / norm_from), and the
+    vision RoPE on [4096, 16, 80]."""
+    import torch
+
+    from respect_amd import _lib
+    L = _lib.lib()
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    M, N, sets = 4096, 4096, 6
+    s = _lib.stream_ptr(dev)
+    bf, f32 = torch.bfloat16, torch.float32
+    out, keep = {}, []
+
+    def rec(name, launchers, nbytes):
+        t = time_launches(launchers, args.steps // 2, args.warmup) * 1e-3
+        out[name] = {"us": round(t * 1e6, 2), "GBps": round(nbytes / t / 1e9, 1),
+                     "hbm_frac_of_peak": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+
+    ls_add, ls_sq, ls_norm = [], [], []
+    for _ in range(sets):
+        r = torch.randn(M, N, generator=g, device=dev).to(bf)
+        h = torch.randn(M, N, generator=g, device=dev).to(bf)
+        x = torch.empty(M, N, device=dev, dtype=bf)
+        sq = torch.empty(M, N, device=dev, dtype=f32)
+        var = torch.rand(M, generator=g, device=dev) + 0.5
+        w = (1 + 0.02 * torch.randn(N, generator=g, device=dev)).to(bf)
+        y = torch.empty(M, N, device=dev, dtype=bf)
+        keep += [r, h, x, sq, var, w, y]
+        ls_add.append(_launcher(L.rspx_add_sq, r.data_ptr(), N, h.data_ptr(), N, x.data_ptr(), N, sq.data_ptr(), N,
+                                M, N, s))
+        ls_sq.append(_launcher(L.rspx_square, r.data_ptr(), N, sq.data_ptr(), N, M, N, s))
+        ls_norm.append(_launcher(L.rspx_norm_apply, r.data_ptr(), N, var.data_ptr(), w.data_ptr(), y.data_ptr(), N,
+                                 M, N, 1e-6, s))
+    rec("add_sq", ls_add, M * N * (2 + 2 + 2 + 4))
+    rec("square", ls_sq, M * N * (2 + 4))
+    rec("norm_apply", ls_norm, M * N * (2 + 2) + M * 4 + N * 2)
+    Lv, NH, D = 4096, 16, 80
+    ls_rope = []
+    for _ in range(sets):
+        xv = torch.randn(Lv, NH, D, generator=g, device=dev).to(bf)
+        cs = torch.randn(Lv, D, generator=g, device=dev)
+        sn = torch.randn(Lv, D, generator=g, device=dev)
+        yv = torch.empty(Lv, NH, D, device=dev, dtype=bf)
+        keep += [xv, cs, sn, yv]
+        ls_rope.append(_launcher(L.rspx_rope_vision, xv.data_ptr(), NH * D, D, cs.data_ptr(), sn.data_ptr(), D,
+                                 yv.data_ptr(), Lv, NH, D, s))
+    rec("rope_vision", ls_rope, Lv * NH * D * 4 + Lv * D * 8)
+    out["workload"] = "rows [4096, 4096] bf16 (fp32 squares); vision RoPE x [4096, 16, 80], fp32 cos/sin"
+    return out
+
+
 def _target_trie(cont, rng, n_seqs=4, length=24, target_nodes=64, vocab=151936):
     """Trie of ``n_seqs`` candidates of ``length`` tokens rooted at cont[0]: one is
     the target's own greedy continuation ``cont``, the others share a prefix of
@@ -477,6 +531,8 @@ def main() -> int:
         _log("timing RMSNorm + q/k norm+RoPE and SwiGLU")
         res["extra"] = {"norm_rope": bench_norm_rope(args), "swiglu": bench_swiglu(args),
                         "copy": bench_copy(args)}
+        _log("timing the Prefill / Flow element-wise kernels")
+        res["extra"]["prefill"] = bench_prefill(args)
         _log("timing the attention sweep (prompt lengths x trie sizes)")
         res["extra"]["attn_sweep"] = bench_sweep(args)
     if not args.no_decoder:
