@@ -81,9 +81,9 @@ const char* rspx_version(void);
  * two calls that can run at the same time.
  * NN <= 4096 (the node-slot limit of the reference dispatcher, NMAX).
  *
- * Launches: one (prompt groups, node fold and merge in one kernel whose
+ * Launches: one (prompt groups, node partials and merge in one kernel whose
  * workgroups wait for each other; used when the grid fits on the device at
- * once) or two (prompt groups, then node fold and merge).  Both give the
+ * once) or two (prompt groups, then node partials and merge).  Both give the
  * same bits.
  *
  * rows_per_wave: 0 = automatic, else 1 or 2 (16-row tiles per wave).  It

@@ -18,10 +18,13 @@
 //            accumulator is rescaled); otherwise probabilities are taken
 //            against the old reference and may reach 2^8.
 //   group    S = 4 NR consecutive steps (NG <= 8 groups): its quarters
-//            k = 0, 1, 2, 3 combined in order.
-//   node     the row's allowed node slots, one at a time in slot order,
-//            fp32 probabilities (the reference's node loop,
-//            attention.py:52-67).  Masked slots are skipped; in the
+//            scaled to the row's maximum M over them (2^(m_k - M), 0 for an
+//            empty quarter) and summed as (q0 + q1) + (q2 + q3), l likewise.
+//   node     score q.k c from a bf16 MFMA chain; m = the maximum over the
+//            row's allowed node slots; p = 2^(s - m) in fp32; l and acc
+//            summed over the allowed slots one at a time in slot order (the
+//            reference's node loop, attention.py:52-67, forms the same sums
+//            with an online maximum).  Masked slots are skipped; in the
 //            reference they are exact no-ops, so only the sequence of
 //            allowed slots matters.
 //   final    the NG groups left to right, then the node partial.
@@ -31,20 +34,19 @@
 // it is verified alone (1-token decoding) or inside a 128-node trie, and
 // wherever its allowed slots sit in the node segment.
 //
-// Two launches on the caller's stream, no host synchronisation:
-//   A  prompt_kernel: workgroup = (kv head g, block of 32 RT GQA rows, key
-//      group), 8 waves = 2 row halves x 4 key quarters.  The waves issue the
-//      group's K/V straight from HBM into an LDS ring (buffer_load ... lds, a
-//      round of 4 steps per ring slot, nothing held in registers), laid out so
-//      that K fragments are one conflict-free ds_read_b128 and V fragments
-//      one ds_read_b64_tr_b16 (the transposing LDS read of gfx950) per MFMA
-//      operand half.  Wave (h, k) computes step 4i + k of round i for its 16 RT
-//      rows; at the end the four quarters of each row are combined through
-//      LDS and the group partial (m, l, acc) is stored.
-//   B  node_merge_kernel: one wave per 4 consecutive rows (16 lanes per row).
-//      It lists each row's allowed node slots (ballots), folds them in order
-//      (dot products reduced with a fixed DPP butterfly), combines the group
-//      partials in group order and the node partial last, writes bf16.
+// Launches on the caller's stream, no host synchronisation.  Normally one,
+// fused_kernel: workgroup = (kv head g, block of 32 RT GQA rows, key group),
+// 8 waves = 2 row halves x 4 key quarters, all resident at once.  The waves
+// issue the group's K/V straight from HBM into an LDS ring (buffer_load ...
+// lds, a round of 4 steps per ring slot), laid out so that K fragments are one
+// conflict-free ds_read_b128 and V fragments one ds_read_b64_tr_b16 (the
+// transposing LDS read of gfx950) per MFMA operand half.  Wave (h, k) computes
+// step 4i + k of round i for its 16 RT rows; the four quarters are combined
+// through LDS and the group partial (m, l, acc) is stored; the workgroup then
+// counts itself, computes the node partials of its share of the block's rows
+// (MFMA scores, one row per wave) and, once the block's groups are all
+// counted, merges its rows.  When the grid cannot be resident at once the
+// same work runs as prompt_kernel then node_merge_kernel -- the same bits.
 //   Rows are packed GQA-wise (row = query * GQA + head-in-group), so a kv
 //   head's K/V is read once from HBM for all query heads that share it.  With
 //   8 kv heads, workgroup g of kernel A lands on XCD g (round-robin dispatch),
@@ -581,7 +583,7 @@ __global__ __launch_bounds__(512) void prompt_kernel(TrieAttnArgs A) {
   prompt_block<D, kRT, false>(A, lds, g, rest % A.NRB, rest / A.NRB, [] {});
 }
 
-// ------------------------------------------------------------------ node fold and merge
+// ------------------------------------------------------------------ node partials and merge
 template <int DN> struct NodeVec;
 template <> struct NodeVec<8> { typedef u32x4 T; };
 template <> struct NodeVec<4> { typedef u32x2 T; };

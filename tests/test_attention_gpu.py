@@ -232,7 +232,7 @@ def _status(case, ws):
 
 @pytest.mark.parametrize("which", ["cfg1", "cfg2", "base37", "long", "gqa2", "d64"])
 def test_one_and_two_launches_equal(which):
-    """The one-kernel path (prompt groups, node fold and merge with workgroups
+    """The one-kernel path (prompt groups, node partials and merge with workgroups
     waiting on per-row-block counters) and the two-kernel path give the same
     bits; the counters are back at zero after each call (repeat calls on one
     workspace stay equal) and no wait ran out."""
