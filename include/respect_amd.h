@@ -86,8 +86,9 @@ const char* rspx_version(void);
  * once) or two (prompt groups, then node partials and merge).  Both give the
  * same bits.
  *
- * rows_per_wave: 0 = automatic, else 1 or 2 (16-row tiles per wave).  It
- * changes only the work distribution, never the result.
+ * rows_per_wave: 0 = automatic (one 16-row tile per wave when that grid
+ * fits on the device at once, e.g. 1-token calls; two otherwise), else 1 or
+ * 2.  It changes only the work distribution, never the result.
  */
 
 int64_t rspx_trie_attn_workspace_bytes(int H, int HK, int M, int P, int D);

@@ -1086,6 +1086,9 @@ struct Plan {
 
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+template <int D, int RT>
+static int fused_capacity();
+
 // Steps per group S = 4 NR and the group count NG <= 8 depend on P only.
 static int make_plan(int H, int HK, int M, int P, int NN, int D, int rows_per_wave, Plan* pl) {
   if (H <= 0 || HK <= 0 || M < 0 || P < 0 || NN < 0 || H % HK != 0) return RSPX_EINVAL;
@@ -1104,7 +1107,14 @@ static int make_plan(int H, int HK, int M, int P, int NN, int D, int rows_per_wa
     pl->S = kQuarters;
     pl->NG = 0;
   }
-  const int rt = rows_per_wave == 0 ? 2 : rows_per_wave;
+  int rt = rows_per_wave;
+  if (rt == 0) {
+    // One 16-row tile per wave while that grid (twice as many row blocks)
+    // still fits on the device at once, else two: the same bits either way.
+    const int nrb1 = (pl->R + 31) / 32;
+    const int cap1 = D == 128 ? fused_capacity<128, 1>() : fused_capacity<64, 1>();
+    rt = (pl->NG > 0 && HK * nrb1 * pl->NG <= cap1) ? 1 : 2;
+  }
   if (rt != 1 && rt != 2) return RSPX_EINVAL;
   pl->RT = rt;
   pl->NRB = (pl->R + 32 * rt - 1) / (32 * rt);
