@@ -44,6 +44,22 @@ extern "C" {
 #define RSPX_EALIGN (-4)       /* pointer or stride not 16-byte aligned */
 #define RSPX_ELAUNCH (-5)      /* HIP launch error */
 
+/* Tiled activation layout.  Passed as the row stride of a bf16 activation
+ * matrix A[M, K] with K % 32 == 0 -- x of rspx_linear, rspx_linear_silu and
+ * rspx_linear_partials; y of rspx_rmsnorm, rspx_add_rmsnorm and
+ * rspx_add_rmsnorm_partials; out of rspx_linear_silu -- RSPX_TILED names
+ * this layout instead of row-major: element (m, k) sits at
+ *   ((((m / 64) * (K / 32) + k / 32) * 4 + (m % 64) / 16) * 64
+ *      + m % 16 + 16 * ((k % 32) / 8)) * 8 + k % 8,
+ * i.e. for each 64-row block and 32-wide k-block the four 16 x 32 MFMA
+ * operand tiles of that block, 1 KB each.  The buffer must hold
+ * ceil(M / 64) * 64 * K elements; what rows M .. of the last block hold never
+ * reaches a result.  The linear layers load a tiled x a whole tile per
+ * instruction and give bit for bit the results of the same x row-major.  No
+ * counterpart in the reference: an activation layout of the decoder step.
+ */
+#define RSPX_TILED ((int64_t)-1)
+
 /* Human-readable text for an RSPX_* code (static storage). */
 const char* rspx_strerror(int code);
 
@@ -124,7 +140,8 @@ int rspx_trie_attn_status(const void* workspace, int H, int HK, int M, int P, in
 /* ---------------------------------------------------------------- RMSNorm
  * y[r] = bf16(w * bf16(x[r] * rsqrt(mean(x[r]^2) + eps))), fp32 statistics
  * (replaces respect/kernels/rmsnorm.py:25 rmsnorm(x, w, eps)).
- * x, y: [rows, n] with row strides sx, sy (elements); w: [n].  n % 8 == 0,
+ * x, y: [rows, n] with row strides sx, sy (elements; sy may be RSPX_TILED,
+ * then n % 32 == 0); w: [n].  n % 8 == 0,
  * n <= 16384.  The sum of squares of a row is taken in an order fixed by n,
  * so a row's output does not depend on `rows`.
  */
@@ -167,7 +184,7 @@ int rspx_silu_mul(const void* g, int64_t sg, const void* u, int64_t su, void* y,
  * bf16 (out_fp32 = 0) or fp32 (out_fp32 = 1) (replaces
  * respect/kernels/gemm.py:30 linear(x, w, ..., out_dtype); bias is the
  * caller's, as in the reference).  Row strides sx, sw, so in elements; rows
- * 16-byte aligned.  N % 16 == 0, K % 256 == 0.
+ * 16-byte aligned; sx may be RSPX_TILED.  N % 16 == 0, K % 256 == 0.
  *
  * Reduction order: K is cut into rspx_linear_splits(N, K) equal chunks (a
  * function of N and K only); each chunk is a fixed chain of bf16 MFMAs in
@@ -185,7 +202,8 @@ int rspx_linear(const void* x, int64_t sx, const void* w, int64_t sw, void* out,
  * rows interleaved (row 2i = gate row i, row 2i + 1 = up row i, N = 2F), and
  * out[m][i] (F columns, row stride so >= F) = bf16(bf16(silu(g)) * u) of the
  * bf16 g = (x.w^T)[m][2i], u = (x.w^T)[m][2i + 1] -- bit for bit rspx_linear
- * followed by rspx_silu_mul on the de-interleaved halves.  Needs a single
+ * followed by rspx_silu_mul on the de-interleaved halves.  so == RSPX_TILED
+ * writes out in the tiled layout of [M, N / 2] (then N % 64 == 0).  Needs a single
  * K chunk (rspx_linear_splits(N, K) == 1; RSPX_EUNSUPPORTED otherwise) and
  * N % 32 == 0.  No counterpart in the reference: it fuses linear
  * (respect/kernels/gemm.py:30) with silu_mul (respect/system/fused.py:116)

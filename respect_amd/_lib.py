@@ -14,6 +14,10 @@ import torch  # noqa: F401  (loads the HIP runtime the library will share)
 
 LIB_PATH = Path(__file__).resolve().with_name("librespect_amd.so")
 
+# Row stride value naming the tiled activation layout (RSPX_TILED of
+# include/respect_amd.h).
+RSPX_TILED = -1
+
 _c_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int

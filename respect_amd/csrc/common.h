@@ -57,6 +57,21 @@ __device__ __forceinline__ int shfl_idx_i(int v, int src) {
   return __builtin_amdgcn_ds_bpermute(src << 2, v);
 }
 
+// The tiled layout of a bf16 activation matrix [M, K] (K % 32 == 0), the
+// one the linear layers read their x operand from fastest: per 64-row block
+// and 32-wide k-block, the four 16 x 32 MFMA operand tiles of that block,
+// 1 KB each, lane n16 + 16 g of a tile holding row n16 of the tile, k
+// 8 g .. 8 g + 7 of the k-block.  Element (m, k) sits at tiled_offset(m, k, K);
+// the buffer holds ceil(M / 64) * 64 * K elements.
+__device__ __forceinline__ int64_t tiled_offset(int m, int k, int K) {
+  return ((((int64_t)(m >> 6) * (K >> 5) + (k >> 5)) * 4 + ((m >> 4) & 3)) * 64 + (m & 15) + 16 * ((k >> 3) & 3)) *
+             8 +
+         (k & 7);
+}
+
+// Row stride value that names the tiled layout (RSPX_TILED of the C ABI).
+constexpr int64_t kTiled = -1;
+
 // The output of a K-split linear layer: the fp32 chunk partials of one
 // element added in chunk order, ((p0 + p1) + p2) + ... (stride = elements
 // between chunks).  Every consumer of split partials uses this, so the value

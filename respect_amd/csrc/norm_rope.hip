@@ -97,9 +97,15 @@ __device__ __forceinline__ void load_row_vec(const RowIn& in, int row, int c, fl
 
 // Normalise a row held by TPR lanes (TPR <= 64, all in one wave), VPL
 // 8-element vectors per lane.
+// Where the 8 outputs (row, c .. c + 7) go: row stride sy, or the tiled
+// layout (tiled_offset) when sy == kTiled.
+__device__ __forceinline__ uint16_t* out_at(uint16_t* y, int64_t sy, int row, int c, int n) {
+  return y + (sy == kTiled ? tiled_offset(row, c, n) : row * sy + c);
+}
+
 template <int TPR, int VPL, int MODE>
-__device__ __forceinline__ void rms_row_wave(const RowIn& in, int row, const uint16_t* w, uint16_t* y, int sub,
-                                             int n, float eps) {
+__device__ __forceinline__ void rms_row_wave(const RowIn& in, int row, const uint16_t* w, uint16_t* y, int64_t sy,
+                                             int sub, int n, float eps) {
   float xv[VPL][8];
   float ss = 0.f;
 #pragma unroll
@@ -124,7 +130,7 @@ __device__ __forceinline__ void rms_row_wave(const RowIn& in, int row, const uin
       unpack8(*reinterpret_cast<const u32x4*>(w + c), wv);
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i] = wv[i] * round_bf16(xv[v][i] * r);
-      *reinterpret_cast<u32x4*>(y + c) = pack8(o);
+      *reinterpret_cast<u32x4*>(out_at(y, sy, row, c, n)) = pack8(o);
     }
   }
 }
@@ -139,7 +145,7 @@ __global__ __launch_bounds__(256) void rmsnorm_small_kernel(RowIn in, const uint
   const int row = (blockIdx.x * 256 + threadIdx.x) / TPR;
   const int sub = lane % TPR;
   if (row >= rows) return;   // whole lane groups leave together (TPR divides 64)
-  rms_row_wave<TPR, VPL, MODE>(in, row, w, y + row * sy, sub, n, eps);
+  rms_row_wave<TPR, VPL, MODE>(in, row, w, y, sy, sub, n, eps);
 }
 
 // Long rows: one 256-thread workgroup per row, VPL 8-element vectors per
@@ -169,7 +175,6 @@ __global__ __launch_bounds__(256) void rmsnorm_row_kernel(RowIn in, const uint16
   __syncthreads();
   const float tot = ((part[0] + part[1]) + part[2]) + part[3];
   const float r = rsqrt_rn(tot / (float)n + eps);
-  uint16_t* yr = y + row * sy;
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
     const int c = (v * 256 + t) * 8;
@@ -178,7 +183,7 @@ __global__ __launch_bounds__(256) void rmsnorm_row_kernel(RowIn in, const uint16
       unpack8(*reinterpret_cast<const u32x4*>(w + c), wvv);
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i] = wvv[i] * round_bf16(xv[v][i] * r);
-      *reinterpret_cast<u32x4*>(yr + c) = pack8(o);
+      *reinterpret_cast<u32x4*>(out_at(y, sy, row, c, n)) = pack8(o);
     }
   }
   (void)lane;
@@ -357,12 +362,20 @@ static int norm_args_ok(int rows, int n) {
   return RSPX_OK;
 }
 
+// Output row stride: a multiple of 8 elements, or kTiled (then n % 32 == 0).
+static int norm_out_ok(int64_t sy, int n) {
+  if (sy == kTiled) return n % 32 == 0 ? RSPX_OK : RSPX_EUNSUPPORTED;
+  if (sy < 0) return RSPX_EINVAL;
+  return sy % 8 ? RSPX_EALIGN : RSPX_OK;
+}
+
 extern "C" int rspx_rmsnorm(const void* x, int64_t sx, const void* w, void* y, int64_t sy, int rows, int n,
                             float eps, void* stream) {
   int rc = norm_args_ok(rows, n);
   if (rc != RSPX_OK || rows == 0) return rc;
   if (!x || !w || !y) return RSPX_EINVAL;
-  if (!al16(x) || !al16(w) || !al16(y) || sx % 8 || sy % 8) return RSPX_EALIGN;
+  if (!al16(x) || !al16(w) || !al16(y) || sx % 8) return RSPX_EALIGN;
+  if ((rc = norm_out_ok(sy, n)) != RSPX_OK) return rc;
   RowIn in{static_cast<const uint16_t*>(x), sx, nullptr, 0, nullptr, 0, 0, 1, nullptr, 0};
   launch_rmsnorm<0>(in, static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy, rows, n, eps,
                     static_cast<hipStream_t>(stream));
@@ -374,8 +387,8 @@ extern "C" int rspx_add_rmsnorm(const void* r, int64_t sr, const void* h, int64_
   int rc = norm_args_ok(rows, n);
   if (rc != RSPX_OK || rows == 0) return rc;
   if (!r || !h || !w || !xo || !y) return RSPX_EINVAL;
-  if (!al16(r) || !al16(h) || !al16(w) || !al16(xo) || !al16(y) || sr % 8 || sh % 8 || sxo % 8 || sy % 8)
-    return RSPX_EALIGN;
+  if (!al16(r) || !al16(h) || !al16(w) || !al16(xo) || !al16(y) || sr % 8 || sh % 8 || sxo % 8) return RSPX_EALIGN;
+  if ((rc = norm_out_ok(sy, n)) != RSPX_OK) return rc;
   RowIn in{static_cast<const uint16_t*>(r), sr, static_cast<const uint16_t*>(h), sh, nullptr, 0, 0, 1,
            static_cast<uint16_t*>(xo), sxo};
   launch_rmsnorm<1>(in, static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy, rows, n, eps,
@@ -389,7 +402,8 @@ extern "C" int rspx_add_rmsnorm_partials(const void* r, int64_t sr, const float*
   if (rc != RSPX_OK || rows == 0) return rc;
   if (S < 1) return RSPX_EINVAL;
   if (!r || !hp || !w || !xo || !y) return RSPX_EINVAL;
-  if (!al16(r) || !al16(hp) || !al16(w) || !al16(xo) || !al16(y) || sr % 8 || sxo % 8 || sy % 8) return RSPX_EALIGN;
+  if (!al16(r) || !al16(hp) || !al16(w) || !al16(xo) || !al16(y) || sr % 8 || sxo % 8) return RSPX_EALIGN;
+  if ((rc = norm_out_ok(sy, n)) != RSPX_OK) return rc;
   RowIn in{static_cast<const uint16_t*>(r), sr, nullptr, 0, hp, n, (int64_t)rows * n, S, static_cast<uint16_t*>(xo),
            sxo};
   launch_rmsnorm<2>(in, static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy, rows, n, eps,

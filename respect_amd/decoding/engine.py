@@ -21,6 +21,10 @@ the epilogue adds them in chunk order and rounds to bf16 -- the exact value
 rspx_linear would store -- so no separate reduction launch is needed.
     logits = y . Wlm^T (fp32)                        rspx_linear
 
+The normalised rows y and the SwiGLU output m, read only by linear layers,
+stay in the tiled activation layout (RSPX_TILED): the linear layers then load
+their x operand a whole MFMA tile per instruction, with the same result bits.
+
 Each kernel computes a row with arithmetic that does not depend on how many
 rows the call carries, and attention folds a row's node slots in slot order,
 so a token verified inside a trie gets the same logits and KV bits as when it
@@ -35,7 +39,6 @@ import torch
 
 from .. import _lib
 from ..kernels.attention import trie_attn
-from ..kernels.gemm import linear
 from ..system.fused import rope_tables
 
 
@@ -62,12 +65,32 @@ class DecoderConfig:
         return 2 * (self.layers * per_layer + V * H + H)
 
 
+# Extra elements at the end of every weight row (the kernels take the row
+# stride).  Rows of 4096 or 12288 bf16 are a multiple of 8 KB apart, so the 16
+# rows one MFMA weight fragment reads sit at the same offset modulo 8 KB and
+# land on few memory channels; 128 bytes more per row spread them: on MI355X
+# the 1-row gate/up projection [24576, 4096] runs in 36.0 us instead of 41.3,
+# the vocabulary projection [151936, 4096] in 206 instead of 219 (64 rows:
+# 51.2 vs 53.2 and 272 vs 280 us); the other layers are unchanged.
+WEIGHT_ROW_PAD = 64
+
+
+def row_padded(w: torch.Tensor, pad: int = WEIGHT_ROW_PAD) -> torch.Tensor:
+    """``w`` [N, K] copied into storage of row stride K + pad; returns the
+    [N, K] view (same values, rows ``pad`` elements further apart)."""
+    N, K = w.shape
+    buf = torch.empty((N, K + pad), dtype=w.dtype, device=w.device)
+    buf[:, :K].copy_(w)
+    return buf[:, :K]
+
+
 class Layer:
     def __init__(self, cfg: DecoderConfig, g: torch.Generator, device, std: float):
         H, D, F = cfg.hidden, cfg.head_dim, cfg.ffn
 
-        def w(*shape):
-            return (torch.randn(*shape, generator=g, device=device) * std).to(torch.bfloat16)
+        def w(*shape, pad=True):
+            t = (torch.randn(*shape, generator=g, device=device) * std).to(torch.bfloat16)
+            return row_padded(t) if pad else t
 
         def norm_w(n):
             return (1.0 + torch.randn(n, generator=g, device=device) * std).to(torch.bfloat16)
@@ -78,12 +101,12 @@ class Layer:
         self.k_norm = norm_w(D)
         self.wo = w(H, cfg.heads * D)
         self.post_norm = norm_w(H)
-        wgu = w(2 * F, H)                           # [gate | up] rows
+        wgu = w(2 * F, H, pad=False)                # [gate | up] rows
         self.wd = w(H, F)
         # With one K chunk the gate/up product carries SwiGLU in its epilogue
         # (rspx_linear_silu), which wants the rows interleaved: 2i gate i, 2i + 1 up i.
         self.gu_fused = _lib.lib().rspx_linear_splits(2 * F, H) == 1
-        self._wgu = wgu.view(2, F, H).transpose(0, 1).reshape(2 * F, H).contiguous() if self.gu_fused else wgu
+        self._wgu = row_padded(wgu.view(2, F, H).transpose(0, 1).reshape(2 * F, H) if self.gu_fused else wgu)
 
     @property
     def wgu(self) -> torch.Tensor:
@@ -105,7 +128,8 @@ class Decoder:
         self.embed = (torch.randn(cfg.vocab, cfg.hidden, generator=g, device=self.device) * std).to(torch.bfloat16)
         self.layers = [Layer(cfg, g, self.device, std) for _ in range(cfg.layers)]
         self.final_norm = (1.0 + torch.randn(cfg.hidden, generator=g, device=self.device) * std).to(torch.bfloat16)
-        self.lm_head = (torch.randn(cfg.vocab, cfg.hidden, generator=g, device=self.device) * std).to(torch.bfloat16)
+        self.lm_head = row_padded(
+            (torch.randn(cfg.vocab, cfg.hidden, generator=g, device=self.device) * std).to(torch.bfloat16))
         self.sm_scale = cfg.head_dim ** -0.5
         self._ws = {}
         self._ws_retired = []   # outgrown buffers: a captured graph may still point at them
@@ -124,21 +148,28 @@ class Decoder:
             self._ws[name] = ws
         return ws
 
-    def _linear(self, x, w, out_dtype=None):
+    def _linear(self, x: int, sx: int, M: int, w: torch.Tensor, out_dtype=torch.bfloat16) -> torch.Tensor:
+        """x (device pointer, row stride sx or RSPX_TILED, M rows) . w^T."""
         L = _lib.lib()
-        need = L.rspx_linear_workspace_bytes(x.shape[0], w.shape[0], w.shape[1])
-        return linear(x, w, out_dtype=out_dtype, workspace=self._workspace("linear", need))
+        N, K = w.shape
+        need = L.rspx_linear_workspace_bytes(M, N, K)
+        ws = self._workspace("linear", max(need, 16))
+        out = torch.empty((M, N), dtype=out_dtype, device=self.device)
+        _lib.check("rspx_linear", L.rspx_linear(
+            x, sx, w.data_ptr(), w.stride(0), out.data_ptr(), out.stride(0), M, N, K,
+            1 if out_dtype == torch.float32 else 0, ws.data_ptr(), ws.numel(), _lib.stream_ptr(self.device)))
+        return out
 
-    def _partials(self, x, w) -> tuple[int, int]:
-        """x . w^T left as fp32 chunk partials in the model's partial buffer;
-        returns (pointer, chunk count) for a consumer that sums them."""
+    def _partials(self, x: int, sx: int, M: int, w: torch.Tensor) -> tuple[int, int]:
+        """x (device pointer, row stride sx or RSPX_TILED, M rows) . w^T left as
+        fp32 chunk partials in the model's partial buffer; returns (pointer,
+        chunk count) for a consumer that sums them."""
         L = _lib.lib()
-        M, K = x.shape
-        N = w.shape[0]
+        N, K = w.shape
         S = L.rspx_linear_splits(N, K)
         buf = self._workspace("partials", S * M * N * 4)
         _lib.check("rspx_linear_partials", L.rspx_linear_partials(
-            x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), buf.data_ptr(), M, N, K, _lib.stream_ptr(self.device)))
+            x, sx, w.data_ptr(), w.stride(0), buf.data_ptr(), M, N, K, _lib.stream_ptr(self.device)))
         return buf.data_ptr(), S
 
     # ------------------------------------------------------------------ forward
@@ -159,44 +190,48 @@ class Decoder:
         T = int(ids.shape[0])
         Hd, HQ, HK, D = cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim
         bf = torch.bfloat16
+        TILED = _lib.RSPX_TILED
+        rows = -(-T // 64) * 64                                   # tiled buffers hold whole 64-row blocks
         x = self.embed.index_select(0, ids)                       # residual stream [T, H]
-        y = torch.empty_like(x)
+        y = torch.empty(rows * Hd, dtype=bf, device=dev)          # normalised rows [T, H], tiled
         _lib.check("rspx_rmsnorm", L.rspx_rmsnorm(x.data_ptr(), Hd, self.layers[0].in_norm.data_ptr(), y.data_ptr(),
-                                                  Hd, T, Hd, cfg.eps, s))
+                                                  TILED, T, Hd, cfg.eps, s))
         cos, sin = rope_tables(positions, D, cfg.theta, device=dev)
         slots32 = slots.to(torch.int32)
         qo = torch.empty((T, HQ, D), dtype=bf, device=dev)
         att = torch.empty((T, HQ, D), dtype=bf, device=dev)
-        mlp = torch.empty((T, cfg.ffn), dtype=bf, device=dev)
+        mlp = torch.empty(rows * cfg.ffn, dtype=bf, device=dev)  # SwiGLU output [T, F], tiled when fused
         ws_attn = self._workspace("attn", L.rspx_trie_attn_workspace_bytes(HQ, HK, T, P, D))
         for li, lay in enumerate(self.layers):
             ck, cv = cache.k[li], cache.v[li]
-            qkvp, S = self._partials(y, lay.wqkv)
+            qkvp, S = self._partials(y.data_ptr(), TILED, T, lay.wqkv)
             _lib.check("rspx_qkv_rope_cache_partials", L.rspx_qkv_rope_cache_partials(
                 qkvp, S, lay.q_norm.data_ptr(), lay.k_norm.data_ptr(), cos.data_ptr(),
                 sin.data_ptr(), cos.stride(0), slots32.data_ptr(), ck.data_ptr(), ck.stride(0), ck.stride(1),
                 cv.data_ptr(), cv.stride(0), cv.stride(1), qo.data_ptr(), T, HQ, HK, D, cfg.eps, s))
             trie_attn(qo.permute(1, 0, 2), ck[:, :P], cv[:, :P], ck[:, P:P + NN], cv[:, P:P + NN], msk,
                       self.sm_scale, out=att.permute(1, 0, 2), workspace=ws_attn)
-            hp, S = self._partials(att.view(T, HQ * D), lay.wo)
+            hp, S = self._partials(att.data_ptr(), HQ * D, T, lay.wo)
             _lib.check("rspx_add_rmsnorm_partials", L.rspx_add_rmsnorm_partials(
-                x.data_ptr(), Hd, hp, S, lay.post_norm.data_ptr(), x.data_ptr(), Hd, y.data_ptr(), Hd,
+                x.data_ptr(), Hd, hp, S, lay.post_norm.data_ptr(), x.data_ptr(), Hd, y.data_ptr(), TILED,
                 T, Hd, cfg.eps, s))
             F = cfg.ffn
             if lay.gu_fused:
                 _lib.check("rspx_linear_silu", L.rspx_linear_silu(
-                    y.data_ptr(), y.stride(0), lay._wgu.data_ptr(), lay._wgu.stride(0), mlp.data_ptr(),
-                    mlp.stride(0), T, 2 * F, Hd, s))
+                    y.data_ptr(), TILED, lay._wgu.data_ptr(), lay._wgu.stride(0), mlp.data_ptr(),
+                    TILED, T, 2 * F, Hd, s))
+                msx = TILED
             else:
-                gu = self._linear(y, lay.wgu)
+                gu = self._linear(y.data_ptr(), TILED, T, lay.wgu)
                 _lib.check("rspx_silu_mul", L.rspx_silu_mul(gu.data_ptr(), gu.stride(0), gu.data_ptr() + 2 * F,
                                                             gu.stride(0), mlp.data_ptr(), F, T, F, s))
-            hp, S = self._partials(mlp, lay.wd)
+                msx = F
+            hp, S = self._partials(mlp.data_ptr(), msx, T, lay.wd)
             nxt = self.layers[li + 1].in_norm if li + 1 < len(self.layers) else self.final_norm
             _lib.check("rspx_add_rmsnorm_partials", L.rspx_add_rmsnorm_partials(
-                x.data_ptr(), Hd, hp, S, nxt.data_ptr(), x.data_ptr(), Hd, y.data_ptr(), Hd,
+                x.data_ptr(), Hd, hp, S, nxt.data_ptr(), x.data_ptr(), Hd, y.data_ptr(), TILED,
                 T, Hd, cfg.eps, s))
-        return self._linear(y, self.lm_head, out_dtype=torch.float32)
+        return self._linear(y.data_ptr(), TILED, T, self.lm_head, out_dtype=torch.float32)
 
     # ------------------------------------------------------------------ prompt
     @torch.no_grad()

@@ -187,3 +187,61 @@ def test_linear_silu_rejects_split_k():
     rc = L.rspx_linear_silu(x.data_ptr(), K, w.data_ptr(), K, out.data_ptr(), N // 2, 4, N, K,
                             _lib.stream_ptr(x.device))
     assert rc == -2   # RSPX_EUNSUPPORTED
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (7, 1024, 4096), (64, 6144, 4096), (130, 512, 768),
+                                   (64, 24576, 4096), (200, 256, 12288)])
+def test_linear_tiled_x_is_bitwise_row_major(M, N, K):
+    """x in the tiled layout (RSPX_TILED) gives the row-major result bit for bit, through
+    rspx_linear (bf16 and fp32 out) and rspx_linear_partials; rows past M in the last
+    64-row block hold NaN and must not reach any stored output."""
+    from _tiled import to_tiled
+    from respect_amd import _lib
+    from respect_amd.kernels.gemm import linear
+    print(f"[linear tiled] M={M} N={N} K={K}", flush=True)
+    L = _lib.lib()
+    x, w = _xw(M * 7 + N, M, N, K)
+    xd, wd = _dev(x), _dev(w)
+    xt = to_tiled(xd, fill=float("nan"))
+    s = _lib.stream_ptr(xd.device)
+    ws = _lib.workspace(xd.device, max(L.rspx_linear_workspace_bytes(M, N, K), 16), tag="linear")
+    for fp32 in (0, 1):
+        ref = linear(xd, wd, out_dtype=torch.float32 if fp32 else torch.bfloat16)
+        out = torch.empty_like(ref)
+        _lib.check("rspx_linear", L.rspx_linear(xt.data_ptr(), _lib.RSPX_TILED, wd.data_ptr(), K, out.data_ptr(), N,
+                                                M, N, K, fp32, ws.data_ptr(), ws.numel(), s))
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+    S = L.rspx_linear_splits(N, K)
+    parts = []
+    for xp, sx in ((xd, K), (xt, _lib.RSPX_TILED)):
+        part = torch.empty((S, M, N), dtype=torch.float32, device="cuda")
+        _lib.check("rspx_linear_partials", L.rspx_linear_partials(xp.data_ptr(), sx, wd.data_ptr(), K,
+                                                                  part.data_ptr(), M, N, K, s))
+        parts.append(part)
+    torch.cuda.synchronize()
+    assert torch.equal(parts[0], parts[1])
+
+
+@pytest.mark.parametrize("M", [1, 7, 64, 130])
+def test_linear_silu_tiled_in_and_out(M):
+    """rspx_linear_silu with a tiled x and a tiled output equals the row-major call, re-tiled."""
+    from _tiled import from_tiled, to_tiled
+    from respect_amd import _lib
+    F, K = 8192, 256
+    print(f"[linear_silu tiled] M={M}", flush=True)
+    L = _lib.lib()
+    x, w = _xw(M + 101, M, 2 * F, K)
+    xd, wd = _dev(x), _dev(w)
+    s = _lib.stream_ptr(xd.device)
+    ref = torch.empty((M, F), dtype=torch.bfloat16, device="cuda")
+    _lib.check("rspx_linear_silu", L.rspx_linear_silu(xd.data_ptr(), K, wd.data_ptr(), K, ref.data_ptr(), F,
+                                                       M, 2 * F, K, s))
+    out = torch.full((-(-M // 64) * 64 * F,), float("nan"), dtype=torch.bfloat16, device="cuda")
+    xt = to_tiled(xd, fill=float("nan"))
+    _lib.check("rspx_linear_silu", L.rspx_linear_silu(xt.data_ptr(), _lib.RSPX_TILED, wd.data_ptr(), K,
+                                                       out.data_ptr(), _lib.RSPX_TILED, M, 2 * F, K, s))
+    torch.cuda.synchronize()
+    assert torch.equal(from_tiled(out, M, F), ref)
+    # rows past M were not written
+    assert torch.isnan(out.float()).sum().item() == (-(-M // 64) * 64 - M) * F

@@ -120,3 +120,35 @@ def test_kernel_errors():
     with pytest.raises(RspxError):
         c = torch.ones(1, 2, 64, device="cuda", dtype=torch.bfloat16)
         rope(torch.ones(1, 1, 2, 64, device="cuda", dtype=torch.bfloat16), c, c)
+
+
+@pytest.mark.parametrize("rows,n", [(1, 4096), (7, 4096), (64, 4096), (130, 4096), (9, 256), (64, 12288)])
+def test_rmsnorm_tiled_output(rows, n):
+    """y written in the tiled layout (RSPX_TILED) holds the row-major result's bits, for
+    rspx_rmsnorm and rspx_add_rmsnorm_partials, and nothing outside rows [0, rows)."""
+    from _tiled import from_tiled, tiled_rows
+    from respect_amd import _lib
+    print(f"[rmsnorm tiled] rows={rows} n={n}", flush=True)
+    L = _lib.lib()
+    s = _lib.stream_ptr(torch.device("cuda"))
+    g = torch.Generator(device="cuda").manual_seed(rows * 13 + n)
+    x = torch.randn((rows, n), generator=g, device="cuda").to(torch.bfloat16)
+    w = (1 + 0.02 * torch.randn(n, generator=g, device="cuda")).to(torch.bfloat16)
+    hp = torch.randn((2, rows, n), generator=g, device="cuda")
+    ref = torch.empty_like(x)
+    out = torch.full((tiled_rows(rows) * n,), float("nan"), dtype=torch.bfloat16, device="cuda")
+    _lib.check("rspx_rmsnorm", L.rspx_rmsnorm(x.data_ptr(), n, w.data_ptr(), ref.data_ptr(), n, rows, n, 1e-6, s))
+    _lib.check("rspx_rmsnorm", L.rspx_rmsnorm(x.data_ptr(), n, w.data_ptr(), out.data_ptr(), _lib.RSPX_TILED, rows,
+                                              n, 1e-6, s))
+    torch.cuda.synchronize()
+    assert torch.equal(from_tiled(out, rows, n), ref)
+    assert torch.isnan(out.float()).sum().item() == (tiled_rows(rows) - rows) * n
+    xo1, xo2 = torch.empty_like(x), torch.empty_like(x)
+    _lib.check("rspx_add_rmsnorm_partials", L.rspx_add_rmsnorm_partials(
+        x.data_ptr(), n, hp.data_ptr(), 2, w.data_ptr(), xo1.data_ptr(), n, ref.data_ptr(), n, rows, n, 1e-6, s))
+    _lib.check("rspx_add_rmsnorm_partials", L.rspx_add_rmsnorm_partials(
+        x.data_ptr(), n, hp.data_ptr(), 2, w.data_ptr(), xo2.data_ptr(), n, out.data_ptr(), _lib.RSPX_TILED, rows, n,
+        1e-6, s))
+    torch.cuda.synchronize()
+    assert torch.equal(from_tiled(out, rows, n), ref)
+    assert torch.equal(xo1, xo2)
