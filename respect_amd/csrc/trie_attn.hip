@@ -596,6 +596,10 @@ constexpr int kChunk = 64;  // node slots staged in LDS at a time
 // many of V rows, then the fp32 scores of up to kMaxNodeRows rows x kChunk
 // slots, then the node partials of those rows.  Streaming uses buffer 0; a
 // prefetched segment of up to kResident chunks sits in buffers 0, 1, ...
+// The scores of a whole prefetched segment (rows x kResident kChunk slots,
+// row stride SROW2) go to S2OFF: the node-partial rows themselves when they
+// are as wide (D = 128; a row's scores are read before its partial is
+// written), else an area of their own.
 constexpr int kMaxNodeRows = 64;  // a workgroup's node rows: at most one prompt row block
 constexpr int kResident = 2;  // node chunks a prefetching caller keeps in LDS at once
 template <int D> struct NodeLds {
@@ -606,7 +610,10 @@ template <int D> struct NodeLds {
   static constexpr int SROW = kChunk + 4;  // floats per score row
   static constexpr int NPOFF = SOFF + kMaxNodeRows * SROW * 4;
   static constexpr int NPROW = D + 4;      // node partial of a row: m, l, pad, pad, acc[D]
-  static constexpr int BYTES = NPOFF + kMaxNodeRows * NPROW * 4;
+  static constexpr int NPEND = NPOFF + kMaxNodeRows * NPROW * 4;
+  static constexpr int SROW2 = kResident * kChunk + 4;  // floats per row of a whole segment's scores
+  static constexpr int S2OFF = NPROW == SROW2 ? NPOFF : NPEND;
+  static constexpr int BYTES = NPROW == SROW2 ? NPEND : NPEND + kMaxNodeRows * SROW2 * 4;
   static __device__ __forceinline__ lds_char* kbuf(lds_char* kv, int b) { return kv + b * KBYTES; }
   static __device__ __forceinline__ lds_char* vbuf(lds_char* kv, int b) { return kv + VOFF + b * VBYTES; }
 };
@@ -700,12 +707,12 @@ __device__ __forceinline__ uint64_t node_masks(const TrieAttnArgs& A, int p0, in
 }
 
 // Scores q.k times A.c of rows [p0, rend) (at most kMaxNodeRows) and chunk
-// c0's slots into S ([row - p0][SROW], fp32) with one 16x16x32 MFMA chain per
+// c0's slots into S ([row - p0][SR], fp32) with one 16x16x32 MFMA chain per
 // task (row tile rt, slot tile kt); waves take tasks w, w + nw, ...  With
 // use_pre, `qpre` is the fragment of task w.  Each score depends only on its
 // row's q and its slot's k: neither the tile nor the lane position changes
 // its bits.
-template <int D>
+template <int D, int SR = NodeLds<D>::SROW>
 __device__ __forceinline__ void node_scores(const TrieAttnArgs& A, int g, int p0, int rend, int c0,
                                             const lds_char* kv, lds_float* S, int w, int nw,
                                             const bf16x8 (&qpre)[D / 32], bool use_pre) {
@@ -731,7 +738,7 @@ __device__ __forceinline__ void node_scores(const TrieAttnArgs& A, int g, int p0
     }
     // Lane (n16, g4), element j: slot 16 kt + 4 g4 + j of row p0 + 16 rt + n16.
     const f32x4 o = sv * A.c;
-    *(__attribute__((address_space(3))) f32x4*)(S + (16 * rt + (lane & 15)) * NodeLds<D>::SROW + 16 * kt +
+    *(__attribute__((address_space(3))) f32x4*)(S + (16 * rt + (lane & 15)) * SR + 16 * kt +
                                                 4 * (lane >> 4)) = o;
   }
 }
@@ -755,6 +762,44 @@ template <> struct NodeLane<1> {
   static __device__ __forceinline__ float at(T v, int) { return __uint_as_float((uint32_t)v << 16); }
 };
 
+// l += p_j and acc += p_j v_j over the slots j of `mm` (bit j = slot j of the
+// chunk) in increasing order, one slot at a time: p_j is lane j's `p`, v_j the
+// chunk's V row j at vl (this lane's head_dim [DL lane, +DL)).
+template <int D>
+__device__ __forceinline__ void node_accumulate(uint64_t mm, float p, const lds_char* vl, float& l,
+                                                float (&acc)[D / 64]) {
+  constexpr int DL = D / 64;
+  constexpr int RB = 2 * D;                          // bytes per node row
+  constexpr int kB = 8;                              // slots per batch
+  typedef NodeLane<DL> NL;
+  typedef typename NL::T LaneT;
+  while (mm != 0) {
+    int js[kB];
+    bool on[kB];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      on[u] = mm != 0;
+      js[u] = on[u] ? __builtin_ctzll(mm) : 0;
+      mm &= mm - 1;
+    }
+    LaneT vr[kB];
+    float pu[kB];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      vr[u] = *(const __attribute__((address_space(3))) LaneT*)(vl + js[u] * RB);
+      pu[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), js[u]));
+    }
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      if (on[u]) {
+        l += pu[u];
+#pragma unroll
+        for (int k = 0; k < DL; ++k) acc[k] = __builtin_fmaf(pu[u], NL::at(vr[u], k), acc[k]);
+      }
+    }
+  }
+}
+
 // Node partials of rows [p0, rend) of kv head g (at most kMaxNodeRows) over
 // each row's allowed node slots (attention.py:52-67): m is the maximum score
 // over every allowed slot, p = exp2(score - m) in fp32, and l and acc are sums
@@ -764,7 +809,9 @@ template <> struct NodeLane<1> {
 // this is wave w) calls it; row p0 + w + 8 i is wave w's round i, and its
 // partial (m, l, acc) is left in the node-partial area of LDS (row i * 8 + w)
 // for the same wave to read.  With more than one chunk a first pass over K
-// finds m.  have_pre: the caller issued a segment of at most kResident chunks
+// finds m -- except for a prefetched segment of more than one chunk, whose
+// scores are all taken at once (one pass: the same m, p and sums).
+// have_pre: the caller issued a segment of at most kResident chunks
 // (chunk c into buffer c) and `pre` (node_prefetch), has since waited for them
 // (vmcnt 0) and passed a workgroup barrier; otherwise chunks stream through
 // buffer 0.  Does nothing when NN = 0.  Ends with every
@@ -774,10 +821,6 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
                                           const NodePre<D>& pre, bool have_pre) {
   constexpr int nw = kWavesA;
   constexpr int DL = D / 64;
-  constexpr int RB = 2 * D;                          // bytes per node row
-  constexpr int kB = 8;                              // slots per accumulation batch
-  typedef NodeLane<DL> NL;
-  typedef typename NL::T LaneT;
   const int lane = __lane_id();
   const int NN = A.NN;
   if (NN == 0) return;
@@ -786,6 +829,42 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
   lds_float* NP = (lds_float*)(kv + NodeLds<D>::NPOFF);
   const bool one = NN <= kChunk;
   const bool res = have_pre && NN <= kResident * kChunk;  // every chunk already in buffer c
+
+  if (res && !one) {
+    // Two resident chunks: every score at once, then per row the maximum over
+    // all its allowed slots and the sums over chunk 0's slots, then chunk 1's.
+    static_assert(kResident == 2, "two resident chunks");
+    lds_float* S2 = (lds_float*)(kv + NodeLds<D>::S2OFF);
+    constexpr int SR2 = NodeLds<D>::SROW2;
+    node_scores<D, SR2>(A, g, p0, rend, 0, NodeLds<D>::kbuf(kv, 0), S2, w, nw, pre.qf, true);
+    node_scores<D, SR2>(A, g, p0, rend, kChunk, NodeLds<D>::kbuf(kv, 1), S2 + kChunk, w, nw, pre.qf, true);
+    lds_barrier();
+    const uint64_t mb0 = pre.mb[0], mb1 = pre.mb[1];
+#pragma unroll 1
+    for (int i = 0; i < nrd; ++i) {
+      const int row = w + nw * i;
+      const lds_float* sr = S2 + row * SR2;
+      const float s0 = sr[lane], s1 = sr[kChunk + lane];
+      const bool ok0 = ((mb0 >> (8 * i)) & 0xff) != 0, ok1 = ((mb1 >> (8 * i)) & 0xff) != 0;
+      const float m = max64(fmaxf(ok0 ? s0 : kNegInf, ok1 ? s1 : kNegInf));
+      const float pa = ok0 ? fexp2(s0 - m) : 0.f, pb = ok1 ? fexp2(s1 - m) : 0.f;
+      const uint64_t m0 = __builtin_amdgcn_ballot_w64(ok0), m1 = __builtin_amdgcn_ballot_w64(ok1);
+      float l = 0.f, acc[DL];
+#pragma unroll
+      for (int k = 0; k < DL; ++k) acc[k] = 0.f;
+      node_accumulate<D>(m0, pa, NodeLds<D>::vbuf(kv, 0) + DL * 2 * lane, l, acc);
+      node_accumulate<D>(m1, pb, NodeLds<D>::vbuf(kv, 1) + DL * 2 * lane, l, acc);
+      // The row's scores are in registers; its partial may now overwrite them.
+      lds_float* np = NP + row * NodeLds<D>::NPROW;
+      if (lane == 0) {
+        np[0] = m;
+        np[1] = l;
+      }
+#pragma unroll
+      for (int k = 0; k < DL; ++k) np[4 + DL * lane + k] = acc[k];
+    }
+    return;
+  }
 
   if (!one) {
     for (int c0 = 0; c0 < NN; c0 += kChunk) {
@@ -842,7 +921,7 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
       lds_float* np = NP + row * NodeLds<D>::NPROW;
       const float m = one ? max64(ok ? s : kNegInf) : np[0];
       const float p = ok ? fexp2(s - m) : 0.f;
-      uint64_t mm = __builtin_amdgcn_ballot_w64(ok);  // wave-uniform: the row's allowed slots
+      const uint64_t mm = __builtin_amdgcn_ballot_w64(ok);  // wave-uniform: the row's allowed slots
       float l = 0.f, acc[DL];
 #pragma unroll
       for (int k = 0; k < DL; ++k) acc[k] = 0.f;
@@ -851,31 +930,7 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
 #pragma unroll
         for (int k = 0; k < DL; ++k) acc[k] = np[4 + DL * lane + k];
       }
-      while (mm != 0) {
-        int js[kB];
-        bool on[kB];
-#pragma unroll
-        for (int u = 0; u < kB; ++u) {
-          on[u] = mm != 0;
-          js[u] = on[u] ? __builtin_ctzll(mm) : 0;
-          mm &= mm - 1;
-        }
-        LaneT vr[kB];
-        float pu[kB];
-#pragma unroll
-        for (int u = 0; u < kB; ++u) {
-          vr[u] = *(const __attribute__((address_space(3))) LaneT*)(vl + js[u] * RB);
-          pu[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), js[u]));
-        }
-#pragma unroll
-        for (int u = 0; u < kB; ++u) {
-          if (on[u]) {
-            l += pu[u];
-#pragma unroll
-            for (int k = 0; k < DL; ++k) acc[k] = __builtin_fmaf(pu[u], NL::at(vr[u], k), acc[k]);
-          }
-        }
-      }
+      node_accumulate<D>(mm, p, vl, l, acc);
       if (lane == 0) {
         np[0] = m;
         np[1] = l;

@@ -230,17 +230,25 @@ def _status(case, ws):
     return _lib.lib().rspx_trie_attn_status(ws.data_ptr(), H, HK, M, P, D, _lib.stream_ptr(ws.device))
 
 
-@pytest.mark.parametrize("which", ["cfg1", "cfg2", "base37", "long", "gqa2", "d64"])
+@pytest.mark.parametrize("which", ["cfg1", "cfg2", "base37", "base100", "n64b40", "long", "gqa2", "d64",
+                                   "d64b90"])
 def test_one_and_two_launches_equal(which):
     """The one-kernel path (prompt groups, node partials and merge with workgroups
     waiting on per-row-block counters) and the two-kernel path give the same
     bits; the counters are back at zero after each call (repeat calls on one
-    workspace stay equal) and no wait ran out."""
+    workspace stay equal) and no wait ran out.  base100 / n64b40 / d64b90 put
+    65-128 slots in the node segment: the one-kernel path takes them in one
+    pass over two prefetched chunks, the two-kernel path streams them in two
+    passes (a maximum pass, then the sums)."""
     from respect_amd import _lib
     c = {"cfg1": gen.cfg1, "cfg2": gen.cfg2, "base37": lambda: gen.cfg2(seed=4, base=37),
+         "base100": lambda: gen.cfg2(seed=4, base=100),
+         "n64b40": lambda: gen.attn_case(11, 32, 8, 128, 3072, 4, 24, 0, 16, 64, kv_scale=128 ** -0.5, base=40),
          "long": lambda: gen.attn_case(8, 32, 8, 128, 16384, 8, 32, 0, 32, 128, kv_scale=128 ** -0.5),
          "gqa2": lambda: gen.attn_case(7, 16, 8, 128, 700, 3, 9, 0, 6, None),
-         "d64": lambda: gen.attn_case(7, 16, 2, 64, 3086, 3, 9, 0, 6, None)}[which]()
+         "d64": lambda: gen.attn_case(7, 16, 2, 64, 3086, 3, 9, 0, 6, None),
+         "d64b90": lambda: gen.attn_case(7, 16, 2, 64, 3086, 3, 9, 0, 6, None, base=90)}[which]()
+    print(f"[one/two launches] {which} NN={c.kn.shape[1]}", flush=True)
     H, M, D = c.q.shape
     HK, P, _ = c.kp.shape
     need = _lib.lib().rspx_trie_attn_workspace_bytes(H, HK, M, P, D)
