@@ -229,7 +229,8 @@ int rspx_add_rmsnorm(const void* r, int64_t sr, const void* h, int64_t sh, const
                      void* y, int64_t sy, int rows, int n, float eps, void* stream);
 
 /* The same with h given as the fp32 chunk partials hp[S][rows][n] of a
- * linear layer (rspx_linear_partials): h = bf16 of their chunk-order sum,
+ * linear layer (rspx_linear_partials; 1 <= S <= 8, the most
+ * rspx_linear_splits gives): h = bf16 of their chunk-order sum,
  * bit for bit the h rspx_linear would have produced.
  */
 int rspx_add_rmsnorm_partials(const void* r, int64_t sr, const float* hp, int S, const void* w, void* xo, int64_t sxo,
@@ -248,7 +249,7 @@ int rspx_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* wq, const voi
                         void* stream);
 
 /* The same with the projection given as fp32 chunk partials
- * qkvp[S][T][(HQ + 2 HK) D] (rspx_linear_partials).
+ * qkvp[S][T][(HQ + 2 HK) D] (rspx_linear_partials; 1 <= S <= 8).
  */
 int rspx_qkv_rope_cache_partials(const float* qkvp, int S, const void* wq, const void* wk, const void* cos,
                                  const void* sin, int64_t scs, const int32_t* slots, void* cache_k, int64_t skh,

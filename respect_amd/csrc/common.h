@@ -74,16 +74,55 @@ constexpr int64_t kTiled = -1;
 
 // The output of a K-split linear layer: the fp32 chunk partials of one
 // element added in chunk order, ((p0 + p1) + p2) + ... (stride = elements
-// between chunks).  Every consumer of split partials uses this, so the value
-// (and its bf16 rounding) is the same wherever the sum is taken.
+// between chunks, 1 <= S <= SC).  Every consumer of split partials uses this,
+// so the value (and its bf16 rounding) is the same wherever the sum is taken.
+// SC (1, 2, 4 or kMaxSplits, a compile-time bound) lets every load be issued
+// before the first add, without branches: chunk s >= S re-reads chunk S - 1
+// and its add is not taken.  The chunks then arrive in one memory latency
+// instead of S in a row.
+constexpr int kMaxSplits = 8;
+template <int SC>
 __device__ __forceinline__ f32x4 sum_parts4(const float* p, int S, int64_t stride) {
-  f32x4 v = *reinterpret_cast<const f32x4*>(p);
-  for (int s = 1; s < S; ++s) {
-    const f32x4 q = *reinterpret_cast<const f32x4*>(p + s * stride);
+  f32x4 q[SC];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = v[e] + q[e];
-  }
+  for (int s = 0; s < SC; ++s) q[s] = *reinterpret_cast<const f32x4*>(p + (int64_t)(s < S ? s : S - 1) * stride);
+  f32x4 v = q[0];
+#pragma unroll
+  for (int s = 1; s < SC; ++s)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = s < S ? v[e] + q[s][e] : v[e];
   return v;
 }
+
+// Eight consecutive elements (two f32x4 at p and p + 4) the same way.
+template <int SC>
+__device__ __forceinline__ void sum_parts8(const float* p, int S, int64_t stride, f32x4& a, f32x4& b) {
+  f32x4 qa[SC], qb[SC];
+#pragma unroll
+  for (int s = 0; s < SC; ++s) {
+    const float* ps = p + (int64_t)(s < S ? s : S - 1) * stride;
+    qa[s] = *reinterpret_cast<const f32x4*>(ps);
+    qb[s] = *reinterpret_cast<const f32x4*>(ps + 4);
+  }
+  a = qa[0];
+  b = qb[0];
+#pragma unroll
+  for (int s = 1; s < SC; ++s) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a[e] = s < S ? a[e] + qa[s][e] : a[e];
+      b[e] = s < S ? b[e] + qb[s][e] : b[e];
+    }
+  }
+}
+
+// The compile-time bound SC for a run-time chunk count S (1 <= S <= 8).
+#define RSPX_WITH_SPLITS(S, SC, ...)                                  \
+  do {                                                                \
+    if ((S) <= 1) { constexpr int SC = 1; __VA_ARGS__; }              \
+    else if ((S) <= 2) { constexpr int SC = 2; __VA_ARGS__; }         \
+    else if ((S) <= 4) { constexpr int SC = 4; __VA_ARGS__; }         \
+    else { constexpr int SC = kMaxSplits; __VA_ARGS__; }              \
+  } while (0)
 
 }  // namespace rspx

@@ -76,7 +76,7 @@ struct RowIn {
   uint16_t* xo; int64_t sxo;
 };
 
-template <int MODE>
+template <int MODE, int SC>
 __device__ __forceinline__ void load_row_vec(const RowIn& in, int row, int c, float* v) {
   unpack8(*reinterpret_cast<const u32x4*>(in.x + row * in.sx + c), v);
   if constexpr (MODE >= 1) {
@@ -85,7 +85,8 @@ __device__ __forceinline__ void load_row_vec(const RowIn& in, int row, int c, fl
       unpack8(*reinterpret_cast<const u32x4*>(in.h + row * in.sh + c), hv);
     } else {
       const float* hp = in.hp + row * in.shp + c;
-      const f32x4 a = sum_parts4(hp, in.S, in.sps), b = sum_parts4(hp + 4, in.S, in.sps);
+      f32x4 a, b;
+      sum_parts8<SC>(hp, in.S, in.sps, a, b);
 #pragma unroll
       for (int e = 0; e < 4; ++e) { hv[e] = round_bf16(a[e]); hv[4 + e] = round_bf16(b[e]); }
     }
@@ -103,7 +104,7 @@ __device__ __forceinline__ uint16_t* out_at(uint16_t* y, int64_t sy, int row, in
   return y + (sy == kTiled ? tiled_offset(row, c, n) : row * sy + c);
 }
 
-template <int TPR, int VPL, int MODE>
+template <int TPR, int VPL, int MODE, int SC>
 __device__ __forceinline__ void rms_row_wave(const RowIn& in, int row, const uint16_t* w, uint16_t* y, int64_t sy,
                                              int sub, int n, float eps) {
   float xv[VPL][8];
@@ -112,7 +113,7 @@ __device__ __forceinline__ void rms_row_wave(const RowIn& in, int row, const uin
   for (int v = 0; v < VPL; ++v) {
     const int c = (v * TPR + sub) * 8;
     if (c < n) {
-      load_row_vec<MODE>(in, row, c, xv[v]);
+      load_row_vec<MODE, SC>(in, row, c, xv[v]);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) xv[v][i] = 0.f;
@@ -138,19 +139,19 @@ __device__ __forceinline__ void rms_row_wave(const RowIn& in, int row, const uin
 }  // namespace
 
 // Rows of up to 64*8*VPL elements: one row per TPR lanes of a wave.
-template <int TPR, int VPL, int MODE>
+template <int TPR, int VPL, int MODE, int SC>
 __global__ __launch_bounds__(256) void rmsnorm_small_kernel(RowIn in, const uint16_t* w, uint16_t* y, int64_t sy,
                                                             int rows, int n, float eps) {
   const int lane = __lane_id();
   const int row = (blockIdx.x * 256 + threadIdx.x) / TPR;
   const int sub = lane % TPR;
   if (row >= rows) return;   // whole lane groups leave together (TPR divides 64)
-  rms_row_wave<TPR, VPL, MODE>(in, row, w, y, sy, sub, n, eps);
+  rms_row_wave<TPR, VPL, MODE, SC>(in, row, w, y, sy, sub, n, eps);
 }
 
 // Long rows: one 256-thread workgroup per row, VPL 8-element vectors per
 // thread.  Wave sums are combined in wave order through LDS.
-template <int VPL, int MODE>
+template <int VPL, int MODE, int SC>
 __global__ __launch_bounds__(256) void rmsnorm_row_kernel(RowIn in, const uint16_t* w, uint16_t* y, int64_t sy, int n,
                                                           float eps) {
   __shared__ float part[4];
@@ -162,7 +163,7 @@ __global__ __launch_bounds__(256) void rmsnorm_row_kernel(RowIn in, const uint16
   for (int v = 0; v < VPL; ++v) {
     const int c = (v * 256 + t) * 8;
     if (c < n) {
-      load_row_vec<MODE>(in, row, c, xv[v]);
+      load_row_vec<MODE, SC>(in, row, c, xv[v]);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) xv[v][i] = 0.f;
@@ -278,6 +279,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* q, in
 // q goes to qo [T, HQ, D], k and v are written straight into the KV cache at
 // the token's physical slot: cache[h][slot[t]][:] (head stride sh, slot
 // stride sn).
+template <int SC>
 __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(const uint16_t* qkv, int64_t sqkv, const float* qp,
                                                              int S, int64_t sps, const uint16_t* wq,
                                                              const uint16_t* wk, const uint16_t* cosb,
@@ -299,7 +301,8 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(const uint16_t* qkv
   u32x4 raw;
   if (qp) {  // the projection's fp32 chunk partials, summed and rounded as rspx_linear would
     const float* p = qp + (int64_t)t * sqkv + col;
-    const f32x4 a = sum_parts4(p, S, sps), b = sum_parts4(p + 4, S, sps);
+    f32x4 a, b;
+    sum_parts8<SC>(p, S, sps, a, b);
     raw[0] = pack_bf16x2(a[0], a[1]); raw[1] = pack_bf16x2(a[2], a[3]);
     raw[2] = pack_bf16x2(b[0], b[1]); raw[3] = pack_bf16x2(b[2], b[3]);
   } else {
@@ -335,24 +338,24 @@ static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) 
 
 namespace rspx {
 // The split depends on n only (never on rows), for every input mode.
-template <int MODE>
+template <int MODE, int SC>
 static void launch_rmsnorm(const RowIn& in, const uint16_t* W, uint16_t* Y, int64_t sy, int rows, int n, float eps,
                            hipStream_t s) {
   const int vec = n / 8;
   if (vec <= 16) {
-    hipLaunchKernelGGL((rmsnorm_small_kernel<16, 1, MODE>), dim3((rows * 16 + 255) / 256), dim3(256), 0, s, in, W, Y,
+    hipLaunchKernelGGL((rmsnorm_small_kernel<16, 1, MODE, SC>), dim3((rows * 16 + 255) / 256), dim3(256), 0, s, in, W, Y,
                        sy, rows, n, eps);
   } else if (vec <= 64) {
-    hipLaunchKernelGGL((rmsnorm_small_kernel<64, 1, MODE>), dim3((rows * 64 + 255) / 256), dim3(256), 0, s, in, W, Y,
+    hipLaunchKernelGGL((rmsnorm_small_kernel<64, 1, MODE, SC>), dim3((rows * 64 + 255) / 256), dim3(256), 0, s, in, W, Y,
                        sy, rows, n, eps);
   } else if (vec <= 256) {
-    hipLaunchKernelGGL((rmsnorm_row_kernel<1, MODE>), dim3(rows), dim3(256), 0, s, in, W, Y, sy, n, eps);
+    hipLaunchKernelGGL((rmsnorm_row_kernel<1, MODE, SC>), dim3(rows), dim3(256), 0, s, in, W, Y, sy, n, eps);
   } else if (vec <= 512) {
-    hipLaunchKernelGGL((rmsnorm_row_kernel<2, MODE>), dim3(rows), dim3(256), 0, s, in, W, Y, sy, n, eps);
+    hipLaunchKernelGGL((rmsnorm_row_kernel<2, MODE, SC>), dim3(rows), dim3(256), 0, s, in, W, Y, sy, n, eps);
   } else if (vec <= 1024) {
-    hipLaunchKernelGGL((rmsnorm_row_kernel<4, MODE>), dim3(rows), dim3(256), 0, s, in, W, Y, sy, n, eps);
+    hipLaunchKernelGGL((rmsnorm_row_kernel<4, MODE, SC>), dim3(rows), dim3(256), 0, s, in, W, Y, sy, n, eps);
   } else {
-    hipLaunchKernelGGL((rmsnorm_row_kernel<8, MODE>), dim3(rows), dim3(256), 0, s, in, W, Y, sy, n, eps);
+    hipLaunchKernelGGL((rmsnorm_row_kernel<8, MODE, SC>), dim3(rows), dim3(256), 0, s, in, W, Y, sy, n, eps);
   }
 }
 }  // namespace rspx
@@ -377,7 +380,7 @@ extern "C" int rspx_rmsnorm(const void* x, int64_t sx, const void* w, void* y, i
   if (!al16(x) || !al16(w) || !al16(y) || sx % 8) return RSPX_EALIGN;
   if ((rc = norm_out_ok(sy, n)) != RSPX_OK) return rc;
   RowIn in{static_cast<const uint16_t*>(x), sx, nullptr, 0, nullptr, 0, 0, 1, nullptr, 0};
-  launch_rmsnorm<0>(in, static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy, rows, n, eps,
+  launch_rmsnorm<0, 1>(in, static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy, rows, n, eps,
                     static_cast<hipStream_t>(stream));
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }
@@ -391,7 +394,7 @@ extern "C" int rspx_add_rmsnorm(const void* r, int64_t sr, const void* h, int64_
   if ((rc = norm_out_ok(sy, n)) != RSPX_OK) return rc;
   RowIn in{static_cast<const uint16_t*>(r), sr, static_cast<const uint16_t*>(h), sh, nullptr, 0, 0, 1,
            static_cast<uint16_t*>(xo), sxo};
-  launch_rmsnorm<1>(in, static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy, rows, n, eps,
+  launch_rmsnorm<1, 1>(in, static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy, rows, n, eps,
                     static_cast<hipStream_t>(stream));
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }
@@ -400,14 +403,14 @@ extern "C" int rspx_add_rmsnorm_partials(const void* r, int64_t sr, const float*
                                          int64_t sxo, void* y, int64_t sy, int rows, int n, float eps, void* stream) {
   int rc = norm_args_ok(rows, n);
   if (rc != RSPX_OK || rows == 0) return rc;
-  if (S < 1) return RSPX_EINVAL;
+  if (S < 1 || S > kMaxSplits) return RSPX_EINVAL;
   if (!r || !hp || !w || !xo || !y) return RSPX_EINVAL;
   if (!al16(r) || !al16(hp) || !al16(w) || !al16(xo) || !al16(y) || sr % 8 || sxo % 8) return RSPX_EALIGN;
   if ((rc = norm_out_ok(sy, n)) != RSPX_OK) return rc;
   RowIn in{static_cast<const uint16_t*>(r), sr, nullptr, 0, hp, n, (int64_t)rows * n, S, static_cast<uint16_t*>(xo),
            sxo};
-  launch_rmsnorm<2>(in, static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy, rows, n, eps,
-                    static_cast<hipStream_t>(stream));
+  RSPX_WITH_SPLITS(S, SC, launch_rmsnorm<2, SC>(in, static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy,
+                                                  rows, n, eps, static_cast<hipStream_t>(stream)));
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }
 
@@ -467,12 +470,14 @@ static int qkv_rope_cache_launch(const uint16_t* qkv, int64_t sqkv, const float*
   if (sqkv % 8 || scs % 8 || skh % 8 || skn % 8 || svh % 8 || svn % 8) return RSPX_EALIGN;
   if (sqkv < (int64_t)(HQ + 2 * HK) * D) return RSPX_EINVAL;
   const int64_t threads = (int64_t)T * (HQ + 2 * HK) * 16;
-  hipLaunchKernelGGL(qkv_rope_cache_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), qkv, sqkv, qp, S, sps,
-                     static_cast<const uint16_t*>(wq), static_cast<const uint16_t*>(wk),
-                     static_cast<const uint16_t*>(cosb), static_cast<const uint16_t*>(sinb), scs, slots,
-                     static_cast<uint16_t*>(cache_k), skh, skn, static_cast<uint16_t*>(cache_v), svh, svn,
-                     static_cast<uint16_t*>(qo), T, HQ, HK, eps);
+  RSPX_WITH_SPLITS(qp ? S : 1, SC,
+                   hipLaunchKernelGGL((qkv_rope_cache_kernel<SC>), dim3((unsigned)((threads + 255) / 256)), dim3(256),
+                                      0, static_cast<hipStream_t>(stream), qkv, sqkv, qp, S, sps,
+                                      static_cast<const uint16_t*>(wq), static_cast<const uint16_t*>(wk),
+                                      static_cast<const uint16_t*>(cosb), static_cast<const uint16_t*>(sinb), scs,
+                                      slots, static_cast<uint16_t*>(cache_k), skh, skn,
+                                      static_cast<uint16_t*>(cache_v), svh, svn, static_cast<uint16_t*>(qo), T, HQ,
+                                      HK, eps));
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }
 
@@ -490,7 +495,7 @@ extern "C" int rspx_qkv_rope_cache_partials(const float* qkvp, int S, const void
                                             void* cache_k, int64_t skh, int64_t skn, void* cache_v, int64_t svh,
                                             int64_t svn, void* qo, int T, int HQ, int HK, int D, float eps,
                                             void* stream) {
-  if (!qkvp || S < 1) return RSPX_EINVAL;
+  if (!qkvp || S < 1 || S > kMaxSplits) return RSPX_EINVAL;
   const int64_t n = (int64_t)(HQ + 2 * HK) * D;
   return qkv_rope_cache_launch(nullptr, n, qkvp, S, (int64_t)T * n, wq, wk, cosb, sinb, scs, slots, cache_k, skh,
                                skn, cache_v, svh, svn, qo, T, HQ, HK, D, eps, stream);
