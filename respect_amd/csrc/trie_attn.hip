@@ -1039,7 +1039,9 @@ __device__ __forceinline__ void merge_rounds(const TrieAttnArgs& A, int g, int p
 
 // ------------------------------------------------------------------ kernel B
 // Workgroup (g, c8): rows [8 c8, 8 c8 + 8) of kv head g, row 8 c8 + w on
-// wave w: node partial, then merge.
+// wave w: node partial, then merge.  A node segment of at most kResident
+// chunks is loaded whole up front (then taken in one pass); a longer one
+// streams.
 template <int D>
 __global__ __launch_bounds__(64 * kWavesA) void node_merge_kernel(TrieAttnArgs A) {
   __shared__ __attribute__((aligned(16))) char kv[NodeLds<D>::BYTES];
@@ -1048,8 +1050,14 @@ __global__ __launch_bounds__(64 * kWavesA) void node_merge_kernel(TrieAttnArgs A
   const int g = blockIdx.x / RC8;
   const int p0 = 8 * (blockIdx.x - g * RC8);
   const int rend = min(p0 + 8, A.R);
-  NodePre<D> none;
-  node_rows<D>(A, g, p0, rend, (lds_char*)kv, w, none, false);
+  NodePre<D> pre;
+  const bool pf = A.NN > 0 && A.NN <= kResident * kChunk;
+  if (pf) {
+    node_prefetch<D>(A, g, p0, rend, (lds_char*)kv, w, pre);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of the segment is in LDS
+    lds_barrier();                       // and every other wave's part
+  }
+  node_rows<D>(A, g, p0, rend, (lds_char*)kv, w, pre, pf);
   merge_rounds<D, false>(A, g, p0, rend, (const lds_char*)kv, w);
 }
 

@@ -237,9 +237,7 @@ def test_one_and_two_launches_equal(which):
     waiting on per-row-block counters) and the two-kernel path give the same
     bits; the counters are back at zero after each call (repeat calls on one
     workspace stay equal) and no wait ran out.  base100 / n64b40 / d64b90 put
-    65-128 slots in the node segment: the one-kernel path takes them in one
-    pass over two prefetched chunks, the two-kernel path streams them in two
-    passes (a maximum pass, then the sums)."""
+    65-128 slots in the node segment (two chunks, loaded whole by both paths)."""
     from respect_amd import _lib
     c = {"cfg1": gen.cfg1, "cfg2": gen.cfg2, "base37": lambda: gen.cfg2(seed=4, base=37),
          "base100": lambda: gen.cfg2(seed=4, base=100),
@@ -262,6 +260,26 @@ def test_one_and_two_launches_equal(which):
     for rpw in (1, 2):
         assert torch.equal(_run(c, launches=1, rows_per_wave=rpw, workspace=ws), two)
     assert _status(c, ws) == 0
+
+
+@pytest.mark.parametrize("shape", ["8b", "d64"])
+def test_one_and_two_pass_node_segments_equal(shape):
+    """The same trie and committed slots in a node segment of 128 slots (loaded whole and
+    taken in one pass: all scores, the row maximum, then the sums chunk by chunk) and of
+    192 / 256 slots (the extra slots masked out; streamed in two passes: a maximum pass, then
+    the sums) give the same bits, through one and two launches."""
+    args = {"8b": (11, 32, 8, 128, 3072, 4, 24, 0, 16, 64), "d64": (7, 16, 2, 64, 3086, 3, 9, 0, 6, None)}[shape]
+    kw = {"kv_scale": 128 ** -0.5} if shape == "8b" else {}
+    base = 40 if shape == "8b" else 90
+    short = gen.attn_case(*args, base=base, **kw)
+    assert 64 < short.kn.shape[1] <= 128
+    ref = _run(short, launches=2)
+    for step in (192, 256):
+        long = gen.attn_case(*args, base=base, nn_step=step, **kw)
+        assert long.kn.shape[1] == step and np.array_equal(long.msk[:, :short.kn.shape[1]], short.msk)
+        for launches in (1, 2):
+            assert torch.equal(_run(long, launches=launches), ref), f"NN={step} launches={launches}"
+    assert torch.equal(_run(short, launches=1), ref)
 
 
 def test_one_launch_workspace_shared_by_shapes():
