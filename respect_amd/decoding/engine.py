@@ -133,6 +133,7 @@ class Decoder:
         self.sm_scale = cfg.head_dim ** -0.5
         self._ws = {}
         self._ws_retired = []   # outgrown buffers: a captured graph may still point at them
+        self._rope = None       # (cos, sin) [positions, head_dim] bf16 tables
         self._graphs = {}
 
     def _workspace(self, name: str, nbytes: int) -> torch.Tensor:
@@ -147,6 +148,24 @@ class Decoder:
             ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)
             self._ws[name] = ws
         return ws
+
+    def _rope_rows(self, positions: torch.Tensor, cap: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """cos/sin rows [T, head_dim] of ``positions``, gathered from tables that
+        rope_tables computes once for positions [0, cap) -- the same bits as
+        computing them per call (every entry depends on its own position only),
+        in two gathers instead of a chain of element-wise launches.  A position
+        a cache of ``cap`` slots cannot hold is clamped into the table."""
+        t = self._rope
+        if t is None or t[0].shape[0] < cap:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("rotary tables must be sized before graph capture")
+            if t is not None:
+                self._ws_retired.append(t)
+            cfg = self.cfg
+            t = rope_tables(torch.arange(cap, device=self.device), cfg.head_dim, cfg.theta, device=self.device)
+            self._rope = t
+        idx = positions.clamp(0, t[0].shape[0] - 1)
+        return t[0].index_select(0, idx), t[1].index_select(0, idx)
 
     def _linear(self, x: int, sx: int, M: int, w: torch.Tensor, out_dtype=torch.bfloat16) -> torch.Tensor:
         """x (device pointer, row stride sx or RSPX_TILED, M rows) . w^T."""
@@ -196,7 +215,7 @@ class Decoder:
         y = torch.empty(rows * Hd, dtype=bf, device=dev)          # normalised rows [T, H], tiled
         _lib.check("rspx_rmsnorm", L.rspx_rmsnorm(x.data_ptr(), Hd, self.layers[0].in_norm.data_ptr(), y.data_ptr(),
                                                   TILED, T, Hd, cfg.eps, s))
-        cos, sin = rope_tables(positions, D, cfg.theta, device=dev)
+        cos, sin = self._rope_rows(positions, cache.cap)
         slots32 = slots.to(torch.int32)
         qo = torch.empty((T, HQ, D), dtype=bf, device=dev)
         att = torch.empty((T, HQ, D), dtype=bf, device=dev)
@@ -275,7 +294,8 @@ class GraphedForward:
         self.T, self.NN = T, NN
         self.scratch = cache.cap - T
         self.ids = torch.zeros(T, dtype=torch.int64, device=dev)
-        self.slots = torch.arange(self.scratch, self.scratch + T, dtype=torch.int32, device=dev)
+        self.pad_slots = torch.arange(self.scratch, self.scratch + T, dtype=torch.int32, device=dev)
+        self.slots = self.pad_slots.clone()
         self.pos = torch.zeros(T, dtype=torch.int64, device=dev)
         self.msk = torch.zeros(T, NN, dtype=torch.uint8, device=dev)
         self.msk[:, 0] = 1
@@ -296,8 +316,8 @@ class GraphedForward:
             self.ids[:n].copy_(ids)
         if slots is not None:
             self.slots[:n].copy_(slots)
-            self.slots[n:] = torch.arange(self.scratch + n, self.scratch + self.T, dtype=torch.int32,
-                                          device=self.slots.device)
+            if n < self.T:
+                self.slots[n:].copy_(self.pad_slots[n:])
         if pos is not None:
             self.pos[:n].copy_(pos)
         if msk is not None:
