@@ -266,6 +266,22 @@ int rspx_qkv_rope_cache_partials(const float* qkvp, int S, const void* wq, const
 int rspx_trie_mask(const int32_t* parent, int N, int base, int M, int NN, uint8_t* msk, int64_t smm, int32_t* depth,
                    void* stream);
 
+/* The row inputs of one forward from a step descriptor in device memory, so a
+ * captured forward takes a new trie (or a new token) from one host-to-device
+ * copy:  desc = [n, base, tok[0..T), parent[0..T)] (int32; parents precede
+ * children, -1 for a root).  Row i < n: ids[i] = tok[i] (0 if outside
+ * [0, vocab)), slots[i] = P + base + i, pos[i] = P + base + depth(i), and the
+ * mask row rspx_trie_mask gives node i; rows n..T-1: ids 0, slots pad0 + i,
+ * pos 0, slot 0 only.  A descriptor with n outside [0, T], base < 0 or
+ * base + n > NN is taken as n = 0.  ids, slots, pos: [T] int32; msk: [T, NN]
+ * uint8 (row stride smm).  No counterpart in the reference: it is
+ * respect/decoding/verify.py:22-41's mask and slot/position set-up moved onto
+ * the device for the decoder's captured forwards (also the 1-token path: a
+ * one-node trie at base = committed count).
+ */
+int rspx_step_inputs(const int32_t* desc, int T, int P, int NN, int pad0, int vocab, int32_t* ids, int32_t* slots,
+                     int32_t* pos, uint8_t* msk, int64_t smm, void* stream);
+
 /* ---------------------------------------------------------------- KV compaction
  * For each of n_tensors cache tensors (device array `bases` of base
  * addresses, each [HK][cap][D] bf16 with head stride sh and slot stride sn)

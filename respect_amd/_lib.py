@@ -61,6 +61,7 @@ SIGNATURES: dict[str, tuple] = {
     "rspx_qkv_rope_cache": (_i32, [_c_p, _i64, _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _c_p, _i64, _i64, _c_p, _i64,
                                    _i64, _c_p, _i32, _i32, _i32, _i32, _f32, _c_p]),
     "rspx_trie_mask": (_i32, [_c_p, _i32, _i32, _i32, _i32, _c_p, _i64, _c_p, _c_p]),
+    "rspx_step_inputs": (_i32, [_c_p, _i32, _i32, _i32, _i32, _i32, _c_p, _c_p, _c_p, _c_p, _i64, _c_p]),
     "rspx_kv_compact": (_i32, [_c_p, _i32, _i32, _i32, _i64, _i64, _i32, _i32, _c_p, _i32, _c_p]),
     "rspx_argmax_workspace_bytes": (_i64, [_i32, _i32]),
     "rspx_argmax_rows": (_i32, [_c_p, _i64, _i32, _i32, _i32, _i32, _c_p, _c_p, _i64, _c_p]),

@@ -35,6 +35,42 @@ __global__ __launch_bounds__(256) void trie_mask_kernel(const int* parent, int N
   depth[i] = d;
 }
 
+// The row inputs of one forward from a device-side step descriptor
+// desc = [n, base, tok[0..T), parent[0..T)]: row i < n gets token tok[i]
+// (clamped into [0, vocab)), cache slot P + base + i, rotary position
+// P + base + depth(i) and the mask row of trie_mask_kernel; rows n..T-1 get
+// token 0, slot pad0 + i, position 0 and slot 0 only.  A descriptor that does
+// not fit (n outside [0, T], base < 0, base + n > NN) counts as n = 0.  One
+// workgroup per row.
+__global__ __launch_bounds__(256) void step_inputs_kernel(const int* desc, int T, int P, int NN, int pad0, int vocab,
+                                                          int* ids, int* slots, int* pos, uint8_t* msk, int64_t smm) {
+  const int i = blockIdx.x;
+  int n = desc[0];
+  const int base = desc[1];
+  if (n < 0 || n > T || base < 0 || base > NN - n) n = 0;
+  const int* tok = desc + 2;
+  const int* parent = desc + 2 + T;
+  uint8_t* row = msk + (int64_t)i * smm;
+  for (int j = threadIdx.x; j < NN; j += 256) row[j] = (i < n) ? (j < base ? 1 : 0) : (j == 0 ? 1 : 0);
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  if (i >= n) {
+    ids[i] = 0;
+    slots[i] = pad0 + i;
+    pos[i] = 0;
+    return;
+  }
+  int d = -1;
+  for (int a = i, steps = 0; a >= 0 && a < n && steps <= n; a = parent[a], ++steps) {
+    row[base + a] = 1;
+    ++d;
+  }
+  const int t = tok[i];
+  ids[i] = (t >= 0 && t < vocab) ? t : 0;
+  slots[i] = P + base + i;
+  pos[i] = P + base + d;
+}
+
 // Workgroup (tensor, head): rows src[0..n) of cache tensor `tensor` (one K or
 // V of one layer), head `head`, copied to rows dst0 .. dst0 + n - 1.  All
 // source rows are read into registers before any row is written, so the
@@ -153,6 +189,17 @@ extern "C" int rspx_trie_mask(const int32_t* parent, int N, int base, int M, int
   if (!msk || (N > 0 && (!parent || !depth))) return RSPX_EINVAL;
   hipLaunchKernelGGL(trie_mask_kernel, dim3(M), dim3(256), 0, static_cast<hipStream_t>(stream), parent, N, base, NN,
                      msk, smm, depth);
+  return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
+}
+
+extern "C" int rspx_step_inputs(const int32_t* desc, int T, int P, int NN, int pad0, int vocab, int32_t* ids,
+                                int32_t* slots, int32_t* pos, uint8_t* msk, int64_t smm, void* stream) {
+  if (T < 0 || P < 0 || NN < 1 || pad0 < 0 || vocab < 1 || smm < NN) return RSPX_EINVAL;
+  if ((int64_t)P + NN > INT32_MAX || (int64_t)pad0 + T > INT32_MAX) return RSPX_EINVAL;
+  if (T == 0) return RSPX_OK;
+  if (!desc || !ids || !slots || !pos || !msk) return RSPX_EINVAL;
+  hipLaunchKernelGGL(step_inputs_kernel, dim3(T), dim3(256), 0, static_cast<hipStream_t>(stream), desc, T, P, NN,
+                     pad0, vocab, ids, slots, pos, msk, smm);
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }
 

@@ -282,10 +282,12 @@ class Decoder:
 
 
 class GraphedForward:
-    """Decoder.forward captured once in a HIP graph for fixed (T, P, NN) and
-    replayed with new inputs copied into its static buffers.  Padding rows
-    (fewer real rows than T) write their K/V to the last T slots of the cache,
-    which no call reads, and attend to node slot 0 only."""
+    """Decoder.forward captured once in a HIP graph for fixed (T, P, NN).  The
+    row inputs -- tokens, cache slots, rotary positions, mask -- are made inside
+    the graph by rspx_step_inputs from a step descriptor [n, base, tokens,
+    parents] in device memory, so a call is one host-to-device copy from pinned
+    memory and a replay.  Padding rows write their K/V to the last T slots of
+    the cache, which no call reads, and attend to node slot 0 only."""
 
     def __init__(self, model: Decoder, cache, P: int, T: int, NN: int):
         dev = model.device
@@ -293,34 +295,45 @@ class GraphedForward:
             raise ValueError("KV cache has no room for the graph's scratch slots")
         self.T, self.NN = T, NN
         self.scratch = cache.cap - T
-        self.ids = torch.zeros(T, dtype=torch.int64, device=dev)
-        self.pad_slots = torch.arange(self.scratch, self.scratch + T, dtype=torch.int32, device=dev)
-        self.slots = self.pad_slots.clone()
-        self.pos = torch.zeros(T, dtype=torch.int64, device=dev)
+        i32 = torch.int32
+        self.desc = torch.zeros(2 + 2 * T, dtype=i32, device=dev)
+        self.host = torch.zeros(2 + 2 * T, dtype=i32).pin_memory()
+        self.copied = torch.cuda.Event()
+        self.ids = torch.zeros(T, dtype=i32, device=dev)
+        self.slots = torch.zeros(T, dtype=i32, device=dev)
+        self.pos = torch.zeros(T, dtype=i32, device=dev)
         self.msk = torch.zeros(T, NN, dtype=torch.uint8, device=dev)
-        self.msk[:, 0] = 1
+        L = _lib.lib()
+        vocab = model.cfg.vocab
+
+        def body():
+            _lib.check("rspx_step_inputs", L.rspx_step_inputs(
+                self.desc.data_ptr(), T, P, NN, self.scratch, vocab, self.ids.data_ptr(), self.slots.data_ptr(),
+                self.pos.data_ptr(), self.msk.data_ptr(), self.msk.stride(0), _lib.stream_ptr(dev)))
+            return model.forward(self.ids, self.slots, self.pos, cache, P, self.msk, NN)
+
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):  # sizes the workspaces and the allocator pools
-            model.forward(self.ids, self.slots, self.pos, cache, P, self.msk, NN)
+            body()
         torch.cuda.current_stream(dev).wait_stream(side)
         torch.cuda.synchronize(dev)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            self.logits = model.forward(self.ids, self.slots, self.pos, cache, P, self.msk, NN)
+            self.logits = body()
 
-    def __call__(self, n: int, ids=None, slots=None, pos=None, msk=None) -> torch.Tensor:
-        """Run with the first ``n`` rows given (device tensors; ``msk`` may also be
-        left in place after writing ``self.msk`` directly).  Returns logits [T, V]."""
-        if ids is not None:
-            self.ids[:n].copy_(ids)
-        if slots is not None:
-            self.slots[:n].copy_(slots)
-            if n < self.T:
-                self.slots[n:].copy_(self.pad_slots[n:])
-        if pos is not None:
-            self.pos[:n].copy_(pos)
-        if msk is not None:
-            self.msk.copy_(msk)
+    def run(self, n: int, base: int, tokens, parents) -> torch.Tensor:
+        """Replay for the n-node trie ``tokens`` / ``parents`` (parents precede
+        children, -1 for a root) after ``base`` committed slots; a 1-token
+        forward is a one-node trie.  Returns logits [T, V] (rows n.. padding)."""
+        if not 0 <= n <= self.T or base < 0 or base + n > self.NN:
+            raise ValueError("trie does not fit the captured forward")
+        self.copied.synchronize()  # the previous call's copy is done with the pinned buffer
+        h = self.host.numpy()
+        h[0], h[1] = n, base
+        h[2:2 + n] = tokens
+        h[2 + self.T:2 + self.T + n] = parents
+        self.desc.copy_(self.host, non_blocking=True)
+        self.copied.record()
         self.graph.replay()
         return self.logits

@@ -14,13 +14,11 @@ def forward_token(model, cache, token: int, P: int, c: int, graph: bool = False)
     P + c); it sees the prompt and node slots [0, c].  Returns fp32 logits [1, V].
     ``graph``: replay a captured forward (node segment padded to 64)."""
     dev = model.device
+    if graph:  # a one-node trie after c committed slots: slot P + c, position P + c, slots [0, c] open
+        NN = node_slots(c, 1, 64)
+        return model.graphed(cache, P, 1, NN).run(1, c, [token], [-1])
     slot = torch.tensor([P + c], dtype=torch.int32, device=dev)
     ids = torch.tensor([token], device=dev)
-    if graph:
-        NN = node_slots(c, 1, 64)
-        gf = model.graphed(cache, P, 1, NN)
-        gf.msk[0].copy_(torch.arange(NN, device=dev) <= c)
-        return gf(1, ids, slot, slot.to(torch.int64))
     NN = node_slots(c, 1)
     msk = (torch.arange(NN, device=dev) <= c).to(torch.uint8)[None]
     return model.forward(ids, slot, slot.to(torch.int64), cache, P, msk, NN)

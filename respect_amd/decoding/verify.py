@@ -36,19 +36,19 @@ def trie_mask(tree: Trie, base: int, NN: int, device, rows: int | None = None,
 @torch.no_grad()
 def verify_trie(model, cache, tree: Trie, P: int, base: int, graph: bool = False) -> torch.Tensor:
     """fp32 logits [N, V] of every trie node.  ``graph``: replay a captured
-    forward (rows padded to a multiple of 64, node segment to a multiple of 64);
+    forward (rows padded to a multiple of 64, node segment to a multiple of 64)
+    whose mask, slots and positions are made on the device (rspx_step_inputs);
     the node segment width never changes a row's result."""
     dev = model.device
     N = len(tree.nodes)
-    ids = torch.from_numpy(tree.tokens).to(dev)
-    start = P + base
-    slots = torch.arange(start, start + N, dtype=torch.int32, device=dev)
     if graph:
         T = max(64, -(-N // 64) * 64)
         NN = node_slots(base, N, 64)
         gf = model.graphed(cache, P, T, NN)
-        _, depth = trie_mask(tree, base, NN, dev, rows=T, out=gf.msk)
-        return gf(N, ids, slots, depth.to(torch.int64) + start)[:N]
+        return gf.run(N, base, tree.tokens, tree.parents)[:N]
+    ids = torch.from_numpy(tree.tokens).to(dev)
+    start = P + base
+    slots = torch.arange(start, start + N, dtype=torch.int32, device=dev)
     NN = node_slots(base, N)
     if P + NN > cache.cap:
         raise ValueError("KV cache too small for the trie")

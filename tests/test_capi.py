@@ -60,3 +60,13 @@ def test_attn_argument_errors(lib):
     assert _attn(lib, NN=4104) == -1              # node segment beyond NMAX = 4096
     assert lib.rspx_trie_attn_workspace_bytes(32, 8, 64, 3072, 128) > 65536
     assert lib.rspx_trie_attn_workspace_bytes(32, 8, 64, 3072, 96) < 0
+
+
+def test_step_inputs_argument_checks(lib):
+    p = 1 << 20           # stand-in pointer: every call below returns before using it
+    assert lib.rspx_step_inputs(p, -1, 0, 32, 0, 10, p, p, p, p, 32, None) == -1     # T < 0
+    assert lib.rspx_step_inputs(p, 4, 0, 0, 0, 10, p, p, p, p, 32, None) == -1       # NN < 1
+    assert lib.rspx_step_inputs(p, 4, 0, 32, 0, 10, p, p, p, p, 16, None) == -1      # mask row stride < NN
+    assert lib.rspx_step_inputs(p, 4, 0, 32, 0, 0, p, p, p, p, 32, None) == -1       # empty vocabulary
+    assert lib.rspx_step_inputs(None, 4, 0, 32, 0, 10, p, p, p, p, 32, None) == -1   # no descriptor
+    assert lib.rspx_step_inputs(p, 0, 0, 32, 0, 10, p, p, p, p, 32, None) == 0       # nothing to do

@@ -143,6 +143,47 @@ def test_trie_mask_from_parents():
         assert depth.cpu().tolist() == tree.depths.tolist()
 
 
+def test_step_inputs_from_device_descriptor():
+    """rspx_step_inputs: node rows get their token, slot P + base + i, position
+    P + base + depth and rspx_trie_mask's mask row; padding rows token 0, slot
+    pad0 + i, position 0, slot 0 only; a descriptor that does not fit counts as
+    an empty trie; out-of-range tokens become 0."""
+    from respect_amd import _lib
+    from respect_amd.candidates.trie import build_trie, node_mask
+    L = _lib.lib()
+    tree = build_trie([(1, 2, 3, 4), (1, 2, 5), (6, 7), (1, 8, 9, 10, 11)])
+    n, T, P, pad0, vocab = len(tree.nodes), 16, 1000, 5000, 100
+    s = _lib.stream_ptr(torch.device("cuda"))
+    for base, NN in ((0, 32), (5, 32), (37, 64), (60, 64)):
+        desc = np.zeros(2 + 2 * T, np.int32)
+        desc[0], desc[1] = n, base
+        desc[2:2 + n] = tree.tokens
+        desc[2 + T:2 + T + n] = tree.parents
+        desc[2 + 3] = 999            # out of the vocabulary: token 0
+        d = torch.from_numpy(desc).cuda()
+        ids, slots, pos = (torch.full((T,), -7, dtype=torch.int32, device="cuda") for _ in range(3))
+        msk = torch.full((T, NN), 9, dtype=torch.uint8, device="cuda")
+        _lib.check("rspx_step_inputs", L.rspx_step_inputs(d.data_ptr(), T, P, NN, pad0, vocab, ids.data_ptr(),
+                                                          slots.data_ptr(), pos.data_ptr(), msk.data_ptr(), NN, s))
+        torch.cuda.synchronize()
+        fits = base + n <= NN
+        print(f"[step_inputs] base {base} NN {NN} fits {fits}", flush=True)
+        m = msk.cpu().numpy().astype(bool)
+        if fits:
+            exp_tok = tree.tokens.astype(np.int64).copy()
+            exp_tok[3] = 0
+            assert ids.cpu().tolist() == exp_tok.tolist() + [0] * (T - n)
+            assert slots.cpu().tolist() == [P + base + i for i in range(n)] + [pad0 + i for i in range(n, T)]
+            assert pos.cpu().tolist() == [P + base + int(x) for x in tree.depths] + [0] * (T - n)
+            assert np.array_equal(m[:n], node_mask(tree, base, NN))
+            pad_rows = m[n:]
+        else:
+            assert ids.cpu().tolist() == [0] * T and pos.cpu().tolist() == [0] * T
+            assert slots.cpu().tolist() == [pad0 + i for i in range(T)]
+            pad_rows = m
+        assert pad_rows[:, 0].all() and not pad_rows[:, 1:].any()
+
+
 def test_kv_compact_overlapping_moves():
     from respect_amd.decoding.kv_buffer import KVCache
     c = KVCache(3, 2, 128, 64)
