@@ -371,7 +371,7 @@ def bench_decoder(args) -> dict:
     from respect_amd.decoding.engine import Decoder, DecoderConfig
     from respect_amd.decoding.kv_buffer import KVCache
     from respect_amd.decoding.respect import respect_step
-    from respect_amd.decoding.sequential import forward_token
+    from respect_amd.decoding.sequential import next_token
 
     cfg = DecoderConfig()
     P, steps = 3072, args.decoder_steps
@@ -406,7 +406,7 @@ def bench_decoder(args) -> dict:
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for c in range(n_ar):
-        G.append(int(greedy_token(forward_token(model, ar, G[-1], P, c, graph=True)).item()))
+        G.append(next_token(model, ar, G[-1], P, c))
     torch.cuda.synchronize()
     ar_ms = (time.perf_counter() - t0) / n_ar * 1e3
     _log(f"decoder: {n_ar} tokens decoded one by one, {ar_ms:.2f} ms per token")

@@ -40,6 +40,7 @@ import torch
 from .. import _lib
 from ..kernels.attention import trie_attn
 from ..system.fused import rope_tables
+from .acceptance import greedy_token
 
 
 @dataclass(frozen=True)
@@ -303,14 +304,21 @@ class GraphedForward:
         self.slots = torch.zeros(T, dtype=i32, device=dev)
         self.pos = torch.zeros(T, dtype=i32, device=dev)
         self.msk = torch.zeros(T, NN, dtype=torch.uint8, device=dev)
+        # the greedy choice of every row (no excluded vocabulary range), also captured
+        self.picks = torch.zeros(T, dtype=torch.int64, device=dev)
+        self.picks_host = torch.zeros(T, dtype=torch.int64).pin_memory()
+        self.picked = torch.cuda.Event()
         L = _lib.lib()
         vocab = model.cfg.vocab
+        argws = torch.zeros(max(16, L.rspx_argmax_workspace_bytes(T, vocab)), dtype=torch.uint8, device=dev)
 
         def body():
             _lib.check("rspx_step_inputs", L.rspx_step_inputs(
                 self.desc.data_ptr(), T, P, NN, self.scratch, vocab, self.ids.data_ptr(), self.slots.data_ptr(),
                 self.pos.data_ptr(), self.msk.data_ptr(), self.msk.stride(0), _lib.stream_ptr(dev)))
-            return model.forward(self.ids, self.slots, self.pos, cache, P, self.msk, NN)
+            logits = model.forward(self.ids, self.slots, self.pos, cache, P, self.msk, NN)
+            greedy_token(logits, out=self.picks, workspace=argws)
+            return logits
 
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
@@ -337,3 +345,11 @@ class GraphedForward:
         self.copied.record()
         self.graph.replay()
         return self.logits
+
+    def greedy(self, n: int) -> list[int]:
+        """The greedy tokens of rows [0, n) of the last replay (rspx_argmax_rows
+        over the whole vocabulary, taken inside the graph), on the host."""
+        self.picks_host[:n].copy_(self.picks[:n], non_blocking=True)
+        self.picked.record()
+        self.picked.synchronize()
+        return self.picks_host[:n].tolist()

@@ -25,6 +25,15 @@ def forward_token(model, cache, token: int, P: int, c: int, graph: bool = False)
 
 
 @torch.no_grad()
+def next_token(model, cache, token: int, P: int, c: int) -> int:
+    """forward_token(graph=True) followed by the greedy choice (whole
+    vocabulary), the argmax taken inside the captured forward."""
+    gf = model.graphed(cache, P, 1, node_slots(c, 1, 64))
+    gf.run(1, c, [token], [-1])
+    return gf.greedy(1)[0]
+
+
+@torch.no_grad()
 def sequential(model, cache, token: int, P: int, base: int, eos: int, offset: int, size: int,
                max_tokens: int) -> list[int]:
     """Generate from ``token`` (already chosen) until EOS or ``max_tokens``, one

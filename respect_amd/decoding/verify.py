@@ -54,3 +54,15 @@ def verify_trie(model, cache, tree: Trie, P: int, base: int, graph: bool = False
         raise ValueError("KV cache too small for the trie")
     msk, depth = trie_mask(tree, base, NN, dev)
     return model.forward(ids, slots, depth.to(torch.int64) + start, cache, P, msk, NN)
+
+
+@torch.no_grad()
+def verify_trie_greedy(model, cache, tree: Trie, P: int, base: int) -> list[int]:
+    """The greedy token (whole vocabulary) of every trie node from one replayed
+    forward whose argmax is taken inside the graph; only the N choices come
+    back to the host."""
+    N = len(tree.nodes)
+    T = max(64, -(-N // 64) * 64)
+    gf = model.graphed(cache, P, T, node_slots(base, N, 64))
+    gf.run(N, base, tree.tokens, tree.parents)
+    return gf.greedy(N)

@@ -201,10 +201,11 @@ def test_kv_compact_overlapping_moves():
 def test_graph_replays_equal_eager(model):
     """Captured forwards (HIP graphs) give the eager bits on every replay, with
     eager work and synchronisations between replays, for tries of different
-    sizes and offsets and for 1-token calls."""
+    sizes and offsets and for 1-token calls; the greedy choices taken inside
+    the graphs equal greedy_token on the eager logits."""
     from respect_amd.decoding.acceptance import greedy_token
-    from respect_amd.decoding.sequential import forward_token
-    from respect_amd.decoding.verify import verify_trie
+    from respect_amd.decoding.sequential import forward_token, next_token
+    from respect_amd.decoding.verify import verify_trie, verify_trie_greedy
     cache, last = _filled_cache(model)
     t0 = int(greedy_token(last).item())
     rng = np.random.default_rng(1)
@@ -217,6 +218,8 @@ def test_graph_replays_equal_eager(model):
         torch.cuda.synchronize()
         print(f"[graph] rep {rep} base {base} nodes {len(tree.nodes)}", flush=True)
         assert torch.equal(eager, graphed)
+        assert verify_trie_greedy(model, cache, tree, P, base) == greedy_token(eager).tolist()
         e1 = forward_token(model, cache, seq[1], P, base).clone()
         g1 = forward_token(model, cache, seq[1], P, base, graph=True).clone()
         assert torch.equal(e1, g1)
+        assert next_token(model, cache, seq[1], P, base) == int(greedy_token(e1).item())
