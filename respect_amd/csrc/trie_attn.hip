@@ -52,6 +52,8 @@
 //   8 kv heads, workgroup g of kernel A lands on XCD g (round-robin dispatch),
 //   so the row blocks that share a head's K/V meet in one XCD's L2.
 
+#include <type_traits>
+
 #include "common.h"
 #include "respect_amd.h"
 
@@ -602,21 +604,24 @@ constexpr int kChunk = 64;  // node slots staged in LDS at a time
 // written), else an area of their own.
 constexpr int kMaxNodeRows = 64;  // a workgroup's node rows: at most one prompt row block
 constexpr int kResident = 2;  // node chunks a prefetching caller keeps in LDS at once
-template <int D> struct NodeLds {
+// RES resident chunks for at most ROWS node rows (RES 3 fits beside 16 rows).
+template <int D, int RES = kResident, int ROWS = kMaxNodeRows> struct NodeLds {
+  static constexpr int DIM = D, kRes = RES, kRows = ROWS;
   static constexpr int KBYTES = kChunk * 2 * D;   // one chunk's K
   static constexpr int VBYTES = kChunk * 2 * D;   // one chunk's V
-  static constexpr int VOFF = kResident * KBYTES;
-  static constexpr int SOFF = VOFF + kResident * VBYTES;
+  static constexpr int VOFF = RES * KBYTES;
+  static constexpr int SOFF = VOFF + RES * VBYTES;
   static constexpr int SROW = kChunk + 4;  // floats per score row
-  static constexpr int NPOFF = SOFF + kMaxNodeRows * SROW * 4;
+  static constexpr int NPOFF = SOFF + ROWS * SROW * 4;
   static constexpr int NPROW = D + 4;      // node partial of a row: m, l, pad, pad, acc[D]
-  static constexpr int NPEND = NPOFF + kMaxNodeRows * NPROW * 4;
-  static constexpr int SROW2 = kResident * kChunk + 4;  // floats per row of a whole segment's scores
+  static constexpr int NPEND = NPOFF + ROWS * NPROW * 4;
+  static constexpr int SROW2 = RES * kChunk + 4;  // floats per row of a whole segment's scores
   static constexpr int S2OFF = NPROW == SROW2 ? NPOFF : NPEND;
-  static constexpr int BYTES = NPROW == SROW2 ? NPEND : NPEND + kMaxNodeRows * SROW2 * 4;
+  static constexpr int BYTES = NPROW == SROW2 ? NPEND : NPEND + ROWS * SROW2 * 4;
   static __device__ __forceinline__ lds_char* kbuf(lds_char* kv, int b) { return kv + b * KBYTES; }
   static __device__ __forceinline__ lds_char* vbuf(lds_char* kv, int b) { return kv + VOFF + b * VBYTES; }
 };
+template <int D> using NodeLds3 = NodeLds<D, 3, 16>;  // three resident chunks, at most 16 rows
 constexpr int kMaxRounds = kMaxNodeRows / kWavesA;  // node rows per wave
 
 // Where a row's result goes: row r of kv head g is query r / GQA of head
@@ -639,14 +644,13 @@ typedef __attribute__((address_space(3))) float lds_float;
 // Loads a caller may issue ahead of node_rows for a node segment of at most
 // kResident chunks: every chunk's K/V in LDS, the score fragment of the wave's
 // first task and the mask bytes of the wave's rows.
-template <int D> struct NodePre {
+template <int D, int RES = kResident> struct NodePre {
+  static_assert(RES == 2 || RES == 3, "two or three resident chunks");
   bf16x8 qf[D / 32];
-  uint64_t mb[kResident];   // chunk c, byte i: the mask byte of round i
-  // mb[b] for a run-time b, kept in registers (selects, no indexed access).
-  __device__ __forceinline__ uint64_t mask(int b) const {
-    static_assert(kResident == 2, "one select");
-    return b == 0 ? mb[0] : mb[1];
-  }
+  // Mask words of chunks 0, 1, 2 (byte i: the mask byte of round i), named
+  // scalars read with constant indices only: a run-time choice between them
+  // can fold into one indexed load, which puts the whole struct in scratch.
+  uint64_t mb0 = 0, mb1 = 0, mb2 = 0;
 };
 static_assert(kMaxRounds <= 8, "mask bytes of every round in one 64-bit word");
 
@@ -655,11 +659,11 @@ __device__ __forceinline__ uint64_t node_masks(const TrieAttnArgs& A, int p0, in
 
 // Chunk c0 of kv head g's node K (score fragments) and, if `withv`, V rows
 // into LDS buffer b: 1 KB pieces x = w, w + nw, ...  Slots past NN read zeros.
-template <int D>
+template <int D, class LY = NodeLds<D>>
 __device__ __forceinline__ void node_issue(const TrieAttnArgs& A, int g, int c0, lds_char* kv, int b, int w,
                                            int nw, bool withv) {
   constexpr int DQ = D / 32, RB = 2 * D;
-  constexpr int KX = NodeLds<D>::KBYTES / 1024, VX = NodeLds<D>::VBYTES / 1024;
+  constexpr int KX = LY::KBYTES / 1024, VX = LY::VBYTES / 1024;
   const int lane = __lane_id();
   const int left = A.NN - c0 - 1;
   const __amdgpu_buffer_rsrc_t rk =
@@ -670,10 +674,10 @@ __device__ __forceinline__ void node_issue(const TrieAttnArgs& A, int g, int c0,
   for (int x = w; x < nx; x += nw) {
     if (x < KX) {
       const int slot = 16 * (x / DQ) + (lane & 15);
-      bdma16(rk, 2 * (slot * A.sknn + 32 * (x % DQ) + 8 * (lane >> 4)), NodeLds<D>::kbuf(kv, b) + x * 1024);
+      bdma16(rk, 2 * (slot * A.sknn + 32 * (x % DQ) + 8 * (lane >> 4)), LY::kbuf(kv, b) + x * 1024);
     } else {
       const int byte = (x - KX) * 1024 + 16 * lane;
-      bdma16(rv, 2 * (byte / RB) * A.svnn + byte % RB, NodeLds<D>::vbuf(kv, b) + (x - KX) * 1024);
+      bdma16(rv, 2 * (byte / RB) * A.svnn + byte % RB, LY::vbuf(kv, b) + (x - KX) * 1024);
     }
   }
 }
@@ -816,46 +820,65 @@ __device__ __forceinline__ void node_accumulate(uint64_t mm, float p, const lds_
 // (vmcnt 0) and passed a workgroup barrier; otherwise chunks stream through
 // buffer 0.  Does nothing when NN = 0.  Ends with every
 // vector load of the calling wave complete.
-template <int D>
+template <int D, class LY = NodeLds<D>>
 __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv, int w,
-                                          const NodePre<D>& pre, bool have_pre) {
+                                          const NodePre<D, LY::kRes>& pre, bool have_pre) {
   constexpr int nw = kWavesA;
   constexpr int DL = D / 64;
   const int lane = __lane_id();
   const int NN = A.NN;
   if (NN == 0) return;
   const int nrd = (rend - p0 - w + nw - 1) / nw;     // rounds of this wave
-  lds_float* S = (lds_float*)(kv + NodeLds<D>::SOFF);
-  lds_float* NP = (lds_float*)(kv + NodeLds<D>::NPOFF);
+  constexpr int RES = LY::kRes;
+  lds_float* S = (lds_float*)(kv + LY::SOFF);
+  lds_float* NP = (lds_float*)(kv + LY::NPOFF);
   const bool one = NN <= kChunk;
-  const bool res = have_pre && NN <= kResident * kChunk;  // every chunk already in buffer c
+  const bool res = have_pre && NN <= RES * kChunk;  // every chunk already in buffer c
 
   if (res && !one) {
-    // Two resident chunks: every score at once, then per row the maximum over
-    // all its allowed slots and the sums over chunk 0's slots, then chunk 1's.
-    static_assert(kResident == 2, "two resident chunks");
-    lds_float* S2 = (lds_float*)(kv + NodeLds<D>::S2OFF);
-    constexpr int SR2 = NodeLds<D>::SROW2;
-    node_scores<D, SR2>(A, g, p0, rend, 0, NodeLds<D>::kbuf(kv, 0), S2, w, nw, pre.qf, true);
-    node_scores<D, SR2>(A, g, p0, rend, kChunk, NodeLds<D>::kbuf(kv, 1), S2 + kChunk, w, nw, pre.qf, true);
+    // Two or more resident chunks: every score at once, then per row the
+    // maximum over all its allowed slots and the sums over chunk 0's slots,
+    // then chunk 1's, ...
+    lds_float* S2 = (lds_float*)(kv + LY::S2OFF);
+    constexpr int SR2 = LY::SROW2;
+    static_assert(RES == 2 || RES == 3, "two or three resident chunks");
+    const int nch = (NN + kChunk - 1) / kChunk;
+    node_scores<D, SR2>(A, g, p0, rend, 0, LY::kbuf(kv, 0), S2, w, nw, pre.qf, true);
+    node_scores<D, SR2>(A, g, p0, rend, kChunk, LY::kbuf(kv, 1), S2 + kChunk, w, nw, pre.qf, true);
+    if (RES > 2 && nch > 2)
+      node_scores<D, SR2>(A, g, p0, rend, 2 * kChunk, LY::kbuf(kv, 2), S2 + 2 * kChunk, w, nw, pre.qf, true);
     lds_barrier();
-    const uint64_t mb0 = pre.mb[0], mb1 = pre.mb[1];
 #pragma unroll 1
     for (int i = 0; i < nrd; ++i) {
       const int row = w + nw * i;
       const lds_float* sr = S2 + row * SR2;
-      const float s0 = sr[lane], s1 = sr[kChunk + lane];
-      const bool ok0 = ((mb0 >> (8 * i)) & 0xff) != 0, ok1 = ((mb1 >> (8 * i)) & 0xff) != 0;
-      const float m = max64(fmaxf(ok0 ? s0 : kNegInf, ok1 ? s1 : kNegInf));
-      const float pa = ok0 ? fexp2(s0 - m) : 0.f, pb = ok1 ? fexp2(s1 - m) : 0.f;
-      const uint64_t m0 = __builtin_amdgcn_ballot_w64(ok0), m1 = __builtin_amdgcn_ballot_w64(ok1);
+      const uint64_t mws[3] = {pre.mb0, pre.mb1, pre.mb2};
+      float sc[RES];
+      bool ok[RES];
+      float x = kNegInf;
+#pragma unroll
+      for (int c = 0; c < RES; ++c) {
+        ok[c] = c < nch && ((mws[c] >> (8 * i)) & 0xff) != 0;
+        sc[c] = c < nch ? sr[c * kChunk + lane] : 0.f;
+        x = fmaxf(x, ok[c] ? sc[c] : kNegInf);
+      }
+      const float m = max64(x);
       float l = 0.f, acc[DL];
 #pragma unroll
       for (int k = 0; k < DL; ++k) acc[k] = 0.f;
-      node_accumulate<D>(m0, pa, NodeLds<D>::vbuf(kv, 0) + DL * 2 * lane, l, acc);
-      node_accumulate<D>(m1, pb, NodeLds<D>::vbuf(kv, 1) + DL * 2 * lane, l, acc);
+      // One call per chunk with constant indices (a loop around the inner
+      // while loop stays rolled and would index sc / ok at run time).
+      auto chunk = [&](int c, bool okc, float scc) {
+        if (c < nch) {
+          const float pc = okc ? fexp2(scc - m) : 0.f;
+          node_accumulate<D>(__builtin_amdgcn_ballot_w64(okc), pc, LY::vbuf(kv, c) + DL * 2 * lane, l, acc);
+        }
+      };
+      chunk(0, ok[0], sc[0]);
+      chunk(1, ok[1], sc[1]);
+      if constexpr (RES > 2) chunk(2, ok[2], sc[2]);
       // The row's scores are in registers; its partial may now overwrite them.
-      lds_float* np = NP + row * NodeLds<D>::NPROW;
+      lds_float* np = NP + row * LY::NPROW;
       if (lane == 0) {
         np[0] = m;
         np[1] = l;
@@ -869,25 +892,23 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
   if (!one) {
     for (int c0 = 0; c0 < NN; c0 += kChunk) {
       if (c0 > 0) lds_barrier();  // every wave is done with the previous chunk's scores
-      const int b = res ? c0 / kChunk : 0;
+      const int b = 0;            // more than one chunk: never resident here
       uint64_t mb;
-      if (res) {
-        mb = pre.mask(b);
-      } else {
-        node_issue<D>(A, g, c0, kv, 0, w, nw, false);
+      {
+        node_issue<D, LY>(A, g, c0, kv, 0, w, nw, false);
         mb = node_masks(A, p0, nrd, w, c0);
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         lds_barrier();
       }
-      node_scores<D>(A, g, p0, rend, c0, NodeLds<D>::kbuf(kv, b), S, w, nw, pre.qf, res);
+      node_scores<D>(A, g, p0, rend, c0, LY::kbuf(kv, b), S, w, nw, pre.qf, res);
       lds_barrier();
 #pragma unroll 1
       for (int i = 0; i < kMaxRounds; ++i) {
         if (i < nrd) {
           const int row = w + nw * i;
           const bool ok = ((mb >> (8 * i)) & 0xff) != 0;
-          const float x = max64(ok ? S[row * NodeLds<D>::SROW + lane] : kNegInf);
-          lds_float* np = NP + row * NodeLds<D>::NPROW;
+          const float x = max64(ok ? S[row * LY::SROW + lane] : kNegInf);
+          lds_float* np = NP + row * LY::NPROW;
           if (lane == 0) np[0] = c0 == 0 ? x : fmaxf(np[0], x);
         }
       }
@@ -897,28 +918,28 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
 
   for (int c0 = 0; c0 < NN; c0 += kChunk) {
     if (c0 > 0) lds_barrier();  // every wave is done with the previous chunk
-    const int b = res ? c0 / kChunk : 0;
+    const int b = 0;              // a resident segment here is one chunk, in buffer 0
     uint64_t mb;
     if (res) {
       // The caller waited for its loads (vmcnt 0) before a workgroup barrier.
       // No wait here: a store or atomic it issued since may still be in flight.
-      mb = pre.mask(b);
+      mb = pre.mb0;
     } else {
-      node_issue<D>(A, g, c0, kv, 0, w, nw, true);
+      node_issue<D, LY>(A, g, c0, kv, 0, w, nw, true);
       mb = node_masks(A, p0, nrd, w, c0);
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of the chunk is in LDS
       lds_barrier();                       // and every other wave's part
     }
-    node_scores<D>(A, g, p0, rend, c0, NodeLds<D>::kbuf(kv, b), S, w, nw, pre.qf, res);
+    node_scores<D>(A, g, p0, rend, c0, LY::kbuf(kv, b), S, w, nw, pre.qf, res);
     lds_barrier();
-    const lds_char* vl = NodeLds<D>::vbuf(kv, b) + DL * 2 * lane;
+    const lds_char* vl = LY::vbuf(kv, b) + DL * 2 * lane;
 
 #pragma unroll 1
     for (int i = 0; i < nrd; ++i) {
       const int row = w + nw * i;
       const bool ok = ((mb >> (8 * i)) & 0xff) != 0;
-      const float s = S[row * NodeLds<D>::SROW + lane];
-      lds_float* np = NP + row * NodeLds<D>::NPROW;
+      const float s = S[row * LY::SROW + lane];
+      lds_float* np = NP + row * LY::NPROW;
       const float m = one ? max64(ok ? s : kNegInf) : np[0];
       const float p = ok ? fexp2(s - m) : 0.f;
       const uint64_t mm = __builtin_amdgcn_ballot_w64(ok);  // wave-uniform: the row's allowed slots
@@ -941,21 +962,23 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
   }
 }
 
-// Issues node_rows' loads for a segment of at most kResident chunks
-// (0 < NN <= kResident kChunk, p0 < rend): chunk c into buffer c.
-template <int D>
+// Issues node_rows' loads for a segment of at most LY::kRes chunks
+// (0 < NN <= LY::kRes kChunk, p0 < rend): chunk c into buffer c.
+template <int D, class LY = NodeLds<D>>
 __device__ __forceinline__ void node_prefetch(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv, int w,
-                                              NodePre<D>& pre) {
+                                              NodePre<D, LY::kRes>& pre) {
   constexpr int nw = kWavesA;
   const int nrd = (rend - p0 - w + nw - 1) / nw;
-#pragma unroll
-  for (int b = 0; b < kResident; ++b) {
-    pre.mb[b] = 0;
-    if (b * kChunk < A.NN) {
-      node_issue<D>(A, g, b * kChunk, kv, b, w, nw, true);
-      pre.mb[b] = node_masks(A, p0, nrd, w, b * kChunk);
-    }
-  }
+  // One call per chunk with a constant index into pre.mb (a rolled loop
+  // would index it at run time and put `pre` in scratch memory).
+  auto chunk = [&](int b) -> uint64_t {
+    if (b * kChunk >= A.NN) return 0;
+    node_issue<D, LY>(A, g, b * kChunk, kv, b, w, nw, true);
+    return node_masks(A, p0, nrd, w, b * kChunk);
+  };
+  pre.mb0 = chunk(0);
+  pre.mb1 = chunk(1);
+  if constexpr (LY::kRes > 2) pre.mb2 = chunk(2);
   if (w < 4 * ((rend - p0 + 15) / 16)) node_q<D>(A, g, p0, rend, w >> 2, pre.qf);
 }
 
@@ -1013,13 +1036,13 @@ __device__ __forceinline__ void merge_row(const TrieAttnArgs& A, int g, int r, f
 
 // The node partial of wave w's round i, left in LDS by node_rows (empty when
 // there are no node slots), merged into row p0 + w + 8 i.
-template <int D, bool COH>
+template <int D, bool COH, class LY = NodeLds<D>>
 __device__ __forceinline__ void merge_rounds(const TrieAttnArgs& A, int g, int p0, int rend, const lds_char* kv,
                                              int w) {
   constexpr int DL = D / 64;
   const int lane = __lane_id();
   const int nrd = (rend - p0 - w + kWavesA - 1) / kWavesA;
-  const lds_float* NP = (const lds_float*)(kv + NodeLds<D>::NPOFF);
+  const lds_float* NP = (const lds_float*)(kv + LY::NPOFF);
 #pragma unroll 1
   for (int i = 0; i < nrd; ++i) {
     const int row = w + kWavesA * i;
@@ -1027,7 +1050,7 @@ __device__ __forceinline__ void merge_rounds(const TrieAttnArgs& A, int g, int p
 #pragma unroll
     for (int k = 0; k < DL; ++k) acc[k] = 0.f;
     if (A.NN > 0) {
-      const lds_float* np = NP + row * NodeLds<D>::NPROW;
+      const lds_float* np = NP + row * LY::NPROW;
       m = np[0];
       l = np[1];
 #pragma unroll
@@ -1039,26 +1062,27 @@ __device__ __forceinline__ void merge_rounds(const TrieAttnArgs& A, int g, int p
 
 // ------------------------------------------------------------------ kernel B
 // Workgroup (g, c8): rows [8 c8, 8 c8 + 8) of kv head g, row 8 c8 + w on
-// wave w: node partial, then merge.  A node segment of at most kResident
-// chunks is loaded whole up front (then taken in one pass); a longer one
-// streams.
+// wave w: node partial, then merge.  A node segment of at most three chunks
+// is loaded whole up front (then taken in one pass); a longer one streams.
 template <int D>
 __global__ __launch_bounds__(64 * kWavesA) void node_merge_kernel(TrieAttnArgs A) {
-  __shared__ __attribute__((aligned(16))) char kv[NodeLds<D>::BYTES];
+  using LY = NodeLds3<D>;
+  static_assert(8 <= LY::kRows, "a workgroup's rows fit the node areas");
+  __shared__ __attribute__((aligned(16))) char kv[LY::BYTES];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int RC8 = (A.R + 7) / 8;
   const int g = blockIdx.x / RC8;
   const int p0 = 8 * (blockIdx.x - g * RC8);
   const int rend = min(p0 + 8, A.R);
-  NodePre<D> pre;
-  const bool pf = A.NN > 0 && A.NN <= kResident * kChunk;
+  NodePre<D, LY::kRes> pre;
+  const bool pf = A.NN > 0 && A.NN <= LY::kRes * kChunk;
   if (pf) {
-    node_prefetch<D>(A, g, p0, rend, (lds_char*)kv, w, pre);
+    node_prefetch<D, LY>(A, g, p0, rend, (lds_char*)kv, w, pre);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of the segment is in LDS
     lds_barrier();                       // and every other wave's part
   }
-  node_rows<D>(A, g, p0, rend, (lds_char*)kv, w, pre, pf);
-  merge_rounds<D, false>(A, g, p0, rend, (const lds_char*)kv, w);
+  node_rows<D, LY>(A, g, p0, rend, (lds_char*)kv, w, pre, pf);
+  merge_rounds<D, false, LY>(A, g, p0, rend, (const lds_char*)kv, w);
 }
 
 // ------------------------------------------------------------------ fused kernel
@@ -1084,11 +1108,14 @@ __global__ __launch_bounds__(64 * kWavesA) void node_merge_kernel(TrieAttnArgs A
 constexpr int kSpinLimit = 1 << 22;
 constexpr int kSyncWords = 4096;   // timeout flag + [HK][NRB][2] counters
 
-template <int D, int kRT>
+// RES3: the node areas of NodeLds3 (three resident chunks), for grids whose
+// workgroups merge at most 16 rows each (fused_rows <= 16).
+template <int D, int kRT, bool RES3>
 __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
-  constexpr int LB = PromptLds<D, kRT>::BYTES > NodeLds<D>::BYTES ? PromptLds<D, kRT>::BYTES : NodeLds<D>::BYTES;
-  static_assert(NodeLds<D>::BYTES <= PromptLds<D, kRT>::RINGBYTES, "node LDS inside the ring");
-  static_assert(32 * kRT <= kMaxNodeRows, "a row block fits the node areas");
+  using LY = typename std::conditional<RES3, NodeLds3<D>, NodeLds<D>>::type;
+  constexpr int LB = PromptLds<D, kRT>::BYTES > LY::BYTES ? PromptLds<D, kRT>::BYTES : LY::BYTES;
+  static_assert(LY::BYTES <= PromptLds<D, kRT>::RINGBYTES, "node LDS inside the ring");
+  static_assert(RES3 || 32 * kRT <= LY::kRows, "a row block fits the node areas");
   __shared__ __attribute__((aligned(16))) char lds[LB];
   const int lane = __lane_id();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1104,10 +1131,10 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
 
   // A node segment of at most kResident chunks (K/V, score fragment, mask
   // bytes) is loaded while the group partial is being stored.
-  const bool pf = A.NN > 0 && A.NN <= kResident * kChunk && r0 < rend;
-  NodePre<D> pre;
+  const bool pf = A.NN > 0 && A.NN <= LY::kRes * kChunk && r0 < rend;
+  NodePre<D, LY::kRes> pre;
   prompt_block<D, kRT, true>(A, lds, g, rb, q, [&] {
-    if (pf) node_prefetch<D>(A, g, r0, rend, (lds_char*)lds, w, pre);
+    if (pf) node_prefetch<D, LY>(A, g, r0, rend, (lds_char*)lds, w, pre);
   });
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
@@ -1115,7 +1142,7 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   if (threadIdx.x == 0) __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   if (r0 < rend) {
-    node_rows<D>(A, g, r0, rend, (lds_char*)lds, w, pre, pf);
+    node_rows<D, LY>(A, g, r0, rend, (lds_char*)lds, w, pre, pf);
     if (w == 0) {
       int v = 0;
       for (int it = 0; it < kSpinLimit; ++it) {
@@ -1127,7 +1154,7 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     }
     lds_barrier();
-    merge_rounds<D, true>(A, g, r0, rend, (const lds_char*)lds, w);
+    merge_rounds<D, true, LY>(A, g, r0, rend, (const lds_char*)lds, w);
   }
   // Counters back to zero once every workgroup of the block is past its wait.
   lds_barrier();
@@ -1195,7 +1222,8 @@ static int make_plan(int H, int HK, int M, int P, int NN, int D, int rows_per_wa
   return RSPX_OK;
 }
 
-// Workgroups of fused_kernel<D, RT> the device holds at once (0 if unknown).
+// Workgroups of fused_kernel<D, RT, *> the device holds at once, the smaller
+// of the two node layouts' figures (0 if unknown).
 template <int D, int RT>
 static int fused_capacity() {
   static int cap[64];
@@ -1203,16 +1231,20 @@ static int fused_capacity() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   if (!done[dev]) {
-    int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fused_kernel<D, RT>, 64 * kWavesA, 0) != hipSuccess ||
+    int a = 0, b = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, fused_kernel<D, RT, false>, 64 * kWavesA, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, fused_kernel<D, RT, true>, 64 * kWavesA, 0) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-      per_cu = cus = 0;
+      a = b = cus = 0;
     }
-    cap[dev] = per_cu * cus;
+    cap[dev] = (a < b ? a : b) * cus;
     done[dev] = true;
   }
   return cap[dev];
 }
+
+// Rows one workgroup of fused_kernel<D, RT> merges (a multiple of 4).
+static int fused_rows(int RT, int NG) { return 4 * ((32 * RT / 4 + NG - 1) / NG); }
 
 template <int D, int RT>
 static void launch_rt(const TrieAttnArgs& a, const Plan& pl, hipStream_t s, int mode) {
@@ -1220,7 +1252,10 @@ static void launch_rt(const TrieAttnArgs& a, const Plan& pl, hipStream_t s, int 
                      (size_t)a.HK * pl.R * pl.NG * D * sizeof(float) < (size_t(1) << 31) &&
                      pl.prompt_wgs <= fused_capacity<D, RT>();
   if (fused) {
-    hipLaunchKernelGGL((fused_kernel<D, RT>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);
+    if (fused_rows(RT, pl.NG) <= NodeLds3<D>::kRows)
+      hipLaunchKernelGGL((fused_kernel<D, RT, true>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);
+    else
+      hipLaunchKernelGGL((fused_kernel<D, RT, false>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);
     return;
   }
   if (pl.prompt_wgs > 0) hipLaunchKernelGGL((prompt_kernel<D, RT>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);

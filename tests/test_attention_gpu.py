@@ -264,10 +264,11 @@ def test_one_and_two_launches_equal(which):
 
 @pytest.mark.parametrize("shape", ["8b", "d64"])
 def test_one_and_two_pass_node_segments_equal(shape):
-    """The same trie and committed slots in a node segment of 128 slots (loaded whole and
-    taken in one pass: all scores, the row maximum, then the sums chunk by chunk) and of
-    192 / 256 slots (the extra slots masked out; streamed in two passes: a maximum pass, then
-    the sums) give the same bits, through one and two launches."""
+    """The same trie and committed slots in a node segment of 128 and 192 slots (loaded
+    whole and taken in one pass: all scores, the row maximum, then the sums chunk by chunk;
+    two and three resident chunks) and of 256 slots (the extra slots masked out; streamed in
+    two passes: a maximum pass, then the sums) give the same bits, through one and two
+    launches."""
     args = {"8b": (11, 32, 8, 128, 3072, 4, 24, 0, 16, 64), "d64": (7, 16, 2, 64, 3086, 3, 9, 0, 6, None)}[shape]
     kw = {"kv_scale": 128 ** -0.5} if shape == "8b" else {}
     base = 40 if shape == "8b" else 90
