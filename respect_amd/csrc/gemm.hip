@@ -67,6 +67,7 @@ struct Args {
   int out_tiled;                  // silu: out in the tiled layout of [M, N / 2] (so unused)
 };
 
+constexpr int kXResRounds = 4;   // X-resident blocks: K chunks of at most 4 rounds (128 KB of LDS)
 constexpr int kOOB = 0x7ffffff0;  // a buffer offset past any descriptor: loads return 0, touch nothing
 constexpr int kOOBRow = 0x40000000;  // the same for a whole lane chunk (k-block steps added stay below 2^31)
 
@@ -147,11 +148,17 @@ __device__ __forceinline__ void vm_wait_n(int n) {
 // NR > 0: the NR rounds are unrolled at compile time, so every wait count is
 // exact and the compiler's own waits for the W registers never drain the
 // prefetch; NR == 0: a run-time loop (any round count, shallower prefetch).
-template <int MT, int NR, int W>
+//
+// XRES (NR <= kXResRounds): the block's whole X chunk is copied into LDS up
+// front (NR x 32 KB), so the main loop streams W with no X loads and no
+// barriers.  The LDS image and the MFMA chain are those of the two-buffer
+// form: the same bits.
+template <int MT, int NR, int W, bool XRES = false>
 __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
+  static_assert(!XRES || (NR > 0 && NR <= kXResRounds), "X-resident blocks hold at most kXResRounds rounds");
   constexpr int kCols = 16 * W;
   constexpr int XPW = 32 / W;                 // X chunks per wave per round
-  __shared__ __attribute__((aligned(16))) char xs[2][kRoundKB * 4 * 1024];  // 2 x 32 KB
+  __shared__ __attribute__((aligned(16))) char xs[XRES ? NR : 2][kRoundKB * 4 * 1024];  // 32 KB each
   constexpr int XB = kRoundKB * 4 * 1024;
   const int lane = __lane_id();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -193,7 +200,22 @@ __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
 #pragma unroll
   for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  if constexpr (NR > 0) {
+  if constexpr (XRES) {
+    u32x4 wbuf[4][kRoundKB];
+#pragma unroll
+    for (int rr = 0; rr < NR; ++rr) issue_x<W>(rx, xoff, xkb, rr, nr, xl + rr * XB, w);
+    issue_w(rw, woff, 0, nr, wbuf[0]);
+    if constexpr (NR > 1) issue_w(rw, woff, 1, nr, wbuf[1]);
+    if constexpr (NR > 2) issue_w(rw, woff, 2, nr, wbuf[2]);
+    vm_wait_n(8 * (1 + (1 < NR) + (2 < NR)));  // every X chunk (issued before the W rounds) landed
+    raw_barrier();
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      if (r + 3 < NR) issue_w(rw, woff, r + 3, nr, wbuf[(r + 3) & 3]);
+      vm_wait_n(8 * ((r + 1 < NR) + (r + 2 < NR) + (r + 3 < NR)));  // W(r) landed
+      round_compute<MT>(xl + r * XB, wbuf[r & 3], acc, lane);
+    }
+  } else if constexpr (NR > 0) {
     // Only loads whose data is used are issued (the compiler would drop the
     // others and the counts below would be off).  Exact wait per round: the
     // loads issued after the later of X(r) and W(r).
@@ -332,6 +354,10 @@ static int linear_launch(const void* x, int64_t sx, const void* w, int64_t sw, v
   const int64_t grid = (int64_t)NT * S * MTILES;
   if (grid > 0x7fffffff) return RSPX_EUNSUPPORTED;
   const int mt = (MTILES > 1 || M >= 64) ? 4 : (M + 15) / 16;  // row tiles per 64-row tile
+  // X-resident blocks pay where X is large against each block's W slice and
+  // the grid is one wave of 8-wave blocks (q/k/v [64 x 4096] . [6144 x 4096]^T:
+  // 17.5 -> 16.7 us); for 4-wave blocks and for one row they cost a little.
+  const bool xres = waves == 8 && M >= 32;
   const int nr = a.KC / gemm::kRoundK;
   const dim3 g((unsigned)grid), b(64 * waves);
 #define RSPX_GEMM_NR(MTV, WV)                                                                     \
@@ -339,7 +365,10 @@ static int linear_launch(const void* x, int64_t sx, const void* w, int64_t sw, v
     case 1: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 1, WV>), g, b, 0, s, a); break;           \
     case 2: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 2, WV>), g, b, 0, s, a); break;           \
     case 3: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 3, WV>), g, b, 0, s, a); break;           \
-    case 4: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 4, WV>), g, b, 0, s, a); break;           \
+    case 4:                                                                                      \
+      if (xres) hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 4, WV, true>), g, b, 0, s, a);        \
+      else hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 4, WV>), g, b, 0, s, a);                   \
+      break;                                                                                     \
     case 6: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 6, WV>), g, b, 0, s, a); break;           \
     case 8: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 8, WV>), g, b, 0, s, a); break;           \
     case 12: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 12, WV>), g, b, 0, s, a); break;         \
