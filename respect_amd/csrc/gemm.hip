@@ -11,8 +11,8 @@
 //   ((c0 + c1) + c2) + ..., then rounded once to the output type.
 // So a row's output bits do not depend on how many rows the call carries.
 //
-// Work split: workgroup = (16 W output columns, chunk s, 64-row tile), W = 4
-// or 8 waves of 16 columns each (the host picks W per shape for speed; the
+// Work split: workgroup = (16 W output columns, chunk s, 64-row tile), W = 4,
+// 6 or 8 waves of 16 columns each (the host picks W per shape for speed; the
 // chunk count S comes from 64-column tiles whatever W is, so W never changes
 // a bit of the result).  W -- the large operand, read exactly once -- goes
 // straight from HBM into the MFMA A operand registers (lane (n16, g4) loads
@@ -95,23 +95,32 @@ __device__ __forceinline__ void round_compute(const lds_char_t* xb, const u32x4 
   }
 }
 
-// X chunks of round rr into LDS buffer xb: the 32 chunks (k-block kb, row
-// tile t) of a round are spread over the W waves, wave w taking row tile
-// t = w % 4 and k-blocks w / 4 + (W / 4) j (rows 16 t + n16, k [8 g4, +8) of
-// the block).  W loads of round rr into registers.  Rounds past the chunk and
-// rows past M use out-of-range offsets: zeros, no memory traffic.  Every wave
-// issues exactly 32 / W X chunks and 8 W loads per round on every path, so
-// the waits below are exact counts.
+// X chunks of round rr into LDS buffer xb: the 32 chunks c = 4 kb + t
+// (k-block kb, row tile t: rows 16 t + n16, k [8 g4, +8) of the block) of a
+// round are spread over the W waves, wave w taking c = w, w + W, ...; xo[t]
+// is this lane's offset of row tile t.  W loads of round rr into registers.
+// Rounds past the chunk and rows past M use out-of-range offsets: zeros, no
+// memory traffic.  Wave w issues the same ceil((32 - w) / W) X chunks and 8
+// W loads per round on every path, so the waits below are exact counts.
 // xkb: bytes between consecutive k-blocks of one lane's chunk (64 row-major,
 // 4096 tiled).
 template <int W>
-__device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t rx, int xoff, int xkb, int rr, int nr, lds_char_t* xb,
-                                        int w) {
+__device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t rx, const int (&xo)[4], int xkb, int rr, int nr,
+                                        lds_char_t* xb, int w) {
   const bool live = rr < nr;
+  if constexpr (32 % W == 0) {
+    // Every chunk of wave w is row tile w % 4, whose offset the caller put in xo[0].
 #pragma unroll
-  for (int j = 0; j < 32 / W; ++j) {
-    const int kb = (w >> 2) + (W / 4) * j;
-    x_dma16(rx, live ? xoff + xkb * (rr * kRoundKB + kb) : kOOB, xb + (kb * 4 + (w & 3)) * 1024);
+    for (int j = 0; j < 32 / W; ++j) {
+      const int kb = (w >> 2) + (W / 4) * j;
+      x_dma16(rx, live ? xo[0] + xkb * (rr * kRoundKB + kb) : kOOB, xb + (kb * 4 + (w & 3)) * 1024);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < (32 + W - 1) / W; ++j) {
+      const int c = w + W * j;                  // chunk: k-block c / 4, row tile c % 4
+      if (c < 32) x_dma16(rx, live ? xo[c & 3] + xkb * (rr * kRoundKB + (c >> 2)) : kOOB, xb + c * 1024);
+    }
   }
   asm volatile("" ::: "memory");
 }
@@ -124,20 +133,75 @@ __device__ __forceinline__ void issue_w(__amdgpu_buffer_rsrc_t rw, int woff, int
   asm volatile("" ::: "memory");
 }
 
-// s_waitcnt vmcnt(n) for the counts the pipeline uses (multiples of 4, <= 32;
-// n is a compile-time constant wherever it is called, so one case remains).
+// s_waitcnt vmcnt(n), 0 <= n <= 63 (a compile-time constant for 4 and 8
+// waves, where one case remains; a per-wave value for 6 waves).
 #define RSPX_VMW(v) __builtin_amdgcn_s_waitcnt(((v) & 15) | (((v) >> 4) << 14) | 0x70 | 0xF00)
 __device__ __forceinline__ void vm_wait_n(int n) {
   switch (n) {
     case 0: RSPX_VMW(0); break;
+    case 1: RSPX_VMW(1); break;
+    case 2: RSPX_VMW(2); break;
+    case 3: RSPX_VMW(3); break;
     case 4: RSPX_VMW(4); break;
+    case 5: RSPX_VMW(5); break;
+    case 6: RSPX_VMW(6); break;
+    case 7: RSPX_VMW(7); break;
     case 8: RSPX_VMW(8); break;
+    case 9: RSPX_VMW(9); break;
+    case 10: RSPX_VMW(10); break;
+    case 11: RSPX_VMW(11); break;
     case 12: RSPX_VMW(12); break;
+    case 13: RSPX_VMW(13); break;
+    case 14: RSPX_VMW(14); break;
+    case 15: RSPX_VMW(15); break;
     case 16: RSPX_VMW(16); break;
+    case 17: RSPX_VMW(17); break;
+    case 18: RSPX_VMW(18); break;
+    case 19: RSPX_VMW(19); break;
     case 20: RSPX_VMW(20); break;
+    case 21: RSPX_VMW(21); break;
+    case 22: RSPX_VMW(22); break;
+    case 23: RSPX_VMW(23); break;
     case 24: RSPX_VMW(24); break;
+    case 25: RSPX_VMW(25); break;
+    case 26: RSPX_VMW(26); break;
+    case 27: RSPX_VMW(27); break;
     case 28: RSPX_VMW(28); break;
-    default: RSPX_VMW(32); break;
+    case 29: RSPX_VMW(29); break;
+    case 30: RSPX_VMW(30); break;
+    case 31: RSPX_VMW(31); break;
+    case 32: RSPX_VMW(32); break;
+    case 33: RSPX_VMW(33); break;
+    case 34: RSPX_VMW(34); break;
+    case 35: RSPX_VMW(35); break;
+    case 36: RSPX_VMW(36); break;
+    case 37: RSPX_VMW(37); break;
+    case 38: RSPX_VMW(38); break;
+    case 39: RSPX_VMW(39); break;
+    case 40: RSPX_VMW(40); break;
+    case 41: RSPX_VMW(41); break;
+    case 42: RSPX_VMW(42); break;
+    case 43: RSPX_VMW(43); break;
+    case 44: RSPX_VMW(44); break;
+    case 45: RSPX_VMW(45); break;
+    case 46: RSPX_VMW(46); break;
+    case 47: RSPX_VMW(47); break;
+    case 48: RSPX_VMW(48); break;
+    case 49: RSPX_VMW(49); break;
+    case 50: RSPX_VMW(50); break;
+    case 51: RSPX_VMW(51); break;
+    case 52: RSPX_VMW(52); break;
+    case 53: RSPX_VMW(53); break;
+    case 54: RSPX_VMW(54); break;
+    case 55: RSPX_VMW(55); break;
+    case 56: RSPX_VMW(56); break;
+    case 57: RSPX_VMW(57); break;
+    case 58: RSPX_VMW(58); break;
+    case 59: RSPX_VMW(59); break;
+    case 60: RSPX_VMW(60); break;
+    case 61: RSPX_VMW(61); break;
+    case 62: RSPX_VMW(62); break;
+    default: RSPX_VMW(63); break;
   }
 }
 #undef RSPX_VMW
@@ -157,11 +221,14 @@ template <int MT, int NR, int W, bool XRES = false>
 __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
   static_assert(!XRES || (NR > 0 && NR <= kXResRounds), "X-resident blocks hold at most kXResRounds rounds");
   constexpr int kCols = 16 * W;
-  constexpr int XPW = 32 / W;                 // X chunks per wave per round
   __shared__ __attribute__((aligned(16))) char xs[XRES ? NR : 2][kRoundKB * 4 * 1024];  // 32 KB each
   constexpr int XB = kRoundKB * 4 * 1024;
   const int lane = __lane_id();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // X chunks this wave issues per round: a constant when W divides 32, so every
+  // wait count below is one too (a run-time count leaves the compiler's own
+  // waits for the W registers conservative).
+  const int XPW = 32 % W == 0 ? 32 / W : (32 - w + W - 1) / W;
   const int n16 = lane & 15, g4 = lane >> 4;
   const int NT = (A.N + kCols - 1) / kCols;
   const int nt = blockIdx.x % NT;
@@ -180,16 +247,27 @@ __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
   // a wave whose tile lies past M loads nothing (rows past M inside a tile are
   // read but only reach output rows that are never stored).
   const int mrows = min(kRows, A.M - row0);
+  // xoff[t]: this lane's offset of row tile t; when W divides 32 a wave only
+  // loads its own tile w % 4, kept in xoff[0].
   __amdgpu_buffer_rsrc_t rx;
-  int xoff, xkb;
+  int xoff[4], xkb;
+  auto tile_off = [&](int t) {
+    return A.x_tiled ? (16 * t < mrows ? 1024 * t + 16 * lane : kOOBRow)
+                     : 2 * ((16 * t + n16) * (int)A.sx + 8 * g4);
+  };
   if (A.x_tiled) {
     rx = rsrc(A.x + (int64_t)mt * kRows * A.K + (int64_t)(k0 / 32) * 2048, (int64_t)(A.K - k0) * 128);
-    xoff = 16 * (w & 3) < mrows ? 1024 * (w & 3) + 16 * lane : kOOBRow;
     xkb = 4096;
   } else {
     rx = rsrc(A.x + (int64_t)row0 * A.sx + k0, 2 * ((int64_t)(mrows - 1) * A.sx + (A.K - k0)));
-    xoff = 2 * ((16 * (w & 3) + n16) * (int)A.sx + 8 * g4);
     xkb = 64;
+  }
+  if constexpr (32 % W == 0) {
+    xoff[0] = tile_off(w & 3);
+    xoff[1] = xoff[2] = xoff[3] = 0;
+  } else {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) xoff[t] = tile_off(t);
   }
   const __amdgpu_buffer_rsrc_t rw =
       rsrc(A.w + (int64_t)(has_cols ? col : 0) * A.sw + k0, has_cols ? 2 * (15 * A.sw + A.KC) : 0);
@@ -349,7 +427,12 @@ static int linear_launch(const void* x, int64_t sx, const void* w, int64_t sw, v
   // it while the grid keeps >= 192 workgroups, and for the widest layers
   // (the vocabulary head) only when the X block is large (many rows).
   const int wg8 = (N + 127) / 128 * S;
-  const int waves = (wg8 >= 192 && (M >= 32 || wg8 < 1024)) ? 8 : 4;
+  // One K chunk whose 8-wave grid leaves CUs idle: 6 waves (96 columns) fill
+  // them (gate/up [64 x 4096] . [24576 x 4096]^T: 192 -> 256 workgroups,
+  // 47.7 -> 42.2 us; one row 38.9 -> 34.8 us).
+  const int wg6 = (N + 95) / 96 * S;
+  const int waves = (S == 1 && N % 96 == 0 && wg8 < 256 && wg6 >= 256 && wg6 <= 512) ? 6
+                    : (wg8 >= 192 && (M >= 32 || wg8 < 1024)) ? 8 : 4;
   const int NT = (N + 16 * waves - 1) / (16 * waves);
   const int64_t grid = (int64_t)NT * S * MTILES;
   if (grid > 0x7fffffff) return RSPX_EUNSUPPORTED;
@@ -380,7 +463,8 @@ static int linear_launch(const void* x, int64_t sx, const void* w, int64_t sw, v
   else if (mt == 3) { RSPX_GEMM_NR(3, WV) } \
   else if (mt == 2) { RSPX_GEMM_NR(2, WV) } \
   else { RSPX_GEMM_NR(1, WV) }
-  if (waves == 8) { RSPX_GEMM_MT(8) }
+  if (waves == 6) { RSPX_GEMM_MT(6) }
+  else if (waves == 8) { RSPX_GEMM_MT(8) }
   else { RSPX_GEMM_MT(4) }
 #undef RSPX_GEMM_MT
 #undef RSPX_GEMM_NR
