@@ -427,20 +427,22 @@ static int linear_launch(const void* x, int64_t sx, const void* w, int64_t sw, v
   // it while the grid keeps >= 192 workgroups, and for the widest layers
   // (the vocabulary head) only when the X block is large (many rows).
   const int wg8 = (N + 127) / 128 * S;
-  // One K chunk whose 8-wave grid leaves CUs idle: 6 waves (96 columns) fill
-  // them (gate/up [64 x 4096] . [24576 x 4096]^T: 192 -> 256 workgroups,
-  // 47.7 -> 42.2 us; one row 38.9 -> 34.8 us).
+  // An 8-wave grid that leaves CUs idle: 6 waves (96 columns) fill them
+  // (gate/up [64 x 4096] . [24576 x 4096]^T: 192 -> 256 workgroups, 47.7 ->
+  // 42.2 us, one row 38.9 -> 34.8 us; q/k/v [6144 x 4096], 4 K chunks: 15.4 ->
+  // 14.8 us with X resident).  The vocabulary head gained nothing from it.
   const int wg6 = (N + 95) / 96 * S;
-  const int waves = (S == 1 && N % 96 == 0 && wg8 < 256 && wg6 >= 256 && wg6 <= 512) ? 6
+  const int waves = (N % 96 == 0 && wg8 < 256 && wg6 >= 256 && wg6 <= 512) ? 6
                     : (wg8 >= 192 && (M >= 32 || wg8 < 1024)) ? 8 : 4;
   const int NT = (N + 16 * waves - 1) / (16 * waves);
   const int64_t grid = (int64_t)NT * S * MTILES;
   if (grid > 0x7fffffff) return RSPX_EUNSUPPORTED;
   const int mt = (MTILES > 1 || M >= 64) ? 4 : (M + 15) / 16;  // row tiles per 64-row tile
   // X-resident blocks pay where X is large against each block's W slice and
-  // the grid is one wave of 8-wave blocks (q/k/v [64 x 4096] . [6144 x 4096]^T:
-  // 17.5 -> 16.7 us); for 4-wave blocks and for one row they cost a little.
-  const bool xres = waves == 8 && M >= 32;
+  // the grid is one wave of 6- or 8-wave blocks (q/k/v [64 x 4096] .
+  // [6144 x 4096]^T: 17.5 -> 16.7 us at 8 waves); for 4-wave blocks and for
+  // one row they cost a little.
+  const bool xres = waves >= 6 && M >= 32;
   const int nr = a.KC / gemm::kRoundK;
   const dim3 g((unsigned)grid), b(64 * waves);
 #define RSPX_GEMM_NR(MTV, WV)                                                                     \
