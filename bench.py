@@ -398,7 +398,7 @@ def bench_decoder(args) -> dict:
         model.graphed(ar, P, 1, NN)
         model.graphed(sp, P, 64, NN)
     torch.cuda.synchronize()
-    _log(f"decoder: {len(model._graphs)} forwards captured in {time.perf_counter() - t0:.1f} s")
+    _log(f"decoder: {sum(len(v) for v in model._graphs.values())} forwards captured in {time.perf_counter() - t0:.1f} s")
     # Token-by-token greedy reference: the tokens the tries are built from.
     first = int(greedy_token(last).item())
     n_ar = 24 * (steps + 1) + 1

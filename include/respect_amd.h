@@ -131,11 +131,20 @@ int rspx_trie_attn_launches(const void* q, int64_t sqh, int64_t sqm, const void*
                             float sm_scale, void* workspace, int64_t workspace_bytes, int rows_per_wave, int launches,
                             void* stream);
 
-/* 1 if a one-launch call on this workspace ever ran out of its bounded wait
- * (its results are then not valid), 0 if not, < 0 on error.  Synchronises the
- * stream.
+/* 1 if a one-launch call on this workspace ever ran out of its bounded wait,
+ * 0 if not, < 0 on error.  Synchronises the stream.  A workgroup whose wait
+ * runs out stores NaN in every element of the output rows it merges, so such
+ * a call's output carries the failure without this query.
  */
 int rspx_trie_attn_status(const void* workspace, int H, int HK, int M, int P, int D, void* stream);
+
+/* Test hook, no counterpart in the reference: sets how many times a one-launch
+ * workgroup polls its row block's counter before its wait gives up (a
+ * negative value restores the default, 2^22 polls); returns the previous
+ * value.  Lets a test drive the give-up path while every kernel still exits
+ * normally.  Process-wide, not thread-safe; read at each launch.
+ */
+int rspx_trie_attn_set_spin_limit(int polls);
 
 /* ---------------------------------------------------------------- RMSNorm
  * y[r] = bf16(w * bf16(x[r] * rsqrt(mean(x[r]^2) + eps))), fp32 statistics
@@ -242,19 +251,23 @@ int rspx_add_rmsnorm_partials(const void* r, int64_t sr, const float* hp, int S,
  * per token, stride scs) with the arithmetic of rspx_qk_norm_rope; q goes to
  * qo [T, HQ, D] (contiguous); k and v are written into the KV cache of the
  * layer: cache_k[h * skh + slots[t] * skn + d] (likewise v).  D == 128.
+ * cap: slots per head of the cache.  A token whose slot lies outside
+ * [0, cap) writes no K/V and gets a NaN q row (the reference's index_copy_
+ * would raise a device-side assert; here the error reaches every output the
+ * token feeds, without a host synchronisation).
  */
 int rspx_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* wq, const void* wk, const void* cos,
-                        const void* sin, int64_t scs, const int32_t* slots, void* cache_k, int64_t skh, int64_t skn,
-                        void* cache_v, int64_t svh, int64_t svn, void* qo, int T, int HQ, int HK, int D, float eps,
-                        void* stream);
+                        const void* sin, int64_t scs, const int32_t* slots, int cap, void* cache_k, int64_t skh,
+                        int64_t skn, void* cache_v, int64_t svh, int64_t svn, void* qo, int T, int HQ, int HK, int D,
+                        float eps, void* stream);
 
 /* The same with the projection given as fp32 chunk partials
  * qkvp[S][T][(HQ + 2 HK) D] (rspx_linear_partials; 1 <= S <= 8).
  */
 int rspx_qkv_rope_cache_partials(const float* qkvp, int S, const void* wq, const void* wk, const void* cos,
-                                 const void* sin, int64_t scs, const int32_t* slots, void* cache_k, int64_t skh,
-                                 int64_t skn, void* cache_v, int64_t svh, int64_t svn, void* qo, int T, int HQ, int HK,
-                                 int D, float eps, void* stream);
+                                 const void* sin, int64_t scs, const int32_t* slots, int cap, void* cache_k,
+                                 int64_t skh, int64_t skn, void* cache_v, int64_t svh, int64_t svn, void* qo, int T,
+                                 int HQ, int HK, int D, float eps, void* stream);
 
 /* ---------------------------------------------------------------- trie mask from a parent array
  * parent: [N] int32 (parent index, -1 for a root; parents precede children).

@@ -10,6 +10,12 @@ attn_blocked  restates the development kernel _fused_attn
               (respect/kernels/reference_blocked.py:14-80): node slots reduced
               tile by tile like the prompt -- the layout-dependent negative control.
 attn_exact    float64 masked softmax attention (the mathematical definition).
+attn_tree     the fixed reduction tree the HIP kernel computes (same semantics as
+              attn_hyb, a different but equally fixed order): 32-key steps with a
+              lazy base-2 reference maximum, four key quarters per group combined
+              at the group maximum, exact-maximum node sums in slot order, groups
+              merged left to right, then the node partial.  The per-element
+              parity target of the GPU kernel.
 
 Inputs are float32 arrays holding bf16 values: q [H, M, D], kp/vp [HK, P, D],
 kn/vn [HK, NN, D], msk [M, NN] bool.  Head h uses kv head h // (H // HK).
@@ -20,6 +26,11 @@ scale fails it); single allowed key => out == v exactly; equal scores =>
 out == bf16(mean v); masked node slots are exact no-ops (layout invariance of
 attn_hyb); attn_blocked *does* change with the layout (the control detects
 layout dependence); brute-force per-row fp64 recomputation on tiny inputs.
+attn_tree and attn_blocked: the same error bound against attn_exact and the
+same planted-slip checks (a dropped node segment, a wrong scale, a missing
+rescale, unscaled quarters), single key => v, equal scores => mean(v).
+
+Test infrastructure only: the product never imports this package.
 """
 from __future__ import annotations
 
@@ -184,3 +195,180 @@ def attn_error_bound(q, kp, vp, kn, vn, msk, sm_scale=None) -> np.ndarray:
     exact = attn_exact(q, kp, vp, kn, vn, msk, sm_scale)
     from .bf16 import ulp
     return 2.0 ** -9 * wv_prompt + 2.0 ** -20 * wv_all + ulp(exact)
+
+
+# ---------------------------------------------------------------- the kernel's own tree
+
+LOG2E = 1.4426950408889634
+KSTEP = 32        # keys per online-softmax step
+QUARTERS = 4      # key quarters (waves) per group
+GROUPS_MAX = 8    # key groups per kv head
+LAZY_TAU = 8.0    # log2 headroom before a quarter's reference maximum moves
+
+
+def prompt_plan(P: int) -> tuple[int, int, int]:
+    """(steps, steps per group S, groups NG): S and NG depend on P only."""
+    steps = -(-P // KSTEP)
+    if steps == 0:
+        return 0, QUARTERS, 0
+    nr = -(-steps // (QUARTERS * GROUPS_MAX))
+    S = QUARTERS * nr
+    return steps, S, -(-steps // S)
+
+
+def _f32(x) -> np.ndarray:
+    return np.asarray(x, dtype=np.float64).astype(np.float32)
+
+
+def _exp2(x) -> np.ndarray:
+    with np.errstate(over="ignore", under="ignore"):
+        return np.exp2(np.asarray(x, dtype=np.float32))
+
+
+def _chain_scores(q: np.ndarray, k: np.ndarray) -> np.ndarray:
+    """Raw fp32 scores q.k [.., M, N]: head_dim in 32-wide chunks, each chunk's dot product
+    exact (bf16 products are exact) and added to the fp32 running sum with one rounding --
+    the chain of 16x16x32 MFMAs the kernel uses for scores."""
+    D = q.shape[-1]
+    acc = np.zeros(q.shape[:-1] + (k.shape[-2],), np.float64)
+    for i in range(0, D, 32):
+        part = np.matmul(q[..., i:i + 32].astype(np.float64), np.swapaxes(k[..., i:i + 32], -1, -2).astype(np.float64))
+        acc = _f32(acc + part).astype(np.float64)
+    return acc.astype(np.float32)
+
+
+def _lane_sum32(p: np.ndarray) -> np.ndarray:
+    """Sum over the last axis (32 keys of a step) in the kernel's order: lane g (0..3) folds
+    keys 4g..4g+3 then 16+4g..16+4g+3 left to right, then (g0 + g1) + (g2 + g3)."""
+    lanes = []
+    for g in range(4):
+        idx = [4 * g + e for e in range(4)] + [16 + 4 * g + e for e in range(4)]
+        r = p[..., idx[0]]
+        for i in idx[1:]:
+            r = _f32(r + p[..., i])
+        lanes.append(r)
+    return _f32(_f32(lanes[0] + lanes[1]) + _f32(lanes[2] + lanes[3]))
+
+
+def _combine(m, l, acc, m2, l2, acc2):
+    """(m, l, acc) <- (m, l, acc) (+) (m2, l2, acc2); an incoming m2 = -inf is left out."""
+    skip = m2 == -np.inf
+    with np.errstate(invalid="ignore"):
+        mn = np.maximum(m, m2)
+        a = _exp2(_f32(m - mn))
+        b = _exp2(_f32(m2 - mn))
+        ln = _f32(l2.astype(np.float64) * b + _f32(l * a))
+        accn = _f32(acc2.astype(np.float64) * b[..., None] + _f32(acc * a[..., None]))
+    return (np.where(skip, m, mn), np.where(skip, l, ln), np.where(skip[..., None], acc, accn))
+
+
+def attn_tree(q, kp, vp, kn, vn, msk, sm_scale=None, _plant: str | None = None) -> np.ndarray:
+    """The HIP kernel's reduction tree (float32 arrays of bf16 values in, bf16 values out).
+
+    Per (head, row), with c = fp32(scale * log2 e) and s the raw fp32 score:
+
+    step     keys [32 t, 32 t + 32) of the prompt; mx = fp32(max(s) * c).
+    quarter  steps 4 i + k of a group (k = 0..3), in order; the reference maximum
+             moves to mx only when mx > mref + 8 (l and acc then scale by
+             2^(mref - mx)); p = 2^fma(s, c, -mref), its bf16 rounding enters PV;
+             l += the step's p summed in the kernel's lane order.
+    group    S = 4 ceil(ceil(P/32) / 32) consecutive steps; quarters scaled by
+             2^(m_k - M) (M their maximum, 0 for an empty quarter) and summed as
+             (q0 + q1) + (q2 + q3).
+    node     s c over the row's allowed slots; m their exact maximum; p = 2^(s c - m)
+             in fp32; l and acc summed slot by slot in slot order (acc by fma).
+    final    groups left to right, then the node partial; out = bf16(acc / l).
+
+    ``_plant`` plants a mistake for the oracle's own tests: "no_rescale" (a moved
+    reference maximum does not rescale l and acc), "flat_quarters" (quarters summed
+    without their 2^(m_k - M) factors).
+    """
+    q = np.asarray(q, np.float32)
+    H, M, D = q.shape
+    HK, P, _ = kp.shape
+    NN = kn.shape[1]
+    scale = np.float32(D ** -0.5 if sm_scale is None else sm_scale)
+    c = np.float32(float(scale) * LOG2E)
+    KP, VP = _kv_for_heads(np.asarray(kp, np.float32), H), _kv_for_heads(np.asarray(vp, np.float32), H)
+    KN, VN = _kv_for_heads(np.asarray(kn, np.float32), H), _kv_for_heads(np.asarray(vn, np.float32), H)
+    msk = np.asarray(msk, dtype=bool)
+    ninf = np.float32(-np.inf)
+
+    fm = np.full((H, M), ninf, np.float32)
+    fl = np.zeros((H, M), np.float32)
+    facc = np.zeros((H, M, D), np.float32)
+
+    steps, S, NG = prompt_plan(P)
+    if steps:
+        raw = _chain_scores(q, KP)                                  # [H, M, P]
+        pad = steps * KSTEP - P
+        if pad:
+            raw = np.concatenate([raw, np.full((H, M, pad), ninf, np.float32)], axis=2)
+            VPp = np.concatenate([VP, np.zeros((H, pad, D), np.float32)], axis=1)
+        else:
+            VPp = VP
+        nr = S // QUARTERS
+        for gi in range(NG):
+            s0 = gi * S
+            ns = min(S, steps - s0)
+            quarters = []
+            for k in range(QUARTERS):
+                mref = np.full((H, M), ninf, np.float32)
+                l = np.zeros((H, M), np.float32)
+                acc = np.zeros((H, M, D), np.float32)
+                for i in range(nr):
+                    sl = QUARTERS * i + k
+                    if sl >= ns:
+                        break
+                    ks = (s0 + sl) * KSTEP
+                    s = raw[..., ks:ks + KSTEP]
+                    mx = _f32(s.max(axis=2).astype(np.float64) * c)
+                    move = mx > _f32(mref.astype(np.float64) + LAZY_TAU)
+                    mn = np.where(move, mx, mref)
+                    with np.errstate(invalid="ignore"):
+                        alpha = _exp2(_f32(mref.astype(np.float64) - mn))
+                    if _plant != "no_rescale":
+                        l = _f32(l * alpha)
+                        acc = _f32(acc * alpha[..., None])
+                    mref = mn
+                    with np.errstate(invalid="ignore"):
+                        p = _exp2(_f32(s.astype(np.float64) * c - mref[..., None]))
+                    p = np.where(s == ninf, np.float32(0), p)
+                    l = _f32(l + _lane_sum32(p))
+                    pv = np.matmul(round_bf16(p).astype(np.float64), VPp[:, ks:ks + KSTEP].astype(np.float64))
+                    acc = _f32(acc.astype(np.float64) + pv)
+                quarters.append((mref, l, acc))
+            mk = np.stack([t[0] for t in quarters])
+            Mg = mk.max(axis=0)
+            with np.errstate(invalid="ignore"):
+                sk = np.where(mk == ninf, np.float32(0), _exp2(_f32(mk.astype(np.float64) - Mg)))
+            if _plant == "flat_quarters":
+                sk = np.where(mk == ninf, np.float32(0), np.float32(1))
+            lk = [_f32(quarters[j][1] * sk[j]) for j in range(4)]
+            ak = [_f32(quarters[j][2] * sk[j][..., None]) for j in range(4)]
+            Lg = _f32(_f32(lk[0] + lk[1]) + _f32(lk[2] + lk[3]))
+            Ag = _f32(_f32(ak[0] + ak[1]) + _f32(ak[2] + ak[3]))
+            fm, fl, facc = _combine(fm, fl, facc, Mg, Lg, Ag)
+
+    if NN:
+        sn = _f32(_chain_scores(q, KN).astype(np.float64) * c)      # [H, M, NN]
+        allow = np.broadcast_to(msk[None], sn.shape)
+        sm = np.where(allow, sn, ninf)
+        m = sm.max(axis=2)
+        with np.errstate(invalid="ignore"):
+            p = np.where(allow, _exp2(_f32(sm.astype(np.float64) - m[..., None])), np.float32(0))
+        l = np.zeros((H, M), np.float32)
+        acc = np.zeros((H, M, D), np.float32)
+        for j in range(NN):
+            on = allow[..., j]
+            if not on.any():
+                continue
+            pj = p[..., j]
+            l = np.where(on, _f32(l + pj), l)
+            accj = _f32(pj[..., None].astype(np.float64) * VN[:, None, j, :] + acc)
+            acc = np.where(on[..., None], accj, acc)
+        fm, fl, facc = _combine(fm, fl, facc, m, l, acc)
+
+    with np.errstate(invalid="ignore", divide="ignore"):
+        out = _f32(facc.astype(np.float64) / fl[..., None])
+    return round_bf16(out)

@@ -45,6 +45,7 @@ SIGNATURES: dict[str, tuple] = {
         _c_p, _i64, _i64, _c_p, _i64, _i64,
         _i32, _i32, _i32, _i32, _i32, _i32, _f32, _c_p, _i64, _i32, _i32, _c_p]),
     "rspx_trie_attn_status": (_i32, [_c_p, _i32, _i32, _i32, _i32, _i32, _c_p]),
+    "rspx_trie_attn_set_spin_limit": (_i32, [_i32]),
     "rspx_square": (_i32, [_c_p, _i64, _c_p, _i64, _i32, _i32, _c_p]),
     "rspx_add_sq": (_i32, [_c_p, _i64, _c_p, _i64, _c_p, _i64, _c_p, _i64, _i32, _i32, _c_p]),
     "rspx_norm_apply": (_i32, [_c_p, _i64, _c_p, _c_p, _c_p, _i64, _i32, _i32, _f32, _c_p]),
@@ -58,7 +59,7 @@ SIGNATURES: dict[str, tuple] = {
     "rspx_linear_workspace_bytes": (_i64, [_i32, _i32, _i32]),
     "rspx_linear": (_i32, [_c_p, _i64, _c_p, _i64, _c_p, _i64, _i32, _i32, _i32, _i32, _c_p, _i64, _c_p]),
     "rspx_add_rmsnorm": (_i32, [_c_p, _i64, _c_p, _i64, _c_p, _c_p, _i64, _c_p, _i64, _i32, _i32, _f32, _c_p]),
-    "rspx_qkv_rope_cache": (_i32, [_c_p, _i64, _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _c_p, _i64, _i64, _c_p, _i64,
+    "rspx_qkv_rope_cache": (_i32, [_c_p, _i64, _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i32, _c_p, _i64, _i64, _c_p, _i64,
                                    _i64, _c_p, _i32, _i32, _i32, _i32, _f32, _c_p]),
     "rspx_trie_mask": (_i32, [_c_p, _i32, _i32, _i32, _i32, _c_p, _i64, _c_p, _c_p]),
     "rspx_step_inputs": (_i32, [_c_p, _i32, _i32, _i32, _i32, _i32, _c_p, _c_p, _c_p, _c_p, _i64, _c_p]),
@@ -69,7 +70,7 @@ SIGNATURES: dict[str, tuple] = {
     "rspx_linear_silu": (_i32, [_c_p, _i64, _c_p, _i64, _c_p, _i64, _i32, _i32, _i32, _c_p]),
     "rspx_add_rmsnorm_partials": (_i32, [_c_p, _i64, _c_p, _i32, _c_p, _c_p, _i64, _c_p, _i64, _i32, _i32, _f32,
                                          _c_p]),
-    "rspx_qkv_rope_cache_partials": (_i32, [_c_p, _i32, _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _c_p, _i64, _i64, _c_p,
+    "rspx_qkv_rope_cache_partials": (_i32, [_c_p, _i32, _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i32, _c_p, _i64, _i64, _c_p,
                                             _i64, _i64, _c_p, _i32, _i32, _i32, _i32, _f32, _c_p]),
 }
 

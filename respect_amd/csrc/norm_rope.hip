@@ -278,13 +278,14 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* q, in
 // q_norm / k_norm RMSNorm and RoPE (the arithmetic of qk_norm_rope_kernel);
 // q goes to qo [T, HQ, D], k and v are written straight into the KV cache at
 // the token's physical slot: cache[h][slot[t]][:] (head stride sh, slot
-// stride sn).
+// stride sn).  A slot outside [0, cap) writes no K/V and makes the token's q
+// NaN, so the error shows in every output that token reaches.
 template <int SC>
 __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(const uint16_t* qkv, int64_t sqkv, const float* qp,
                                                              int S, int64_t sps, const uint16_t* wq,
                                                              const uint16_t* wk, const uint16_t* cosb,
                                                              const uint16_t* sinb, int64_t scs, const int* slots,
-                                                             uint16_t* ck, int64_t skh, int64_t skn, uint16_t* cv,
+                                                             int cap, uint16_t* ck, int64_t skh, int64_t skn, uint16_t* cv,
                                                              int64_t svh, int64_t svn, uint16_t* qo, int T, int HQ,
                                                              int HK, float eps) {
   constexpr int D = 128;
@@ -308,8 +309,11 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(const uint16_t* qkv
   } else {
     raw = *reinterpret_cast<const u32x4*>(qkv + (int64_t)t * sqkv + col);
   }
+  const int slot = slots[t];
+  const bool slot_ok = slot >= 0 && slot < cap;
+  if (kind != 0 && !slot_ok) return;
   if (kind == 2) {
-    *reinterpret_cast<u32x4*>(cv + hh * svh + (int64_t)slots[t] * svn + sub * 8) = raw;
+    *reinterpret_cast<u32x4*>(cv + hh * svh + (int64_t)slot * svn + sub * 8) = raw;
     return;
   }
   float xv[8];
@@ -326,7 +330,11 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(const uint16_t* qkv
   unpack8(*reinterpret_cast<const u32x4*>(cosb + (int64_t)t * scs + sub * 8), cs);
   unpack8(*reinterpret_cast<const u32x4*>(sinb + (int64_t)t * scs + sub * 8), sn);
   rope_vec(nv, cs, sn, sub, o);
-  uint16_t* dst = kind == 0 ? qo + ((int64_t)t * HQ + hh) * D : ck + hh * skh + (int64_t)slots[t] * skn;
+  uint16_t* dst = kind == 0 ? qo + ((int64_t)t * HQ + hh) * D : ck + hh * skh + (int64_t)slot * skn;
+  if (!slot_ok) {
+    *reinterpret_cast<u32x4*>(dst + sub * 8) = u32x4{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
+    return;
+  }
   *reinterpret_cast<u32x4*>(dst + sub * 8) = pack8(o);
 }
 
@@ -456,10 +464,10 @@ extern "C" int rspx_qk_norm_rope(const void* q, int64_t sqt, int64_t sqh, const 
 
 static int qkv_rope_cache_launch(const uint16_t* qkv, int64_t sqkv, const float* qp, int S, int64_t sps,
                                  const void* wq, const void* wk, const void* cosb, const void* sinb, int64_t scs,
-                                 const int32_t* slots, void* cache_k, int64_t skh, int64_t skn, void* cache_v,
+                                 const int32_t* slots, int cap, void* cache_k, int64_t skh, int64_t skn, void* cache_v,
                                  int64_t svh, int64_t svn, void* qo, int T, int HQ, int HK, int D, float eps,
                                  void* stream) {
-  if (T < 0 || HQ <= 0 || HK <= 0) return RSPX_EINVAL;
+  if (T < 0 || HQ <= 0 || HK <= 0 || cap < 0) return RSPX_EINVAL;
   if (D != 128) return RSPX_EUNSUPPORTED;
   if (T == 0) return RSPX_OK;
   if ((!qkv && !qp) || !wq || !wk || !cosb || !sinb || !slots || !cache_k || !cache_v || !qo) return RSPX_EINVAL;
@@ -475,28 +483,28 @@ static int qkv_rope_cache_launch(const uint16_t* qkv, int64_t sqkv, const float*
                                       0, static_cast<hipStream_t>(stream), qkv, sqkv, qp, S, sps,
                                       static_cast<const uint16_t*>(wq), static_cast<const uint16_t*>(wk),
                                       static_cast<const uint16_t*>(cosb), static_cast<const uint16_t*>(sinb), scs,
-                                      slots, static_cast<uint16_t*>(cache_k), skh, skn,
+                                      slots, cap, static_cast<uint16_t*>(cache_k), skh, skn,
                                       static_cast<uint16_t*>(cache_v), svh, svn, static_cast<uint16_t*>(qo), T, HQ,
                                       HK, eps));
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }
 
 extern "C" int rspx_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* wq, const void* wk, const void* cosb,
-                                   const void* sinb, int64_t scs, const int32_t* slots, void* cache_k, int64_t skh,
-                                   int64_t skn, void* cache_v, int64_t svh, int64_t svn, void* qo, int T, int HQ,
-                                   int HK, int D, float eps, void* stream) {
+                                   const void* sinb, int64_t scs, const int32_t* slots, int cap, void* cache_k,
+                                   int64_t skh, int64_t skn, void* cache_v, int64_t svh, int64_t svn, void* qo, int T,
+                                   int HQ, int HK, int D, float eps, void* stream) {
   if (!qkv) return RSPX_EINVAL;
   return qkv_rope_cache_launch(static_cast<const uint16_t*>(qkv), sqkv, nullptr, 1, 0, wq, wk, cosb, sinb, scs, slots,
-                               cache_k, skh, skn, cache_v, svh, svn, qo, T, HQ, HK, D, eps, stream);
+                               cap, cache_k, skh, skn, cache_v, svh, svn, qo, T, HQ, HK, D, eps, stream);
 }
 
 extern "C" int rspx_qkv_rope_cache_partials(const float* qkvp, int S, const void* wq, const void* wk,
                                             const void* cosb, const void* sinb, int64_t scs, const int32_t* slots,
-                                            void* cache_k, int64_t skh, int64_t skn, void* cache_v, int64_t svh,
+                                            int cap, void* cache_k, int64_t skh, int64_t skn, void* cache_v, int64_t svh,
                                             int64_t svn, void* qo, int T, int HQ, int HK, int D, float eps,
                                             void* stream) {
   if (!qkvp || S < 1 || S > kMaxSplits) return RSPX_EINVAL;
   const int64_t n = (int64_t)(HQ + 2 * HK) * D;
-  return qkv_rope_cache_launch(nullptr, n, qkvp, S, (int64_t)T * n, wq, wk, cosb, sinb, scs, slots, cache_k, skh,
+  return qkv_rope_cache_launch(nullptr, n, qkvp, S, (int64_t)T * n, wq, wk, cosb, sinb, scs, slots, cap, cache_k, skh,
                                skn, cache_v, svh, svn, qo, T, HQ, HK, D, eps, stream);
 }

@@ -82,6 +82,7 @@ struct TrieAttnArgs {
   float* gp_ml;       // [HK][R][NG][2]  group partial (m, l)
   float* gp_acc;      // [HK][R][NG][D]
   int* sync;          // fused launch: a timeout flag, then [HK][NRB][2] counters
+  int spin;           // fused launch: polls of a block's counter before the wait gives up
 };
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -1085,15 +1086,32 @@ __global__ __launch_bounds__(64 * kWavesA) void node_merge_kernel(TrieAttnArgs A
   merge_rounds<D, false, LY>(A, g, p0, rend, (const lds_char*)kv, w);
 }
 
+// NaN in every element of rows [p0, rend) of kv head g (row p0 + w + 8 i on
+// wave w): the output of a workgroup whose wait for the group partials gave up.
+template <int D>
+__device__ __forceinline__ void nan_rows(const TrieAttnArgs& A, int g, int p0, int rend, int w) {
+  constexpr int DL = D / 64;
+  const int lane = __lane_id();
+  for (int r = p0 + w; r < rend; r += kWavesA) {
+    const RowRef R = row_ref(A, g, r, r);
+    uint16_t* o = A.out + (R.hd * A.soh + R.mq * A.som + DL * lane);
+    if constexpr (DL == 2) *reinterpret_cast<uint32_t*>(o) = 0x7fc07fc0u;
+    else *o = (uint16_t)0x7fc0;
+  }
+}
+
 // ------------------------------------------------------------------ fused kernel
 // One launch: workgroup (g, rb, q) runs prompt_block, counts itself in
 // cnt[g][rb], computes the node partials of its share of the block's rows --
 // rows q RPW .. q RPW + RPW - 1 of the block, row r0 + w + 8 i on wave w --
 // and, once all NG groups of the block are counted, merges those rows.  Every
 // workgroup of the grid is resident at once (the host launches this kernel
-// only when the grid fits), so the wait always ends; it is also bounded, and a
-// bound reached raises a flag the host can read.  The last workgroup of a
-// block to finish its merge resets the block's counters to zero.
+// only when the grid fits), so the wait always ends; it is also bounded
+// (A.spin polls), and a workgroup whose wait gives up stores NaN in every
+// element of the rows it would merge -- the failure reaches the caller's
+// output without a host synchronisation -- and raises a flag the host can
+// read.  The last workgroup of a block to finish resets the block's counters
+// to zero, whether or not a wait gave up.
 //
 // Visibility without cache-wide fences: every word that crosses workgroups
 // (group partials, counters) is written by an agent-scope atomic store or
@@ -1106,6 +1124,9 @@ __global__ __launch_bounds__(64 * kWavesA) void node_merge_kernel(TrieAttnArgs A
 // buffer_inv of the whole L2) would order the same accesses at several
 // microseconds per workgroup.
 constexpr int kSpinLimit = 1 << 22;
+// Polls before a fused launch's wait gives up (rspx_trie_attn_set_spin_limit
+// lowers it so tests can exercise the give-up path with every kernel exiting).
+static int g_spin_limit = kSpinLimit;
 constexpr int kSyncWords = 4096;   // timeout flag + [HK][NRB][2] counters
 
 // RES3: the node areas of NodeLds3 (three resident chunks), for grids whose
@@ -1113,8 +1134,8 @@ constexpr int kSyncWords = 4096;   // timeout flag + [HK][NRB][2] counters
 template <int D, int kRT, bool RES3>
 __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   using LY = typename std::conditional<RES3, NodeLds3<D>, NodeLds<D>>::type;
-  constexpr int LB = PromptLds<D, kRT>::BYTES > LY::BYTES ? PromptLds<D, kRT>::BYTES : LY::BYTES;
-  static_assert(LY::BYTES <= PromptLds<D, kRT>::RINGBYTES, "node LDS inside the ring");
+  constexpr int LB = PromptLds<D, kRT>::BYTES > LY::BYTES + 16 ? PromptLds<D, kRT>::BYTES : LY::BYTES + 16;
+  static_assert(LY::BYTES + 16 <= PromptLds<D, kRT>::RINGBYTES, "node LDS and the wait flag inside the ring");
   static_assert(RES3 || 32 * kRT <= LY::kRows, "a row block fits the node areas");
   __shared__ __attribute__((aligned(16))) char lds[LB];
   const int lane = __lane_id();
@@ -1143,18 +1164,23 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
 
   if (r0 < rend) {
     node_rows<D, LY>(A, g, r0, rend, (lds_char*)lds, w, pre, pf);
+    int* gave_up = reinterpret_cast<int*>(lds + LY::BYTES);  // one LDS word past the node areas
     if (w == 0) {
       int v = 0;
-      for (int it = 0; it < kSpinLimit; ++it) {
+      for (int it = 0; it < A.spin; ++it) {
         v = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (v >= A.NG) break;
         __builtin_amdgcn_s_sleep(2);
       }
-      if (v < A.NG && lane == 0) __hip_atomic_store(A.sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane == 0) {
+        *gave_up = v < A.NG;
+        if (v < A.NG) __hip_atomic_store(A.sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     }
     lds_barrier();
-    merge_rounds<D, true, LY>(A, g, r0, rend, (const lds_char*)lds, w);
+    if (__builtin_amdgcn_readfirstlane(*gave_up)) nan_rows<D>(A, g, r0, rend, w);
+    else merge_rounds<D, true, LY>(A, g, r0, rend, (const lds_char*)lds, w);
   }
   // Counters back to zero once every workgroup of the block is past its wait.
   lds_barrier();
@@ -1330,6 +1356,7 @@ static int trie_attn_impl(const void* q, int64_t sqh, int64_t sqm, const void* k
   a.gp_ml = reinterpret_cast<float*>(ws + pl.off_gp_ml);
   a.gp_acc = reinterpret_cast<float*>(ws + pl.off_gp_acc);
   a.sync = reinterpret_cast<int*>(ws + pl.off_sync);
+  a.spin = g_spin_limit;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (D == 128) launch_all<128>(a, pl, s, mode);
@@ -1359,6 +1386,12 @@ extern "C" int rspx_trie_attn_launches(const void* q, int64_t sqh, int64_t sqm, 
   return trie_attn_impl(q, sqh, sqm, kp, skph, skpn, vp, svph, svpn, kn, sknh, sknn, vn, svnh, svnn, msk, smm, smn,
                         out, soh, som, H, HK, M, P, NN, D, sm_scale, workspace, workspace_bytes, rows_per_wave,
                         stream, launches);
+}
+
+extern "C" int rspx_trie_attn_set_spin_limit(int polls) {
+  const int prev = g_spin_limit;
+  g_spin_limit = polls < 0 ? kSpinLimit : polls;
+  return prev;
 }
 
 extern "C" int rspx_trie_attn_status(const void* workspace, int H, int HK, int M, int P, int D, void* stream) {

@@ -36,16 +36,27 @@ def greedy_token(logits: torch.Tensor, offset: int = 0, size: int = 0, out: torc
 
 def walk(tree: Trie, first: int, cap: int, eos: int,
          pick: Callable[[list[int], int], int]) -> tuple[list[int], list[int], int]:
-    """Follow the trie from ``first`` while candidates match the target's choice
-    (acceptance.py:26-46).  Returns (node path, accepted tokens, correction token)."""
-    path, acc = [], []
-    ch, rec = tree.roots.get(first), first
-    while ch is not None and len(acc) < cap:
-        nd = tree.nodes[ch]
-        path.append(ch)
-        acc.append(nd.token)
-        if nd.token == eos:
+    """Accept trie tokens while they match the target's choice (acceptance.py:26-46).
+
+    Starts at the root whose token is ``first`` and takes at most ``cap`` nodes.
+    After each accepted node (unless its token is ``eos``) ``pick(tokens, node)``
+    gives the target's next token; the walk descends to the child carrying it, or
+    stops when there is none.  Returns (node path, accepted tokens, correction
+    token): the correction is the last token ``pick`` returned, ``first`` if it
+    was never called.
+    """
+    path: list[int] = []
+    tokens: list[int] = []
+    correction = first
+    node = tree.roots.get(first)
+    for _ in range(max(cap, 0)):
+        if node is None:
             break
-        rec = pick(acc, ch)
-        ch = nd.children.get(rec)
-    return path, acc, rec
+        entry = tree.nodes[node]
+        path.append(node)
+        tokens.append(entry.token)
+        if entry.token == eos:
+            break
+        correction = pick(tokens, node)
+        node = entry.children.get(correction)
+    return path, tokens, correction

@@ -33,6 +33,7 @@ is decoded alone -- the property the reference's verification relies on
 """
 from __future__ import annotations
 
+import weakref
 from dataclasses import dataclass
 
 import torch
@@ -135,7 +136,7 @@ class Decoder:
         self._ws = {}
         self._ws_retired = []   # outgrown buffers: a captured graph may still point at them
         self._rope = None       # (cos, sin) [positions, head_dim] bf16 tables
-        self._graphs = {}
+        self._graphs: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
 
     def _workspace(self, name: str, nbytes: int) -> torch.Tensor:
         """Scratch owned by the model, grown (never while a graph is being
@@ -208,6 +209,8 @@ class Decoder:
         dev = self.device
         s = _lib.stream_ptr(dev)
         T = int(ids.shape[0])
+        if P < 0 or NN < 0 or P + NN > cache.cap:
+            raise ValueError(f"forward: prompt {P} + node segment {NN} exceeds the cache's {cache.cap} slots")
         Hd, HQ, HK, D = cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim
         bf = torch.bfloat16
         TILED = _lib.RSPX_TILED
@@ -227,7 +230,7 @@ class Decoder:
             qkvp, S = self._partials(y.data_ptr(), TILED, T, lay.wqkv)
             _lib.check("rspx_qkv_rope_cache_partials", L.rspx_qkv_rope_cache_partials(
                 qkvp, S, lay.q_norm.data_ptr(), lay.k_norm.data_ptr(), cos.data_ptr(),
-                sin.data_ptr(), cos.stride(0), slots32.data_ptr(), ck.data_ptr(), ck.stride(0), ck.stride(1),
+                sin.data_ptr(), cos.stride(0), slots32.data_ptr(), cache.cap, ck.data_ptr(), ck.stride(0), ck.stride(1),
                 cv.data_ptr(), cv.stride(0), cv.stride(1), qo.data_ptr(), T, HQ, HK, D, cfg.eps, s))
             trie_attn(qo.permute(1, 0, 2), ck[:, :P], cv[:, :P], ck[:, P:P + NN], cv[:, P:P + NN], msk,
                       self.sm_scale, out=att.permute(1, 0, 2), workspace=ws_attn)
@@ -260,6 +263,8 @@ class Decoder:
         forward: a chunk sees the earlier chunks as its prompt segment and
         itself causally as its node segment.  Returns the last row's logits."""
         n = int(ids.shape[0])
+        if n > cache.cap:
+            raise ValueError(f"prefill: {n} prompt tokens exceed the cache's {cache.cap} slots")
         dev = self.device
         logits = None
         for c0 in range(0, n, chunk):
@@ -273,13 +278,27 @@ class Decoder:
 
     # ------------------------------------------------------------------ graphs
     def graphed(self, cache, P: int, T: int, NN: int) -> "GraphedForward":
-        """A captured forward for T rows, prompt P and node segment NN (cached)."""
-        key = (id(cache), P, T, NN)
-        g = self._graphs.get(key)
+        """A captured forward for T rows, prompt P and node segment NN over
+        ``cache``.  Graphs are kept per cache object (a weak key: they are
+        dropped with the cache whose device pointers they hold, so a new cache
+        never replays a graph of a freed one)."""
+        per_cache = self._graphs.get(cache)
+        if per_cache is None:
+            per_cache = {}
+            self._graphs[cache] = per_cache
+        key = (P, T, NN, cache.cap)
+        g = per_cache.get(key)
         if g is None:
             g = GraphedForward(self, cache, P, T, NN)
-            self._graphs[key] = g
+            per_cache[key] = g
         return g
+
+    def release_graphs(self, cache=None) -> None:
+        """Drop the captured forwards of ``cache`` (all caches if None) and their memory pools."""
+        if cache is None:
+            self._graphs.clear()
+        else:
+            self._graphs.pop(cache, None)
 
 
 class GraphedForward:
@@ -310,7 +329,9 @@ class GraphedForward:
         self.picked = torch.cuda.Event()
         L = _lib.lib()
         vocab = model.cfg.vocab
-        argws = torch.zeros(max(16, L.rspx_argmax_workspace_bytes(T, vocab)), dtype=torch.uint8, device=dev)
+        # Held by the object: the captured argmax writes here on every replay.
+        self.argws = argws = torch.zeros(max(16, L.rspx_argmax_workspace_bytes(T, vocab)), dtype=torch.uint8,
+                                         device=dev)
 
         def body():
             _lib.check("rspx_step_inputs", L.rspx_step_inputs(

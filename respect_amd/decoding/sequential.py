@@ -14,6 +14,8 @@ def forward_token(model, cache, token: int, P: int, c: int, graph: bool = False)
     P + c); it sees the prompt and node slots [0, c].  Returns fp32 logits [1, V].
     ``graph``: replay a captured forward (node segment padded to 64)."""
     dev = model.device
+    if c < 0 or P + c >= cache.cap:
+        raise ValueError(f"forward_token: slot {P + c} outside the cache's {cache.cap} slots")
     if graph:  # a one-node trie after c committed slots: slot P + c, position P + c, slots [0, c] open
         NN = node_slots(c, 1, 64)
         return model.graphed(cache, P, 1, NN).run(1, c, [token], [-1])

@@ -135,12 +135,22 @@ def test_invariance_sweep(P, tri):
         assert torch.equal(one[:, 0], full[:, i]), f"P={P} n={n} base={base} node {i}"
 
 
+def _slot_layout_fixture():
+    import json
+    from pathlib import Path
+    kats = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
+    return kats["slot_layout"]
+
+
 def test_slot_layout_invariance_reference_shapes():
     """tests/test_kernel_invariance.py:30-54 of the reference: 26 node values in slots
-    0-25 vs 0-17 + 200-207, H=32, HK=8, D=128, NP=300, NN=224, 64 query rows."""
+    0-25 vs 0-17 + 200-207, H=32, HK=8, D=128, NP=300, NN=224, 64 query rows (sizes read
+    from tests/golden/reference_kats.json)."""
+    fx = _slot_layout_fixture()
     rng = np.random.default_rng(0)
-    H, HK, D, NP, n, NN = 32, 8, 128, 300, 26, 224
-    q = gen.bf16_normal(rng, (H, 64, D))
+    H, HK, D, NP, n, NN, M = fx["H"], fx["HK"], fx["D"], fx["NP"], fx["n"], fx["NN"], fx["M"]
+    assert n == 26 and NN == 224
+    q = gen.bf16_normal(rng, (H, M, D))
     kp = gen.bf16_normal(rng, (HK, NP, D))
     vp = gen.bf16_normal(rng, (HK, NP, D))
     kk = gen.bf16_normal(rng, (HK, n, D))
@@ -149,7 +159,7 @@ def test_slot_layout_invariance_reference_shapes():
     for slots in (list(range(n)), list(range(18)) + list(range(200, 208))):
         kn = np.zeros((HK, NN, D), np.float32)
         vn = np.zeros_like(kn)
-        msk = np.zeros((64, NN), bool)
+        msk = np.zeros((M, NN), bool)
         kn[:, slots] = kk
         vn[:, slots] = vv
         msk[:, slots] = True
@@ -162,7 +172,7 @@ def test_slot_layout_invariance_reference_shapes():
         slots = sorted(np.random.default_rng(seed).choice(NN, n, replace=False).tolist())
         kn = np.zeros((HK, NN, D), np.float32)
         vn = np.zeros_like(kn)
-        msk = np.zeros((64, NN), bool)
+        msk = np.zeros((M, NN), bool)
         kn[:, slots] = kk
         vn[:, slots] = vv
         msk[:, slots] = True
@@ -298,3 +308,30 @@ def test_one_launch_workspace_shared_by_shapes():
         for c, w in zip(cases, want):
             assert torch.equal(_run(c, launches=1, workspace=ws), w)
     assert _status(cases[0], ws) == 0
+
+
+@pytest.mark.parametrize("which", ["cfg2", "cfg1"])
+def test_wait_that_gives_up_poisons_its_rows(which):
+    """One-launch path with the counter wait forced to give up at once (the spin limit
+    lowered through the test hook, so every workgroup still exits normally): every row
+    whose merge could not wait is NaN in every element -- the failure reaches the
+    output without a host synchronisation -- and the status flag is raised.  With the
+    default limit restored the same workspace gives the two-launch bits again (the
+    counters were left at zero)."""
+    from respect_amd import _lib
+    c = gen.cfg2(seed=6) if which == "cfg2" else gen.cfg1()
+    H, M, D = c.q.shape
+    HK, P, _ = c.kp.shape
+    L = _lib.lib()
+    ws = torch.zeros(L.rspx_trie_attn_workspace_bytes(H, HK, M, P, D), dtype=torch.uint8, device="cuda")
+    ref = _run(c, launches=2)
+    prev = L.rspx_trie_attn_set_spin_limit(0)
+    try:
+        bad = _run(c, launches=1, workspace=ws)
+    finally:
+        L.rspx_trie_attn_set_spin_limit(prev)
+    assert _status(c, ws) == 1
+    # a limit of 0 polls gives up in every workgroup: every row is NaN in every element
+    assert torch.isnan(bad.float()).all()
+    good = _run(c, launches=1, workspace=ws)
+    assert torch.equal(good, ref)

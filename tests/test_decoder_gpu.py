@@ -223,3 +223,35 @@ def test_graph_replays_equal_eager(model):
         g1 = forward_token(model, cache, seq[1], P, base, graph=True).clone()
         assert torch.equal(e1, g1)
         assert next_token(model, cache, seq[1], P, base) == int(greedy_token(e1).item())
+
+
+def test_graphs_are_tied_to_their_cache(model):
+    """A captured forward holds its cache's device pointers: dropping the cache drops its
+    graphs, and a new cache (which may get the old one's id) captures its own."""
+    import gc
+    from respect_amd.decoding.acceptance import greedy_token
+    from respect_amd.decoding.sequential import forward_token
+    model.release_graphs()
+    cache, last = _filled_cache(model)
+    t0 = int(greedy_token(last).item())
+    g1 = model.graphed(cache, P, 1, 64)
+    assert len(model._graphs) == 1 and model.graphed(cache, P, 1, 64) is g1
+    del cache, last, g1
+    gc.collect()
+    assert len(model._graphs) == 0
+    cache2, last2 = _filled_cache(model)
+    eager = forward_token(model, cache2, t0, P, 0).clone()
+    graphed = forward_token(model, cache2, t0, P, 0, graph=True).clone()
+    assert torch.equal(eager, graphed)
+    assert len(model._graphs) == 1 and model._graphs.get(cache2) is not None
+
+
+def test_capacity_is_enforced(model):
+    """Slots past the cache's capacity are refused on the host (eager paths) before any
+    kernel is queued."""
+    from respect_amd.decoding.sequential import forward_token
+    cache, _ = _filled_cache(model)
+    with pytest.raises(ValueError):
+        forward_token(model, cache, 1, P, cache.cap - P)
+    with pytest.raises(ValueError):
+        model.prefill(torch.zeros(cache.cap + 1, dtype=torch.int64, device="cuda"), cache)

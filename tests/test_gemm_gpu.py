@@ -135,8 +135,8 @@ def test_partials_consumers_equal_linear_then_op():
         ck = torch.zeros(HK, P, D, device="cuda", dtype=torch.bfloat16)
         cv = torch.zeros_like(ck)
         qo = torch.empty(T, HQ, D, device="cuda", dtype=torch.bfloat16)
-        common = (wq.data_ptr(), wk.data_ptr(), cos.data_ptr(), sin.data_ptr(), D, slots.data_ptr(), ck.data_ptr(),
-                  P * D, D, cv.data_ptr(), P * D, D, qo.data_ptr(), T, HQ, HK, D, 1e-6, s)
+        common = (wq.data_ptr(), wk.data_ptr(), cos.data_ptr(), sin.data_ptr(), D, slots.data_ptr(), P,
+                  ck.data_ptr(), P * D, D, cv.data_ptr(), P * D, D, qo.data_ptr(), T, HQ, HK, D, 1e-6, s)
         if use_part:
             assert L.rspx_qkv_rope_cache_partials(part.data_ptr(), S, *common) == 0
         else:
@@ -145,6 +145,25 @@ def test_partials_consumers_equal_linear_then_op():
     for a, b in zip(*outs):
         assert torch.equal(a, b)
     assert torch.equal(outs[0][2][:, 3:3 + T].transpose(0, 1), qkv[:, (HQ + HK) * D:].view(T, HK, D))
+    # Slots outside [0, cap): no K/V write anywhere, the token's q row is NaN, the other
+    # tokens are unchanged.
+    bad = slots.clone()
+    bad[1], bad[T - 1] = P, -1
+    ck = torch.zeros(HK, P + 8, D, device="cuda", dtype=torch.bfloat16)   # 8 guard slots past cap
+    cv = torch.zeros_like(ck)
+    qo = torch.empty(T, HQ, D, device="cuda", dtype=torch.bfloat16)
+    assert L.rspx_qkv_rope_cache(qkv.data_ptr(), n, wq.data_ptr(), wk.data_ptr(), cos.data_ptr(), sin.data_ptr(), D,
+                                 bad.data_ptr(), P, ck.data_ptr(), (P + 8) * D, D, cv.data_ptr(), (P + 8) * D, D,
+                                 qo.data_ptr(), T, HQ, HK, D, 1e-6, s) == 0
+    torch.cuda.synchronize()
+    assert torch.isnan(qo[1]).all() and torch.isnan(qo[T - 1]).all()
+    good = [t for t in range(T) if t not in (1, T - 1)]
+    assert torch.equal(qo[good], outs[0][0][good])
+    assert torch.equal(ck[:, :P][:, slots[good].long()], outs[0][1][:, slots[good].long()])
+    assert not ck[:, P:].any() and not cv[:, P:].any()
+    written = torch.zeros(P + 8, dtype=torch.bool)
+    written[slots[good].long().cpu()] = True
+    assert not ck[:, ~written.cuda()].any()
 
 
 @pytest.mark.parametrize("M", [1, 7, 64, 130])
