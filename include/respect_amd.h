@@ -138,6 +138,23 @@ int rspx_trie_attn_launches(const void* q, int64_t sqh, int64_t sqm, const void*
  */
 int rspx_trie_attn_status(const void* workspace, int H, int HK, int M, int P, int D, void* stream);
 
+/* rspx_trie_attn without a workspace argument: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * scratch is a 32 MiB array in the library's code object, one per GPU,
+ * held until the process ends; the call allocates nothing.  Calls whose
+ * rspx_trie_attn_workspace_bytes(H, HK, M, P, D) exceeds 32 MiB return
+ * RSPX_EWORKSPACE (the 8B shape holds up to 251 query rows at 3072 prompt
+ * keys).  Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (two streams, two host threads) race and give invalid results.
+ * Same results, bit for bit, as rspx_trie_attn.
+ */
+int rspx_trie_attn_noalloc(const void* q, int64_t sqh, int64_t sqm, const void* kp, int64_t skph, int64_t skpn,
+                           const void* vp, int64_t svph, int64_t svpn, const void* kn, int64_t sknh, int64_t sknn,
+                           const void* vn, int64_t svnh, int64_t svnn, const uint8_t* msk, int64_t smm, int64_t smn,
+                           void* out, int64_t soh, int64_t som, int H, int HK, int M, int P, int NN, int D,
+                           float sm_scale, int rows_per_wave, void* stream);
+
 /* Test hook, no counterpart in the reference: sets how many times a one-launch
  * workgroup polls its row block's counter before its wait gives up (a
  * negative value restores the default, 2^22 polls); returns the previous

@@ -52,6 +52,7 @@
 //   8 kv heads, workgroup g of kernel A lands on XCD g (round-robin dispatch),
 //   so the row blocks that share a head's K/V meet in one XCD's L2.
 
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1372,6 +1373,61 @@ extern "C" int rspx_trie_attn(const void* q, int64_t sqh, int64_t sqm, const voi
                               void* stream) {
   return trie_attn_impl(q, sqh, sqm, kp, skph, skpn, vp, svph, svpn, kn, sknh, sknn, vn, svnh, svnn, msk, smm, smn,
                         out, soh, som, H, HK, M, P, NN, D, sm_scale, workspace, workspace_bytes, rows_per_wave,
+                        stream, 0);
+}
+
+// ------------------------------------------------------------------ allocation-free variant
+// A workspace that lives in the code object: one per GPU the library runs on,
+// held until the process ends.  Its first kSyncWords ints are the one-launch
+// synchronisation words (zero between calls: every call leaves them at zero);
+// the group partials follow, as in a caller's workspace.  In host code the
+// array's name is only a stand-in: the device address comes from
+// hipGetSymbolAddress, once per device, and is what kernels are given.
+constexpr size_t kStaticScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) char scratch[kStaticScratchBytes];
+
+__global__ void zero_words_kernel(int* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64];
+
+// Device address of this device's scratch; the first call on a device looks it
+// up and queues a fill kernel that zeroes the synchronisation words.
+static int static_scratch(void** out, hipStream_t s) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return RSPX_ELAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return RSPX_ELAUNCH;
+    hipLaunchKernelGGL(zero_words_kernel, dim3((kSyncWords + 255) / 256), dim3(256), 0, s, static_cast<int*>(p),
+                       kSyncWords);
+    if (hipGetLastError() != hipSuccess) return RSPX_ELAUNCH;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return RSPX_OK;
+}
+
+extern "C" int rspx_trie_attn_noalloc(const void* q, int64_t sqh, int64_t sqm, const void* kp, int64_t skph,
+                                      int64_t skpn, const void* vp, int64_t svph, int64_t svpn, const void* kn,
+                                      int64_t sknh, int64_t sknn, const void* vn, int64_t svnh, int64_t svnn,
+                                      const uint8_t* msk, int64_t smm, int64_t smn, void* out, int64_t soh,
+                                      int64_t som, int H, int HK, int M, int P, int NN, int D, float sm_scale,
+                                      int rows_per_wave, void* stream) {
+  Plan pl;
+  const int rc = make_plan(H, HK, M, P, NN, D, rows_per_wave, &pl);
+  if (rc != RSPX_OK) return rc;
+  if (pl.total > kStaticScratchBytes) return RSPX_EWORKSPACE;
+  if (M == 0) return RSPX_OK;
+  void* ws = nullptr;
+  const int sr = static_scratch(&ws, static_cast<hipStream_t>(stream));
+  if (sr != RSPX_OK) return sr;
+  return trie_attn_impl(q, sqh, sqm, kp, skph, skpn, vp, svph, svpn, kn, sknh, sknn, vn, svnh, svnn, msk, smm, smn,
+                        out, soh, som, H, HK, M, P, NN, D, sm_scale, ws, (int64_t)kStaticScratchBytes, rows_per_wave,
                         stream, 0);
 }
 
