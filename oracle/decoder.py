@@ -13,8 +13,12 @@ SwiGLU), attention is the exact softmax in float64.
 Test infrastructure only: it checks the wiring of the GPU decoder (which
 projection rows are q, k, v; where RoPE applies; which slots a row sees),
 not bits -- bitwise parity of the GPU path is against its own 1-token path.
-Pinned by: its pieces are oracle.norm (pinned against PyTorch) and exact
-float64 attention; tests/test_oracle_decoder.py checks, on tiny models, that
+Pinned by: transformers' own Qwen3-VL text decoder on the CPU with the same
+weights (logits within 3 % of the largest, where a RoPE sign, swapped k/v or
+gate/up rows, dropped q/k norms, swapped layer norms or a row not seeing its
+own slot each move them by 25 % or more); its pieces are oracle.norm (pinned
+against PyTorch) and exact float64 attention; tests/test_oracle_decoder.py
+also checks, on tiny models, that
 its batched forward equals its own token-by-token forward, that the cache
 slot layout does not matter, and that with a single visible key the q/k
 weights cannot change the logits (the attention output is that key's value).

@@ -1,13 +1,29 @@
 """GPU parity and invariance tests of the trie-verification attention kernel.
 
-Parity: every output element lies within the deterministic error bound of the
-reference's rounding points around the float64 answer
-(oracle.attention.attn_error_bound: 2^-9 relative error of the bf16 prompt
-probabilities + fp32 slack + 1 bf16 ulp), exactly the bound the oracle
-restatement of the reference kernel itself satisfies.  In bf16 ulps (at
-max(|exact|, rms/8)) the kernel must be at least as close to fp64 as the
-reference's own arithmetic: the fraction within 2 ulp and the mean ulp error
-may not be worse than the oracle's.
+Parity, three ways:
+(1) per element, within 2 bf16 ulp of oracle.attention.attn_tree -- the CPU
+    restatement of the kernel's own fixed reduction tree, itself pinned against
+    float64 attention (tests/test_oracle.py) -- the ulp taken at
+    max(|kernel|, |tree|, max|row| / 64).  The restatement
+    (oracle/c/attn_tree.c, bit for bit the numpy attn_tree) models each MFMA
+    as measured on MI355X and uses a correctly rounded exp2; the device's
+    v_exp_f32 differs from that by one fp32 ulp on ~5 % of inputs and the MFMA
+    model is exact on ~98.6 % (scores) / ~81 % (PV) of elements, so now and
+    then a probability rounds to bf16 differently and moves its whole row by
+    about an ulp at the row's scale -- an element 64x smaller than its row's
+    largest then shows several of its own ulps (measured at cfg2: 99.989 % of
+    elements bit-equal, max 1.0 ulp with the floor, 7 without);
+(2) every output element within the deterministic error bound of the
+    reference's rounding points around the float64 answer
+    (oracle.attention.attn_error_bound: 2^-9 relative error of the bf16 prompt
+    probabilities + fp32 slack + 1 bf16 ulp), the bound the restatement of the
+    reference kernel (attn_hyb) itself satisfies;
+(3) in bf16 ulps (at max(|exact|, rms/8)) at least as close to fp64 as the
+    reference's own arithmetic (attn_hyb): the fraction within 2 ulp and the
+    mean ulp error may not be worse.  attn_hyb's 128-key online softmax rounds
+    p against a different running maximum than any split-K tree, so the kernel
+    is not within 2 ulp of it everywhere (measured: 92-96 % of elements, at
+    most 13-16 ulp); (1) is the per-element bar.
 
 Invariance (bitwise, torch.equal): trie rows vs 1-token calls along each
 root path, slot layouts, committed-token offsets, rows-per-wave settings.
@@ -41,10 +57,31 @@ def _np(t):
     return t.float().cpu().numpy()
 
 
+TREE_ULP = 2.0   # per-element bar against the kernel-tree restatement, in bf16 ulp
+
+
+TREE_FLOOR = 64  # ulp taken at no less than max|row| / TREE_FLOOR
+
+
+def _check_tree(case, o):
+    """|kernel - attn_tree| <= 2 bf16 ulp of max(|kernel|, |attn_tree|, max|row| / 64),
+    every element."""
+    a = (case.q, case.kp, case.vp, case.kn, case.vn, case.msk, case.sm_scale)
+    t = A.attn_tree_c(*a)
+    mag = np.maximum(np.abs(o), np.abs(t))
+    err = np.abs(o.astype(np.float64) - t)
+    ud = err / bf16.ulp(np.maximum(mag, mag.max(axis=-1, keepdims=True) / TREE_FLOOR))
+    raw = err / bf16.ulp(mag)
+    print(f"  vs kernel tree: max {ud.max():.2f} ulp (no floor {raw.max():.1f}), "
+          f"<=1 {(ud <= 1).mean():.5f}, equal {(o == t).mean():.5f}", flush=True)
+    assert ud.max() <= TREE_ULP, f"max {ud.max():.2f} ulp at {np.unravel_index(ud.argmax(), ud.shape)}"
+
+
 def _check_parity(case, out):
     a = (case.q, case.kp, case.vp, case.kn, case.vn, case.msk, case.sm_scale)
     o = _np(out)
     assert np.isfinite(o).all()
+    _check_tree(case, o)
     e = A.attn_exact(*a)
     bound = A.attn_error_bound(*a)
     ratio = np.abs(o - e) / bound
@@ -128,6 +165,7 @@ def test_invariance_sweep(P, tri):
     base = int(rng.integers(0, 48))
     c = gen.attn_case(P + n, 32, 8, 128, P, seqs, length, lo, hi, n, kv_scale=128 ** -0.5, base=base)
     full = _run(c)
+    _check_tree(c, _np(full))
     depth = np.array([nd.depth for nd in c.tree.nodes])
     picks = {int(np.argmax(depth))} | {int(i) for i in rng.choice(n, min(n, 4), replace=False)}
     for i in sorted(picks):

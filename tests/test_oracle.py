@@ -201,3 +201,130 @@ def test_hyb_matches_one_token_paths_bitwise():
         pc = gen.path_case(c, i)
         one = A.attn_hyb(pc.q, pc.kp, pc.vp, pc.kn, pc.vn, pc.msk, pc.sm_scale)
         assert np.array_equal(one[:, 0], full[:, i])
+
+
+# ---------------------------------------------------------------- the kernel's tree and the blocked control
+
+def _growing(seed=0, H=4, HK=2, D=16, P=3000, M=6, NN=48, p_allow=0.4):
+    """Prompt keys whose norm grows along the prompt, so a quarter's reference maximum moves
+    by more than 2^8 between steps (the lazy rescale is exercised); P = 3000 spans 8 groups
+    of 12 steps with a ragged last step."""
+    q, kp, vp, kn, vn, msk = _small(seed, H, HK, D, P, M, NN, p_allow)
+    kp = bf16.round_bf16(kp * np.linspace(0.2, 4.0, P, dtype=np.float32)[None, :, None])
+    return q, kp, vp, kn, vn, msk
+
+
+@pytest.mark.parametrize("case", ["small", "growing", "cfg1"])
+def test_tree_close_to_exact_and_slips_fail(case):
+    args = {"small": lambda: _small(3, P=300), "growing": _growing,
+            "cfg1": lambda: (lambda c: (c.q, c.kp, c.vp, c.kn, c.vn, c.msk))(gen.cfg1())}[case]()
+    e = A.attn_exact(*args)
+    bound = A.attn_error_bound(*args)
+    o = A.attn_tree(*args)
+    assert (np.abs(o - e) <= bound).all()
+    q, kp, vp, kn, vn, msk = args
+    slips = {"no node segment": A.attn_tree(q, kp, vp, kn, vn, np.zeros_like(msk)),
+             "scale": A.attn_tree(*args, sm_scale=0.97 * q.shape[-1] ** -0.5),
+             "flat quarters": A.attn_tree(*args, _plant="flat_quarters")}
+    if case == "growing":
+        # the grown prompt keys take nearly all the weight: nodes are not checked here
+        del slips["no node segment"]
+        slips["no rescale"] = A.attn_tree(*args, _plant="no_rescale")
+    for name, bad in slips.items():
+        assert (np.abs(bad - e) > bound).mean() > 0.02, name
+
+
+def test_tree_plan_matches_the_kernels():
+    """prompt_plan's group count is the kernel's: the workspace the library asks for holds
+    HK * H/HK * M * NG group partials of (2 + D) floats after 16 KiB of counters."""
+    from respect_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("librespect_amd.so not built")
+    L = _lib.lib()
+    al = lambda x: (x + 255) // 256 * 256
+    for P in (1, 31, 32, 33, 512, 1023, 1024, 3000, 3072, 3086, 8192, 16384, 50000):
+        _, S, NG = A.prompt_plan(P)
+        for H, HK, M, D in ((32, 8, 64, 128), (8, 2, 16, 64)):
+            parts = HK * (H // HK) * M * NG
+            assert L.rspx_trie_attn_workspace_bytes(H, HK, M, P, D) == 16384 + al(parts * 8) + al(parts * D * 4), P
+
+
+def test_tree_known_answers():
+    rng = np.random.default_rng(5)
+    H, HK, D = 4, 2, 64
+    q = gen.bf16_normal(rng, (H, 3, D))
+    kp = gen.bf16_normal(rng, (HK, 1, D))
+    vp = gen.bf16_normal(rng, (HK, 1, D))
+    kn = gen.bf16_normal(rng, (HK, 16, D))
+    vn = gen.bf16_normal(rng, (HK, 16, D))
+    # one prompt key, no node slot allowed: out = v
+    o = A.attn_tree(q, kp, vp, kn, vn, np.zeros((3, 16), bool))
+    assert np.array_equal(o, np.repeat(vp, 2, axis=0)[:, [0, 0, 0]])
+    # no prompt, one allowed node slot anywhere: out = that slot's v
+    msk = np.zeros((3, 16), bool)
+    msk[:, 9] = True
+    o = A.attn_tree(q, kp[:, :0], vp[:, :0], kn, vn, msk)
+    assert np.array_equal(o, np.repeat(vn, 2, axis=0)[:, [9, 9, 9]])
+    # equal scores: the mean of the visible values
+    args = list(_small(7, P=200, NN=16, p_allow=0.5))
+    args[0] = np.zeros_like(args[0])
+    q, kp, vp, kn, vn, msk = args
+    o = A.attn_tree(*args)
+    VP = np.repeat(vp, H // kp.shape[0], 0).astype(np.float64)
+    VN = np.repeat(vn, H // kp.shape[0], 0).astype(np.float64)
+    for m in range(q.shape[1]):
+        mean = np.concatenate([VP, VN[:, msk[m]]], axis=1).mean(axis=1)
+        assert bf16.ulp_diff(o[:, m], mean, np.abs(mean).max() / 8).max() <= 1.0
+
+
+def test_tree_layout_invariant_and_matches_one_token_paths():
+    a, b = _layout_case()
+    assert np.array_equal(A.attn_tree(*a), A.attn_tree(*b))
+    c = gen.cfg1()
+    full = A.attn_tree(c.q, c.kp, c.vp, c.kn, c.vn, c.msk, c.sm_scale)
+    for i in range(len(c.tree.nodes)):
+        pc = gen.path_case(c, i)
+        one = A.attn_tree(pc.q, pc.kp, pc.vp, pc.kn, pc.vn, pc.msk, pc.sm_scale)
+        assert np.array_equal(one[:, 0], full[:, i])
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_blocked_close_to_exact_and_slips_fail(seed):
+    """attn_blocked (reference_blocked.py:14-80) against fp64 within the bound of its own
+    rounding points: p rounded to bf16 for prompt *and* node tiles."""
+    args = _small(seed, P=300, NN=96)
+    e = A.attn_exact(*args)
+    bound = A.attn_error_bound(*args, node_p_bf16=True)
+    assert (np.abs(A.attn_blocked(*args) - e) <= bound).all()
+    q, kp, vp, kn, vn, msk = args
+    for name, bad in {"mask ignored": A.attn_blocked(q, kp, vp, kn, vn, np.ones_like(msk)),
+                      "no node segment": A.attn_blocked(q, kp, vp, kn, vn, np.zeros_like(msk)),
+                      "scale": A.attn_blocked(*args, sm_scale=0.97 * q.shape[-1] ** -0.5)}.items():
+        assert (np.abs(bad - e) > bound).mean() > 0.02, name
+
+
+@pytest.mark.parametrize("shape", ["small", "growing", "cfg1", "nodes_only", "ragged"])
+def test_tree_c_equals_numpy_bitwise(shape):
+    """oracle/c/attn_tree.c, the restatement the GPU tests use at full size, is the numpy
+    attn_tree bit for bit (including sampled rows)."""
+    if shape == "cfg1":
+        c = gen.cfg1()
+        args = (c.q, c.kp, c.vp, c.kn, c.vn, c.msk, c.sm_scale)
+    elif shape == "growing":
+        args = _growing(P=700) + (None,)
+    elif shape == "nodes_only":
+        q, kp, vp, kn, vn, msk = _small(4, P=0, NN=48)
+        msk[:, 0] = True
+        args = (q, kp, vp, kn, vn, msk, None)
+    elif shape == "ragged":
+        args = _small(5, H=8, HK=2, D=64, P=1057, M=5, NN=80) + (0.11,)
+    else:
+        args = _small(3, P=300) + (None,)
+    a = A.attn_tree(*args)
+    b = A.attn_tree_c(*args)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    H, M = a.shape[:2]
+    rows = [0, H * M - 1, (H * M) // 2]
+    s = A.attn_tree_c(*args, rows=rows)
+    flat_a, flat_s = a.reshape(H * M, -1), s.reshape(H * M, -1)
+    assert np.array_equal(flat_s[rows].view(np.uint32), flat_a[rows].view(np.uint32))
