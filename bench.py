@@ -11,8 +11,9 @@ the 256 MB last-level cache.
 Timing: W untimed warm-up calls, then K calls enqueued behind a GPU sleep so the
 host never starves the queue; two HIP events on the launch stream bracket the K
 back-to-back calls.  ms_per_step = GPU time of the K calls / K, and
-roofline.achieved = algorithmic bytes per call / that time.  cpu_baseline times the CPU oracle (a numpy
-restatement of the reference kernel's arithmetic) on one input set.
+roofline.achieved = algorithmic bytes per call / that time.  cpu_baseline times the reference
+math on the host cores on one input set: fp32 masked SDPA in PyTorch on up to 16 threads,
+and beside it the literal logical-order fold on one thread.
 
 Prints ONE JSON line.  Only one GPU is used: --gpus N with N > 1 exits.
 """
@@ -54,35 +55,74 @@ def time_launches(launchers, steps: int, warmup: int) -> float:
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda._sleep(int(max(steps, 1) * 20e-6 * 2.4e9) + 10_000_000)
     start.record()
-    for i in range(steps):
-        launchers[i % n]()
+    for i in range(steps):   # the rotation continues after the warm-up's sets
+        launchers[(warmup + i) % n]()
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
 
 
+def cpu_threads() -> int:
+    """Host threads for the CPU baseline: the cores this process may run on, at most 16
+    (a GPU box's CPU share per GPU)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
 def cpu_baseline_attn(wl, budget_s: float = 20.0) -> dict:
-    """Time the CPU oracle (reference arithmetic in numpy) on input set 0, one thread."""
-    import numpy as np
+    """The reference math on the host cores, on input set 0 of the same workload.
+
+    (i) the headline figure: vectorised fp32 masked SDPA in PyTorch (torch's CPU
+        scaled_dot_product_attention, the prompt keys open to every row, node slots
+        by the mask; GQA by repeating K/V), torch.set_num_threads(cpu_threads());
+        3 warm-ups, then the median of up to 20 calls within the budget;
+    (ii) beside it: the literal logical-order fold of respect/kernels/attention.py:36-71
+        (the numpy oracle attn_hyb), one thread, median of a few calls.
+    """
+    import torch
     from threadpoolctl import threadpool_limits
 
     from oracle import attention as A
-    q, kp, vp, kn, vn = (t.float().cpu().numpy() for t in wl.sets[0])
-    msk = wl.msk.cpu().numpy()
-    times = []
-    with threadpool_limits(limits=1):
-        A.attn_hyb(q[:, :1], kp, vp, kn, vn, msk[:1], wl.sm_scale)  # warm numpy paths
-        t_end = time.perf_counter() + budget_s
-        while time.perf_counter() < t_end or len(times) < 2:
+    q, kp, vp, kn, vn = (t.float().cpu() for t in wl.sets[0])
+    msk = wl.msk.cpu().bool()
+    H, M, D = q.shape
+    rep = H // kp.shape[0]
+    K = torch.cat([kp, kn], 1).repeat_interleave(rep, 0).contiguous()
+    V = torch.cat([vp, vn], 1).repeat_interleave(rep, 0).contiguous()
+    allow = torch.cat([torch.ones(M, kp.shape[1], dtype=torch.bool), msk], 1)
+    threads = cpu_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        def sdpa():
+            return torch.nn.functional.scaled_dot_product_attention(q, K, V, attn_mask=allow, scale=wl.sm_scale)
+        for _ in range(3):
+            sdpa()
+        times, t_end = [], time.perf_counter() + budget_s / 2
+        while len(times) < 20 and (time.perf_counter() < t_end or len(times) < 3):
             t0 = time.perf_counter()
-            A.attn_hyb(q, kp, vp, kn, vn, msk, wl.sm_scale)
+            sdpa()
             times.append(time.perf_counter() - t0)
-            if len(times) >= 20:
-                break
+    finally:
+        torch.set_num_threads(prev)
     med = statistics.median(times)
-    return {"value": round(med * 1e6, 1), "unit": "us per call", "cores": 1, "kind": "port",
-            "sample": f"{len(times)} full calls of the 8B-shape 64-node attention on input set 0 "
-                      f"(numpy oracle restating respect/kernels/attention.py, one thread; median)"}
+    qn, kpn, vpn, knn, vnn = (t.numpy() for t in (q, kp, vp, kn, vn))
+    fold = []
+    with threadpool_limits(limits=1):
+        t_end = time.perf_counter() + budget_s / 2
+        while len(fold) < 3 and (time.perf_counter() < t_end or not fold):
+            t0 = time.perf_counter()
+            A.attn_hyb(qn, kpn, vpn, knn, vnn, msk.numpy(), wl.sm_scale)
+            fold.append(time.perf_counter() - t0)
+    return {"value": round(med * 1e6, 1), "unit": "us per call", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} full calls of the 8B-shape 64-node attention on input set 0: fp32 masked "
+                      f"SDPA in PyTorch on {threads} host threads (median)",
+            "literal_fold": {"value": round(statistics.median(fold) * 1e6, 1), "unit": "us per call", "cores": 1,
+                             "sample": f"{len(fold)} calls of the numpy logical-order fold of "
+                                       "respect/kernels/attention.py:36-71 (one thread; median)"}}
 
 
 def bench_attn(args) -> dict:
@@ -148,6 +188,37 @@ def traffic_probe(args) -> int:
     dst = torch.empty_like(src)
     dst.copy_(src)
     torch.cuda.synchronize()
+    return 0
+
+
+def counter_probe(args) -> int:
+    """Child run for rocprofv3 --pmc (MFMA counters): per dispatch, in this order, three
+    attention calls at 8B heads with a 3072-token prompt KV and tries of 16, 64 and 128
+    nodes, then the 64-row linear layers of one 8B decoder layer (q/k/v [6144, 4096],
+    o [4096, 4096], gate/up [24576, 4096], down [4096, 12288]) once each."""
+    import torch
+
+    from respect_amd import _lib
+    from respect_amd.kernels.attention import make_launcher
+    from respect_amd.workloads import AttnWorkload, merged_trie
+    for n, seqs, length, lo, hi in ((16, 2, 10, 4, 4), (64, 4, 24, 0, 16), (128, 5, 32, 8, 8)):
+        wl = AttnWorkload(P=3072, tree=merged_trie(7, seqs, length, lo, hi, n), sets=1, seed=n)
+        launch, _ = make_launcher(*wl.sets[0], wl.msk, wl.sm_scale)
+        launch()
+        torch.cuda.synchronize()
+        _log(f"counter probe: attention, {n} nodes")
+    L = _lib.lib()
+    dev = torch.device("cuda")
+    s = _lib.stream_ptr(dev)
+    x = torch.randn(64, 12288, device=dev).to(torch.bfloat16)
+    for N, K in ((6144, 4096), (4096, 4096), (24576, 4096), (4096, 12288)):
+        w = (0.02 * torch.randn(N, K, device=dev)).to(torch.bfloat16)
+        y = torch.empty(64, N, device=dev, dtype=torch.bfloat16)
+        ws = torch.zeros(max(16, L.rspx_linear_workspace_bytes(64, N, K)), dtype=torch.uint8, device=dev)
+        _lib.check("rspx_linear", L.rspx_linear(x.data_ptr(), 12288, w.data_ptr(), K, y.data_ptr(), N, 64, N, K, 0,
+                                                ws.data_ptr(), ws.numel(), s))
+        torch.cuda.synchronize()
+        _log(f"counter probe: linear 64 x [{N}, {K}]")
     return 0
 
 
@@ -356,6 +427,22 @@ def _target_trie(cont, rng, n_seqs=4, length=24, target_nodes=64, vocab=151936):
     return tree
 
 
+def _distractor_trie(first, target_next, rng, nodes=64, vocab=151936):
+    """``nodes`` nodes under the root ``first`` (sequences of 21 tokens, the last one cut to
+    fit), none of whose children carries ``target_next``."""
+    from respect_amd.candidates.trie import build_trie
+    seqs = []
+    while True:
+        s = [first] + [int(t) for t in rng.integers(0, vocab, 20)]
+        if s[1] == target_next:
+            s[1] = (target_next + 1) % vocab
+        have = len(build_trie(seqs).nodes) if seqs else 0
+        grown = build_trie(seqs + [s])
+        if len(grown.nodes) >= nodes:
+            return build_trie(seqs + [s[:nodes - have + (1 if seqs else 0)]])
+        seqs.append(s)
+
+
 def bench_decoder(args) -> dict:
     """One speculative verification step of a random-init 36-layer 8B-shape GQA
     decoder (hidden 4096, 32 q / 8 kv heads, head_dim 128, FFN 12288 SwiGLU,
@@ -363,7 +450,9 @@ def bench_decoder(args) -> dict:
     from random ids: a 64-node trie is verified in one forward, walked with the
     target's greedy choices, and the accepted path's KV compacted; then the
     same tokens are decoded one forward per token.  Tokens and committed KV
-    must match bitwise; committed tok/s = accepted tokens / verification time."""
+    must match bitwise; committed tok/s = accepted tokens / verification time.  The
+    same number of distractor-only steps (tries that never continue past their root:
+    one accepted token per step) is reported beside it."""
     import numpy as np
     import torch
 
@@ -401,7 +490,7 @@ def bench_decoder(args) -> dict:
     _log(f"decoder: {sum(len(v) for v in model._graphs.values())} forwards captured in {time.perf_counter() - t0:.1f} s")
     # Token-by-token greedy reference: the tokens the tries are built from.
     first = int(greedy_token(last).item())
-    n_ar = 24 * (steps + 1) + 1
+    n_ar = 24 * (steps + 1) + steps + 2
     G = [first]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -426,6 +515,20 @@ def bench_decoder(args) -> dict:
             nodes.append(len(tree.nodes))
         base += len(acc)
         nxt = rec
+    # Distractor-only tries: 64 nodes under the root whose children never carry the
+    # target's next token, so each step accepts one token (the worst case).
+    d_times, d_acc = [], 0
+    for step in range(steps):
+        tree = _distractor_trie(nxt, G[base + 1], rng)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        acc, rec, path = respect_step(model, sp, tree, nxt, P, base, eos=-1, graph=True)
+        torch.cuda.synchronize()
+        d_times.append(time.perf_counter() - t1)
+        ok &= acc == G[base:base + len(acc)] and rec == G[base + len(acc)]
+        d_acc += len(acc)
+        base += len(acc)
+        nxt = rec
     kv_equal = all(torch.equal(sp.k[i][:, P:P + base], ar.k[i][:, P:P + base]) and
                    torch.equal(sp.v[i][:, P:P + base], ar.v[i][:, P:P + base]) for i in range(cfg.layers))
     step_s = sum(times) / len(times)
@@ -436,6 +539,10 @@ def bench_decoder(args) -> dict:
             "steps": len(times), "trie_nodes": nodes, "ms_per_verify_step": round(step_s * 1e3, 3),
             "accepted_per_step": accepted / len(times),
             "committed_tok_s": round(accepted / sum(times), 1),
+            "distractor_only": {"steps": len(d_times), "accepted_per_step": d_acc / max(1, len(d_times)),
+                                "ms_per_verify_step": round(sum(d_times) / max(1, len(d_times)) * 1e3, 3),
+                                "committed_tok_s": round(d_acc / max(sum(d_times), 1e-9), 1),
+                                "trie": "64 nodes under the root, no child carries the target's next token"},
             "ar_ms_per_token": round(ar_ms, 3), "ar_tok_s": round(1e3 / ar_ms, 1),
             "weight_GBps_verify": round(wbytes / step_s / 1e9, 1),
             "tokens_equal_1token_decoding": bool(ok), "committed_kv_bitwise_equal": bool(kv_equal),
@@ -506,9 +613,13 @@ def main() -> int:
     ap.add_argument("--no-decoder", action="store_true", help="skip the 36-layer verification-step line")
     ap.add_argument("--decoder-steps", type=int, default=4, help="timed verification steps")
     ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--counter-probe", action="store_true",
+                    help="a few attention and linear-layer dispatches for rocprofv3 --pmc (MFMA counters)")
     args = ap.parse_args()
     if args.traffic_probe:
         return traffic_probe(args)
+    if args.counter_probe:
+        return counter_probe(args)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: the verification kernels run on a single MI355X "
