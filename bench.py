@@ -585,6 +585,36 @@ def bench_sweep(args) -> dict:
             "points": points}
 
 
+def bench_floor(args) -> dict:
+    """What the 8B-shape attention launch costs before any arithmetic (rspx_floor_launch):
+    its grid (256 x 512 threads, 147 KB LDS) empty; streaming each workgroup's K/V share
+    with every load in flight (196 KB per workgroup, each byte read by 4 row blocks, as the
+    attention reads it; and 49 KB unique shares); and the attention's own 2-round
+    direct-to-LDS load schedule without arithmetic.  32 rotating K/V sets (403 MB)."""
+    import ctypes
+
+    import torch
+
+    from respect_amd import _lib
+    L = _lib.lib()
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    sets = [(torch.randn(8, 3072, 128, generator=g, device=dev).to(torch.bfloat16),
+             torch.randn(8, 3072, 128, generator=g, device=dev).to(torch.bfloat16)) for _ in range(32)]
+    out = torch.zeros(256 * 512, dtype=torch.int32, device=dev)
+    s = _lib.stream_ptr(dev)
+    res = {}
+    for which, name in ((0, "empty_grid_us"), (1, "stream_196KB_per_wg_us"), (2, "stream_49KB_unique_us"),
+                        (3, "ring_schedule_us")):
+        ls = [_launcher(L.rspx_floor_launch, which, ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
+                        ctypes.c_void_p(out.data_ptr()), s) for k, v in sets]
+        res[name] = round(time_launches(ls, args.steps, args.warmup) * 1e3, 2)
+    res["workload"] = ("the attention's 8B-shape grid over K/V [8, 3072, 128] bf16: empty, streaming, "
+                       "and its own load schedule without arithmetic")
+    return res
+
+
 def bench_copy(args) -> dict:
     """Device-to-device copy of a 1 GiB bf16 buffer (torch's copy kernel): the
     measured HBM ceiling the kernels above are compared with, and the known-size
@@ -642,6 +672,8 @@ def main() -> int:
         _log("timing RMSNorm + q/k norm+RoPE and SwiGLU")
         res["extra"] = {"norm_rope": bench_norm_rope(args), "swiglu": bench_swiglu(args),
                         "copy": bench_copy(args)}
+        _log("timing the attention launch floor")
+        res["extra"]["attn_floor"] = bench_floor(args)
         _log("timing the Prefill / Flow element-wise kernels")
         res["extra"]["prefill"] = bench_prefill(args)
         _log("timing the attention sweep (prompt lengths x trie sizes)")

@@ -155,6 +155,16 @@ int rspx_trie_attn_noalloc(const void* q, int64_t sqh, int64_t sqm, const void* 
                            void* out, int64_t soh, int64_t som, int H, int HK, int M, int P, int NN, int D,
                            float sm_scale, int rows_per_wave, void* stream);
 
+/* Measurement kernels, no counterpart in the reference: the floor of the
+ * 8B-shape attention launch (256 workgroups x 512 threads, 147 KB LDS each)
+ * over K, V [8][3072][128] bf16 (out: >= 256 x 512 ints, never written in
+ * practice).  which: 0 empty grid; 1 every workgroup streams its 196 KB share
+ * of K/V (each byte read by 4 row blocks) with all loads in flight; 2 the same
+ * with 49 KB unique shares; 3 the attention's own 2-round direct-to-LDS load
+ * schedule without its arithmetic.
+ */
+int rspx_floor_launch(int which, const void* K, const void* V, void* out, void* stream);
+
 /* Test hook, no counterpart in the reference: sets how many times a one-launch
  * workgroup polls its row block's counter before its wait gives up (a
  * negative value restores the default, 2^22 polls); returns the previous
