@@ -155,6 +155,21 @@ int rspx_trie_attn_noalloc(const void* q, int64_t sqh, int64_t sqm, const void* 
                            void* out, int64_t soh, int64_t som, int H, int HK, int M, int P, int NN, int D,
                            float sm_scale, int rows_per_wave, void* stream);
 
+/* ---------------------------------------------------------------- tile-wise (blocked) attention
+ * The negative control of the slot-layout experiment, replacing
+ * respect/kernels/reference_blocked.py:83 fused_attn(q, kp, vp, kn, vn, msk,
+ * sm_scale, BM, BN, ...): the same arguments as rspx_trie_attn (no
+ * workspace), but node slots reduced tile by tile (BN in {32, 64, 128}) like
+ * the prompt, one online-softmax update per tile, bf16 probabilities in every
+ * PV product -- so the result depends on where the node slots sit.  D in
+ * {64, 128}.  Output row stride and base 8-byte aligned.
+ */
+int rspx_blocked_attn(const void* q, int64_t sqh, int64_t sqm, const void* kp, int64_t skph, int64_t skpn,
+                      const void* vp, int64_t svph, int64_t svpn, const void* kn, int64_t sknh, int64_t sknn,
+                      const void* vn, int64_t svnh, int64_t svnn, const uint8_t* msk, int64_t smm, int64_t smn,
+                      void* out, int64_t soh, int64_t som, int H, int HK, int M, int P, int NN, int D, int BN,
+                      float sm_scale, void* stream);
+
 /* Measurement kernels, no counterpart in the reference: the floor of the
  * 8B-shape attention launch (256 workgroups x 512 threads, 147 KB LDS each)
  * over K, V [8][3072][128] bf16 (out: >= 256 x 512 ints, never written in

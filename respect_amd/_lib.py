@@ -47,6 +47,10 @@ SIGNATURES: dict[str, tuple] = {
     "rspx_trie_attn_status": (_i32, [_c_p, _i32, _i32, _i32, _i32, _i32, _c_p]),
     "rspx_trie_attn_set_spin_limit": (_i32, [_i32]),
     "rspx_floor_launch": (_i32, [_i32, _c_p, _c_p, _c_p, _c_p]),
+    "rspx_blocked_attn": (_i32, [
+        _c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _i64, _i64,
+        _c_p, _i64, _i64, _c_p, _i64, _i64,
+        _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _c_p]),
     "rspx_trie_attn_noalloc": (_i32, [
         _c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _i64, _i64,
         _c_p, _i64, _i64, _c_p, _i64, _i64,
