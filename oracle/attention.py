@@ -13,7 +13,8 @@ attn_exact    float64 masked softmax attention (the mathematical definition).
 attn_tree     the fixed reduction tree the HIP kernel computes (same semantics as
               attn_hyb, a different but equally fixed order): 32-key steps with a
               lazy base-2 reference maximum, four key quarters per group combined
-              at the group maximum, exact-maximum node sums in slot order, groups
+              at the group maximum, exact-maximum node sums over the row's allowed
+              slots in rank tiles of 32 on the MFMA (p as bf16 hi + lo), groups
               merged left to right, then the node partial.  The per-element
               parity target of the GPU kernel.
 
@@ -29,6 +30,8 @@ layout dependence); brute-force per-row fp64 recomputation on tiny inputs.
 attn_tree and attn_blocked: the same error bound against attn_exact and the
 same planted-slip checks (a dropped node segment, a wrong scale, a missing
 rescale, unscaled quarters), single key => v, equal scores => mean(v).
+_node_partial (attn_tree's node sums): l and acc against float64 sums within
+2^-15 relative, where dropping the lo half of p fails.
 
 Test infrastructure only: the product never imports this package.
 """
@@ -174,6 +177,7 @@ def attn_error_bound(q, kp, vp, kn, vn, msk, sm_scale=None, node_p_bf16: bool = 
     rounding of the output):
 
         2^-9 * sum_prompt p_i |v_i| / sum_all p_i     (bf16 p: relative error <= 2^-9)
+      + 2^-15 * sum_node p_i |v_i| / sum_all p_i      (node p as bf16 hi + lo: <= 2^-16)
       + 2^-20 * sum_all p_i |v_i| / sum_all p_i       (fp32 accumulation and exp)
       + 1 bf16 ulp of the exact value                 (final rounding, with margin)
 
@@ -195,9 +199,10 @@ def attn_error_bound(q, kp, vp, kn, vn, msk, sm_scale=None, node_p_bf16: bool = 
     Pb = e.shape[-1] if node_p_bf16 else P
     wv_prompt = np.einsum("hmn,hnd->hmd", e[..., :Pb], V[:, :Pb]) / l
     wv_all = np.einsum("hmn,hnd->hmd", e, V) / l
+    wv_node = np.einsum("hmn,hnd->hmd", e[..., P:], V[:, P:]) / l
     exact = attn_exact(q, kp, vp, kn, vn, msk, sm_scale)
     from .bf16 import ulp
-    return 2.0 ** -9 * wv_prompt + 2.0 ** -20 * wv_all + ulp(exact)
+    return 2.0 ** -9 * wv_prompt + 2.0 ** -15 * wv_node + 2.0 ** -20 * wv_all + ulp(exact)
 
 
 # ---------------------------------------------------------------- the kernel's own tree
@@ -206,6 +211,7 @@ LOG2E = 1.4426950408889634
 KSTEP = 32        # keys per online-softmax step
 QUARTERS = 4      # key quarters (waves) per group
 GROUPS_MAX = 8    # key groups per kv head
+NODE_TILE = 32    # node ranks per MFMA tile
 LAZY_TAU = 8.0    # log2 headroom before a quarter's reference maximum moves
 
 
@@ -292,6 +298,35 @@ def _lane_sum32(p: np.ndarray) -> np.ndarray:
     return _f32(_f32(lanes[0] + lanes[1]) + _f32(lanes[2] + lanes[3]))
 
 
+def _node_partial(s: np.ndarray, v: np.ndarray, exp2=_exp2, hi_only: bool = False):
+    """Node partial (m, l, acc) of scores s [.., n] (fp32, scale and log2 e applied) and
+    values v [.., n, D] in rank order (n >= 1): m = max(s); p = 2^(s - m) in fp32 split
+    as hi = bf16(p), lo = bf16(p - hi); ranks in tiles of NODE_TILE, the last padded with
+    p = 0, v = 0; per tile acc <- MFMA(v, hi, acc) then MFMA(v, lo, acc), l likewise with
+    v = 1, k-slots in the prompt's PV order.  ``hi_only`` drops lo (a planted mistake)."""
+    lead, n = s.shape[:-1], s.shape[-1]
+    D = v.shape[-1]
+    m = s.max(axis=-1)
+    with np.errstate(invalid="ignore"):
+        p = exp2(_f32(s.astype(np.float64) - m[..., None]))
+    hi = round_bf16(p)
+    lo = np.zeros_like(hi) if hi_only else round_bf16(_f32(p.astype(np.float64) - hi))
+    T = -(-n // NODE_TILE)
+    pad = T * NODE_TILE - n
+    z = np.zeros(lead + (pad,), np.float32)
+    hi, lo = np.concatenate([hi, z], axis=-1), np.concatenate([lo, z], axis=-1)
+    V = np.concatenate([np.asarray(v, np.float32), np.zeros(lead + (pad, D), np.float32)], axis=-2)
+    ones = np.ones(lead + (NODE_TILE, 1), np.float32)
+    a = np.zeros(lead + (1, D), np.float32)
+    ll = np.zeros(lead + (1, 1), np.float32)
+    for t in range(T):
+        sl = slice(NODE_TILE * t, NODE_TILE * (t + 1))
+        for w in (hi, lo):
+            a = _mfma_acc(w[..., None, sl], V[..., sl, :], a, PV_KSLOTS)
+            ll = _mfma_acc(w[..., None, sl], ones, ll, PV_KSLOTS)
+    return m, ll[..., 0, 0], a[..., 0, :]
+
+
 def _combine(m, l, acc, m2, l2, acc2, exp2=_exp2):
     """(m, l, acc) <- (m, l, acc) (+) (m2, l2, acc2); an incoming m2 = -inf is left out."""
     skip = m2 == -np.inf
@@ -317,15 +352,20 @@ def attn_tree(q, kp, vp, kn, vn, msk, sm_scale=None, _plant: str | None = None, 
     group    S = 4 ceil(ceil(P/32) / 32) consecutive steps; quarters scaled by
              2^(m_k - M) (M their maximum, 0 for an empty quarter) and summed as
              (q0 + q1) + (q2 + q3).
-    node     s c over the row's allowed slots; m their exact maximum; p = 2^(s c - m)
-             in fp32; l and acc summed slot by slot in slot order (acc by fma).
+    node     s c over the row's allowed slots, taken in slot order (rank i = the
+             row's i-th allowed slot); m their exact maximum; p = 2^(s c - m) in fp32,
+             split as hi = bf16(p), lo = bf16(p - hi); ranks cut into tiles of 32 (the
+             last one padded with p = 0, v = 0); per tile, in tile order,
+             acc <- MFMA(v, hi, acc) then MFMA(v, lo, acc), and l likewise with v = 1
+             (the PV k-slot order of the prompt steps, rank in place of key).
     final    groups left to right, then the node partial; out = bf16(acc / l).
 
     ``_plant`` plants a mistake for the oracle's own tests: "no_rescale" (a moved
     reference maximum does not rescale l and acc), "flat_quarters" (quarters summed
-    without their 2^(m_k - M) factors).  ``exp2``: the fp32 2^x to use (default:
-    correctly rounded); a test may pass the values of another implementation to take
-    exp2's last-ulp rounding out of a comparison.
+    without their 2^(m_k - M) factors), "node_p_hi_only" (node p without its lo
+    part).  ``exp2``: the fp32 2^x to use (default: correctly rounded); a test may pass
+    the values of another implementation to take exp2's last-ulp rounding out of a
+    comparison.
     """
     ex = _exp2 if exp2 is None else exp2
     q = np.asarray(q, np.float32)
@@ -396,21 +436,14 @@ def attn_tree(q, kp, vp, kn, vn, msk, sm_scale=None, _plant: str | None = None, 
 
     if NN:
         sn = _f32(_chain_scores(q, KN).astype(np.float64) * c)      # [H, M, NN]
-        allow = np.broadcast_to(msk[None], sn.shape)
-        sm = np.where(allow, sn, ninf)
-        m = sm.max(axis=2)
-        with np.errstate(invalid="ignore"):
-            p = np.where(allow, ex(_f32(sm.astype(np.float64) - m[..., None])), np.float32(0))
+        m = np.full((H, M), ninf, np.float32)
         l = np.zeros((H, M), np.float32)
         acc = np.zeros((H, M, D), np.float32)
-        for j in range(NN):
-            on = allow[..., j]
-            if not on.any():
-                continue
-            pj = p[..., j]
-            l = np.where(on, _f32(l + pj), l)
-            accj = _f32(pj[..., None].astype(np.float64) * VN[:, None, j, :] + acc)
-            acc = np.where(on[..., None], accj, acc)
+        for mq in range(M):
+            idx = np.nonzero(msk[mq])[0]            # the row's allowed slots: rank order
+            if len(idx):
+                m[:, mq], l[:, mq], acc[:, mq] = _node_partial(sn[:, mq, idx], VN[:, idx], ex,
+                                                               hi_only=_plant == "node_p_hi_only")
         fm, fl, facc = _combine(fm, fl, facc, m, l, acc, ex)
 
     with np.errstate(invalid="ignore", divide="ignore"):

@@ -588,43 +588,46 @@ __global__ __launch_bounds__(512) void prompt_kernel(TrieAttnArgs A) {
 }
 
 // ------------------------------------------------------------------ node partials and merge
-template <int DN> struct NodeVec;
-template <> struct NodeVec<8> { typedef u32x4 T; };
-template <> struct NodeVec<4> { typedef u32x2 T; };
+constexpr int kChunk = 64;       // node slots staged in LDS at a time
+constexpr int kNodeTile = 32;    // ranks per MFMA tile of the node sums
+constexpr int kNodeRows = 16;    // rows of one node_rows call (at most one MFMA tile of columns)
+constexpr int kNodeRes = 3;      // chunks a resident node segment holds
+constexpr int kRankTab = 128;    // entries of a wave's rolling rank -> slot table
+constexpr int kStageSlots = 6;   // waves with a double-buffered V stage when streaming
+static_assert(kMaxNodeSlots % kChunk == 0, "whole mask words");
 
-constexpr int kChunk = 64;  // node slots staged in LDS at a time
-
-// Node LDS: kResident buffers of a chunk's K as score fragments -- 1 KB per
-// 16-slot tile kt and 32-wide head_dim step i, lane (n16, g4)'s 16 bytes are
-// K[16 kt + n16][32 i + 8 g4, +8), read back with one ds_read_b128 -- then as
-// many of V rows, then the fp32 scores of up to kMaxNodeRows rows x kChunk
-// slots, then the node partials of those rows.  Streaming uses buffer 0; a
-// prefetched segment of up to kResident chunks sits in buffers 0, 1, ...
-// The scores of a whole prefetched segment (rows x kResident kChunk slots,
-// row stride SROW2) go to S2OFF: the node-partial rows themselves when they
-// are as wide (D = 128; a row's scores are read before its partial is
-// written), else an area of their own.
-constexpr int kMaxNodeRows = 64;  // a workgroup's node rows: at most one prompt row block
-constexpr int kResident = 2;  // node chunks a prefetching caller keeps in LDS at once
-// RES resident chunks for at most ROWS node rows (RES 3 fits beside 16 rows).
-template <int D, int RES = kResident, int ROWS = kMaxNodeRows> struct NodeLds {
-  static constexpr int DIM = D, kRes = RES, kRows = ROWS;
-  static constexpr int KBYTES = kChunk * 2 * D;   // one chunk's K
-  static constexpr int VBYTES = kChunk * 2 * D;   // one chunk's V
-  static constexpr int VOFF = RES * KBYTES;
-  static constexpr int SOFF = VOFF + RES * VBYTES;
-  static constexpr int SROW = kChunk + 4;  // floats per score row
-  static constexpr int NPOFF = SOFF + ROWS * SROW * 4;
-  static constexpr int NPROW = D + 4;      // node partial of a row: m, l, pad, pad, acc[D]
-  static constexpr int NPEND = NPOFF + ROWS * NPROW * 4;
-  static constexpr int SROW2 = RES * kChunk + 4;  // floats per row of a whole segment's scores
-  static constexpr int S2OFF = NPROW == SROW2 ? NPOFF : NPEND;
-  static constexpr int BYTES = NPROW == SROW2 ? NPEND : NPEND + ROWS * SROW2 * 4;
-  static __device__ __forceinline__ lds_char* kbuf(lds_char* kv, int b) { return kv + b * KBYTES; }
-  static __device__ __forceinline__ lds_char* vbuf(lds_char* kv, int b) { return kv + VOFF + b * VBYTES; }
+// Node LDS, for at most kNodeRows rows:
+//   KB   kNodeRes chunks of K as score fragments -- 1 KB per 16-slot tile kt and
+//        32-wide head_dim step i; lane (n16, g4)'s 16 bytes are K[16 kt + n16][32 i +
+//        8 g4, +8), one ds_read_b128;
+//   VB   kNodeRes chunks of V rows, 2 D bytes per slot; 16-byte unit u of row r holds
+//        the row's unit u ^ vswz(r), so the transposing reads of four rows hit
+//        distinct banks.  When the segment streams, KB and VB hold instead
+//        kStageSlots double-buffered V stages of kNodeTile rows (same row layout);
+//   S    fp32 scores (times c) of the rows x the resident slots (or one chunk);
+//   NP   the node partial of each row: m, l, pad, pad, acc[D];
+//   MW   per group of rows, the 64-bit allowed-slot mask word of every chunk;
+//   TAB  per wave, kRankTab int16: the slot of rank r at r % kRankTab;
+//   Z    2 D bytes of zeros (the V row of a rank past the row's allowed count);
+//   CNT  per group, the number of allowed slots.
+template <int D> struct NodeLds {
+  static constexpr int CB = kChunk * 2 * D;   // one chunk's K (or V)
+  static constexpr int KOFF = 0;
+  static constexpr int VOFF = kNodeRes * CB;
+  static constexpr int STAGE = 2 * kNodeTile * 2 * D;   // one wave's double-buffered V stage
+  static_assert(kStageSlots * STAGE <= 2 * kNodeRes * CB, "stages fit KB + VB");
+  static constexpr int SR = kNodeRes * kChunk + 4;      // floats per score row
+  static constexpr int SOFF = 2 * kNodeRes * CB;
+  static constexpr int NPROW = D + 4;
+  static constexpr int NPOFF = SOFF + kNodeRows * SR * 4;
+  static constexpr int MWOFF = NPOFF + kNodeRows * NPROW * 4;
+  static constexpr int TOFF = MWOFF + kNodeRows * (kMaxNodeSlots / kChunk) * 8;
+  static constexpr int ZOFF = TOFF + kWavesA * kRankTab * 2;
+  static constexpr int CNTOFF = ZOFF + 2 * D;
+  static constexpr int BYTES = CNTOFF + kNodeRows * 4;
+  static __device__ __forceinline__ lds_char* kbuf(lds_char* kv, int b) { return kv + KOFF + b * CB; }
+  static __device__ __forceinline__ lds_char* vbuf(lds_char* kv, int b) { return kv + VOFF + b * CB; }
 };
-template <int D> using NodeLds3 = NodeLds<D, 3, 16>;  // three resident chunks, at most 16 rows
-constexpr int kMaxRounds = kMaxNodeRows / kWavesA;  // node rows per wave
 
 // Where a row's result goes: row r of kv head g is query r / GQA of head
 // g GQA + r % GQA.  Rows past R shadow a valid row and are never stored.
@@ -642,56 +645,59 @@ __device__ __forceinline__ RowRef row_ref(const TrieAttnArgs& A, int g, int r, i
 }
 
 typedef __attribute__((address_space(3))) float lds_float;
+typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) int16_t lds_i16;
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
 
-// Loads a caller may issue ahead of node_rows for a node segment of at most
-// kResident chunks: every chunk's K/V in LDS, the score fragment of the wave's
-// first task and the mask bytes of the wave's rows.
-template <int D, int RES = kResident> struct NodePre {
-  static_assert(RES == 2 || RES == 3, "two or three resident chunks");
+constexpr int kNodeRounds = kNodeRows / kWavesA;  // rows per wave in one node_rows call
+
+// Loads a caller may issue ahead of node_rows for a resident node segment (at
+// most kNodeRes chunks): every chunk's K/V in LDS, the score fragment of the
+// wave's first task and the mask bytes of the wave's rows.
+template <int D> struct NodePre {
   bf16x8 qf[D / 32];
   // Mask words of chunks 0, 1, 2 (byte i: the mask byte of round i), named
   // scalars read with constant indices only: a run-time choice between them
   // can fold into one indexed load, which puts the whole struct in scratch.
-  uint64_t mb0 = 0, mb1 = 0, mb2 = 0;
+  uint32_t mb0 = 0, mb1 = 0, mb2 = 0;
 };
-static_assert(kMaxRounds <= 8, "mask bytes of every round in one 64-bit word");
-
-// Mask bytes of the wave's rounds for chunk c0, byte i for row p0 + w + 8 i.
-__device__ __forceinline__ uint64_t node_masks(const TrieAttnArgs& A, int p0, int nrd, int w, int c0);
+static_assert(kNodeRounds <= 4, "mask bytes of every round in one 32-bit word");
 
 // Chunk c0 of kv head g's node K (score fragments) and, if `withv`, V rows
-// into LDS buffer b: 1 KB pieces x = w, w + nw, ...  Slots past NN read zeros.
-template <int D, class LY = NodeLds<D>>
+// (16-byte units swizzled by row) into LDS buffer b: 1 KB pieces x = w, w + nw,
+// ...  Slots past NN read zeros.
+template <int D>
 __device__ __forceinline__ void node_issue(const TrieAttnArgs& A, int g, int c0, lds_char* kv, int b, int w,
                                            int nw, bool withv) {
+  using LY = NodeLds<D>;
   constexpr int DQ = D / 32, RB = 2 * D;
-  constexpr int KX = LY::KBYTES / 1024, VX = LY::VBYTES / 1024;
+  constexpr int KX = LY::CB / 1024;
   const int lane = __lane_id();
   const int left = A.NN - c0 - 1;
   const __amdgpu_buffer_rsrc_t rk =
       buffer_rsrc(A.kn + (g * A.sknh + c0 * A.sknn), 2 * (left * A.sknn + D));
   const __amdgpu_buffer_rsrc_t rv =
       buffer_rsrc(A.vn + (g * A.svnh + c0 * A.svnn), 2 * (left * A.svnn + D));
-  const int nx = withv ? KX + VX : KX;
+  const int nx = withv ? 2 * KX : KX;
   for (int x = w; x < nx; x += nw) {
     if (x < KX) {
       const int slot = 16 * (x / DQ) + (lane & 15);
       bdma16(rk, 2 * (slot * A.sknn + 32 * (x % DQ) + 8 * (lane >> 4)), LY::kbuf(kv, b) + x * 1024);
     } else {
       const int byte = (x - KX) * 1024 + 16 * lane;
-      bdma16(rv, 2 * (byte / RB) * A.svnn + byte % RB, LY::vbuf(kv, b) + (x - KX) * 1024);
+      const int row = byte / RB, u = (byte % RB) / 16;
+      bdma16(rv, 2 * row * A.svnn + 16 * (u ^ vswz<D>(row)), LY::vbuf(kv, b) + (x - KX) * 1024);
     }
   }
 }
 
-// Score fragment of row tile rt of the rows starting at p0: lane (n16, g4)
-// holds head_dim [32 i + 8 g4, +8) of row p0 + 16 rt + n16 (rows at or past
-// rend shadow row p0).
+// Score fragment of the rows starting at p0: lane (n16, g4) holds head_dim
+// [32 i + 8 g4, +8) of row p0 + n16 (rows at or past rend shadow row p0).
 template <int D>
-__device__ __forceinline__ void node_q(const TrieAttnArgs& A, int g, int p0, int rend, int rt,
-                                       bf16x8 (&qf)[D / 32]) {
+__device__ __forceinline__ void node_q(const TrieAttnArgs& A, int g, int p0, int rend, bf16x8 (&qf)[D / 32]) {
   const int lane = __lane_id();
-  const int r = p0 + 16 * rt + (lane & 15);
+  const int r = p0 + (lane & 15);
   const RowRef R = row_ref(A, g, r < rend ? r : p0, p0);
   const uint16_t* qp = A.q + (R.hd * A.sqh + R.mq * A.sqm + 8 * (lane >> 4));
 #pragma unroll
@@ -704,49 +710,35 @@ __device__ __forceinline__ uint8_t node_mask(const TrieAttnArgs& A, int r, int c
   return t < A.NN ? A.msk[(r >> A.GQS) * A.smm + t * A.smn] : (uint8_t)0;
 }
 
-__device__ __forceinline__ uint64_t node_masks(const TrieAttnArgs& A, int p0, int nrd, int w, int c0) {
-  uint64_t mb = 0;
+// Mask bytes of the wave's rounds for chunk c0: byte i for row p0 + w + 8 i.
+__device__ __forceinline__ uint32_t node_masks(const TrieAttnArgs& A, int p0, int nrd, int w, int c0) {
+  uint32_t mb = 0;
 #pragma unroll
-  for (int i = 0; i < kMaxRounds; ++i)
-    if (i < nrd) mb |= (uint64_t)node_mask(A, p0 + w + kWavesA * i, c0) << (8 * i);
+  for (int i = 0; i < kNodeRounds; ++i)
+    if (i < nrd) mb |= (uint32_t)node_mask(A, p0 + w + kWavesA * i, c0) << (8 * i);
   return mb;
 }
 
-// Scores q.k times A.c of rows [p0, rend) (at most kMaxNodeRows) and chunk
-// c0's slots into S ([row - p0][SR], fp32) with one 16x16x32 MFMA chain per
-// task (row tile rt, slot tile kt); waves take tasks w, w + nw, ...  With
-// use_pre, `qpre` is the fragment of task w.  Each score depends only on its
-// row's q and its slot's k: neither the tile nor the lane position changes
-// its bits.
-template <int D, int SR = NodeLds<D>::SROW>
-__device__ __forceinline__ void node_scores(const TrieAttnArgs& A, int g, int p0, int rend, int c0,
-                                            const lds_char* kv, lds_float* S, int w, int nw,
-                                            const bf16x8 (&qpre)[D / 32], bool use_pre) {
+// Scores q.k times A.c of rows [p0, rend) (at most kNodeRows) and chunk c0's
+// slots into S ([row - p0][SR], fp32): one 16x16x32 MFMA chain per 16-slot
+// tile, waves 0..3 one tile each; qf is the score fragment of rows p0 + n16.
+// Each score depends only on its row's q and its slot's k (the chain over
+// head_dim is the same in every tile and lane): no position changes its bits.
+template <int D, int SR>
+__device__ __forceinline__ void node_scores(const TrieAttnArgs& A, int c0, const lds_char* kb, lds_float* S, int w,
+                                            const bf16x8 (&qf)[D / 32]) {
   constexpr int DQ = D / 32;
   const int lane = __lane_id();
-  const int nrt = (rend - p0 + 15) / 16;
-  const int nkt = min(kChunk, A.NN - c0 + 15) / 16;
-  for (int t = w; t < 4 * nrt; t += nw) {
-    const int rt = t >> 2, kt = t & 3;
-    if (kt >= nkt) continue;
-    bf16x8 qf[DQ];
-    if (use_pre && t == w) {
+  const int kt = w;
+  if (kt >= 4 || 16 * kt >= A.NN - c0) return;
+  f32x4 sv = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < DQ; ++i) qf[i] = qpre[i];
-    } else {
-      node_q<D>(A, g, p0, rend, rt, qf);
-    }
-    f32x4 sv = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < DQ; ++i) {
-      const bf16x8 a = *(const __attribute__((address_space(3))) bf16x8*)(kv + (kt * DQ + i) * 1024 + 16 * lane);
-      sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[i], sv, 0, 0, 0);
-    }
-    // Lane (n16, g4), element j: slot 16 kt + 4 g4 + j of row p0 + 16 rt + n16.
-    const f32x4 o = sv * A.c;
-    *(__attribute__((address_space(3))) f32x4*)(S + (16 * rt + (lane & 15)) * SR + 16 * kt +
-                                                4 * (lane >> 4)) = o;
+  for (int i = 0; i < DQ; ++i) {
+    const bf16x8 a = *(const __attribute__((address_space(3))) bf16x8*)(kb + (kt * DQ + i) * 1024 + 16 * lane);
+    sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[i], sv, 0, 0, 0);
   }
+  // Lane (n16, g4), element j: slot 16 kt + 4 g4 + j of row p0 + n16.
+  *(lds_f32x4*)(S + (lane & 15) * SR + 16 * kt + 4 * (lane >> 4)) = sv * A.c;
 }
 
 __device__ __forceinline__ float max64(float x) {
@@ -757,231 +749,316 @@ __device__ __forceinline__ float max64(float x) {
   return rows4_max(x);
 }
 
-// Node lane vector: head_dim [DL l, +DL) of a row held by lane l.
-template <int DL> struct NodeLane;
-template <> struct NodeLane<2> {
-  typedef uint32_t T;
-  static __device__ __forceinline__ float at(T v, int k) { return k == 0 ? bf16_lo(v) : bf16_hi(v); }
-};
-template <> struct NodeLane<1> {
-  typedef uint16_t T;
-  static __device__ __forceinline__ float at(T v, int) { return __uint_as_float((uint32_t)v << 16); }
-};
+__device__ __forceinline__ int lanes_below(uint64_t mm) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mm, 0));
+}
+__device__ __forceinline__ uint64_t lds_u64_uniform(const lds_char* p) {
+  const u32x2 v = *(const __attribute__((address_space(3))) u32x2*)p;
+  return ((uint64_t)__builtin_amdgcn_readfirstlane(v[1]) << 32) | (uint32_t)__builtin_amdgcn_readfirstlane(v[0]);
+}
 
-// l += p_j and acc += p_j v_j over the slots j of `mm` (bit j = slot j of the
-// chunk) in increasing order, one slot at a time: p_j is lane j's `p`, v_j the
-// chunk's V row j at vl (this lane's head_dim [DL lane, +DL)).
-template <int D>
-__device__ __forceinline__ void node_accumulate(uint64_t mm, float p, const lds_char* vl, float& l,
-                                                float (&acc)[D / 64]) {
-  constexpr int DL = D / 64;
-  constexpr int RB = 2 * D;                          // bytes per node row
-  constexpr int kB = 8;                              // slots per batch
-  typedef NodeLane<DL> NL;
-  typedef typename NL::T LaneT;
-  while (mm != 0) {
-    int js[kB];
-    bool on[kB];
-#pragma unroll
-    for (int u = 0; u < kB; ++u) {
-      on[u] = mm != 0;
-      js[u] = on[u] ? __builtin_ctzll(mm) : 0;
-      mm &= mm - 1;
-    }
-    LaneT vr[kB];
-    float pu[kB];
-#pragma unroll
-    for (int u = 0; u < kB; ++u) {
-      vr[u] = *(const __attribute__((address_space(3))) LaneT*)(vl + js[u] * RB);
-      pu[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), js[u]));
-    }
-#pragma unroll
-    for (int u = 0; u < kB; ++u) {
-      if (on[u]) {
-        l += pu[u];
-#pragma unroll
-        for (int k = 0; k < DL; ++k) acc[k] = __builtin_fmaf(pu[u], NL::at(vr[u], k), acc[k]);
-      }
-    }
+// The rank -> slot table of one wave for one group: mask words are consumed in
+// slot order, each allowed slot written at its rank % kRankTab, until the ranks
+// below `upto` are all in the table (or the words run out).  Entries of ranks in
+// [upto - 64, upto + 63] never alias each other.
+// rc: next mask word, rbase: ranks before word rc (wave-uniform).
+__device__ __forceinline__ void rank_fill(int& rc, int& rbase, int upto, int nch, const lds_char* mw, lds_i16* tab) {
+  const int lane = __lane_id();
+  while (rbase < upto && rc < nch) {
+    const uint64_t mm = lds_u64_uniform(mw + 8 * rc);
+    if ((mm >> lane) & 1) tab[(rbase + lanes_below(mm)) & (kRankTab - 1)] = (int16_t)(kChunk * rc + lane);
+    rbase += __builtin_popcountll(mm);
+    ++rc;
   }
 }
 
-// Node partials of rows [p0, rend) of kv head g (at most kMaxNodeRows) over
-// each row's allowed node slots (attention.py:52-67): m is the maximum score
-// over every allowed slot, p = exp2(score - m) in fp32, and l and acc are sums
-// over the allowed slots taken one at a time in slot order -- every bit
-// depends only on the ordered list of the row's allowed (k, v), not on where
-// in the node area they sit.  Every wave of the workgroup (kWavesA of them,
-// this is wave w) calls it; row p0 + w + 8 i is wave w's round i, and its
-// partial (m, l, acc) is left in the node-partial area of LDS (row i * 8 + w)
-// for the same wave to read.  With more than one chunk a first pass over K
-// finds m -- except for a prefetched segment of more than one chunk, whose
-// scores are all taken at once (one pass: the same m, p and sums).
-// have_pre: the caller issued a segment of at most kResident chunks
-// (chunk c into buffer c) and `pre` (node_prefetch), has since waited for them
-// (vmcnt 0) and passed a workgroup barrier; otherwise chunks stream through
-// buffer 0.  Does nothing when NN = 0.  Ends with every
-// vector load of the calling wave complete.
-template <int D, class LY = NodeLds<D>>
+// The node sums of one group of rows (the rows of query mq among [p0, rend);
+// MFMA column n16 is row p0 + n16, whose score fragment is qf, and columns of
+// rows outside the group carry p = 0) over d-tiles [NJ sl, NJ sl + NJ) of head_dim,
+// and l when sl = 0.  Ranks in tiles of kNodeTile: per tile, S^T = K Q^T for the
+// tile's slots (the same chain as node_scores), p = 2^(s - m) in fp32 for ranks
+// below the group's allowed count n (0 past it), hi = bf16(p), lo = bf16(p - hi),
+// then acc <- MFMA(V^T, hi, acc), acc <- MFMA(V^T, lo, acc), l likewise with
+// V = 1 -- k-slot 8 g4 + i of the B operand is rank 4 g4 + i (i < 4) or
+// 16 + 4 g4 + i - 4, as the prompt's PV product.  RES: K fragments and V rows
+// are gathered from the resident chunks by slot; otherwise K comes straight from
+// memory and each tile's V rows are copied by rank into this wave's stage.
+template <int D, bool RES, int NJ>
+__device__ __forceinline__ void node_task(const TrieAttnArgs& A, int g, int p0, int rend, int mq, int gl, int sl,
+                                          lds_char* kv, int w, int nch, const bf16x8 (&qf)[D / 32]) {
+  using LY = NodeLds<D>;
+  constexpr int DQ = D / 32, RB = 2 * D;
+  const int lane = __lane_id();
+  const int n16 = lane & 15, g4 = lane >> 4, e4 = n16 >> 2, c4 = n16 & 3;
+  const int row = p0 + n16;                            // column n16: row p0 + n16 (qf's rows)
+  const bool col = row < rend && (row >> A.GQS) == mq;
+  const int rl = col ? n16 : 0;                        // its local row
+  lds_float* NP = (lds_float*)(kv + LY::NPOFF);
+  const lds_char* mw = kv + LY::MWOFF + gl * (kMaxNodeSlots / kChunk) * 8;
+  lds_i16* tab = (lds_i16*)(kv + LY::TOFF) + w * kRankTab;
+  const lds_char* zrow = kv + LY::ZOFF;
+  const int n = __builtin_amdgcn_readfirstlane(*(const lds_u32*)(kv + LY::CNTOFF + 4 * gl));
+  const float mcol = NP[rl * LY::NPROW];
+
+  const __amdgpu_buffer_rsrc_t rk =
+      buffer_rsrc(A.kn + g * A.sknh, 2 * ((A.NN - 1) * A.sknn + D));
+  const __amdgpu_buffer_rsrc_t rv =
+      buffer_rsrc(A.vn + g * A.svnh, 2 * ((A.NN - 1) * A.svnn + D));
+  lds_char* stage = kv + LY::KOFF + w * LY::STAGE;
+
+  const uint32_t one2 = 0x3f803f80u;   // two bf16 1.0
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{one2, one2, one2, one2});
+  f32x4 acc[NJ], lacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int jj = 0; jj < NJ; ++jj) acc[jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  int rc = 0, rbase = 0;
+  const int ntile = (n + kNodeTile - 1) / kNodeTile;
+  for (int t = 0; t < ntile; ++t) {
+    const int r0 = kNodeTile * t;
+    rank_fill(rc, rbase, r0 + kNodeTile, nch, mw, tab);
+    // K fragments of the tile's two 16-rank blocks: lane (n16, g4) rank r0 + 16 kb + n16.
+    u32x4 kf[2][DQ];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int rk_ = r0 + 16 * kb + n16;
+      const int s = rk_ < n ? tab[rk_ & (kRankTab - 1)] : 0;
+#pragma unroll
+      for (int i = 0; i < DQ; ++i) {
+        if constexpr (RES) {
+          const int ch = s >> 6, sc = s & 63;
+          kf[kb][i] = *(const lds_u32x4*)(LY::kbuf(kv, ch) + ((sc >> 4) * DQ + i) * 1024 + 16 * ((sc & 15) + 16 * g4));
+        } else {
+          kf[kb][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    rk, 2 * (s * A.sknn + 32 * i + 8 * g4), 0, 0));
+        }
+      }
+    }
+    // V rows of the tile's ranks: RES reads them in place; otherwise the 32 rows
+    // are copied by rank into the stage (rows past n read zeros).
+    const lds_char *vrow0, *vrow1;
+    int vsw0, vsw1;
+    if constexpr (RES) {
+      auto vsrc = [&](int kh, const lds_char*& vr, int& sw) {
+        const int rv_ = r0 + 16 * kh + 4 * g4 + e4;
+        const int s = rv_ < n ? tab[rv_ & (kRankTab - 1)] : -1;
+        vr = s >= 0 ? LY::vbuf(kv, s >> 6) + (s & 63) * RB : zrow;
+        sw = s >= 0 ? vswz<D>(s & 63) : 0;
+      };
+      vsrc(0, vrow0, vsw0);
+      vsrc(1, vrow1, vsw1);
+    } else {
+      lds_char* st = stage + (t & 1) * (kNodeTile * RB);
+#pragma unroll
+      for (int x = 0; x < kNodeTile * RB / 1024; ++x) {
+        const int byte = x * 1024 + 16 * lane;
+        const int rr = byte / RB, u = (byte % RB) / 16;
+        const int rv_ = r0 + rr;
+        const int s = rv_ < n ? tab[rv_ & (kRankTab - 1)] : -1;
+        bdma16(rv, s >= 0 ? 2 * s * A.svnn + 16 * (u ^ vswz<D>(rr)) : 0x7ffffff0, st + x * 1024);
+      }
+      const int rr0 = 4 * g4 + e4, rr1 = 16 + 4 * g4 + e4;
+      vrow0 = st + rr0 * RB;
+      vrow1 = st + rr1 * RB;
+      vsw0 = vswz<D>(rr0);
+      vsw1 = vswz<D>(rr1);
+      __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): K fragments and this wave's stage rows
+    }
+    // Scores, then p of ranks r0 + 16 kb + 4 g4 + j (the B operand's k-slots).
+    float pv[8];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      f32x4 sv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < DQ; ++i)
+        sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[kb][i]), qf[i], sv, 0, 0, 0);
+      const f32x4 s = sv * A.c;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool on = col && r0 + 16 * kb + 4 * g4 + j < n;
+        pv[4 * kb + j] = on ? fexp2(s[j] - mcol) : 0.f;
+      }
+    }
+    u32x4 hw, lw;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      hw[i] = pack_bf16x2(pv[2 * i], pv[2 * i + 1]);
+      lw[i] = pack_bf16x2(pv[2 * i] - bf16_lo(hw[i]), pv[2 * i + 1] - bf16_hi(hw[i]));
+    }
+    const bf16x8 hop = __builtin_bit_cast(bf16x8, hw), lop = __builtin_bit_cast(bf16x8, lw);
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) {
+      const int b = 2 * (NJ * sl + jj) + (c4 >> 1);
+      const s16x4 lo = lds_read_tr(vrow0 + 16 * (b ^ vsw0) + 8 * (c4 & 1));
+      const s16x4 hi = lds_read_tr(vrow1 + 16 * (b ^ vsw1) + 8 * (c4 & 1));
+      const bf16x8 vop = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, hop, acc[jj], 0, 0, 0);
+      acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, lop, acc[jj], 0, 0, 0);
+    }
+    if (sl == 0) {
+      lacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, hop, lacc, 0, 0, 0);
+      lacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, lop, lacc, 0, 0, 0);
+    }
+  }
+  // Lane (n16, g4) holds head_dim 16 j + 4 g4 + e of column n16.
+  if (col) {
+    lds_float* np = NP + rl * LY::NPROW;
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) *(lds_f32x4*)(np + 4 + 16 * (NJ * sl + jj) + 4 * g4) = acc[jj];
+    if (sl == 0 && g4 == 0) np[1] = lacc[0];
+  }
+}
+
+// Node partials of rows [p0, rend) of kv head g (at most kNodeRows) over each
+// row's allowed node slots (attention.py:52-67): m is the exact maximum score
+// over the allowed slots; the sums run over the allowed slots in slot order
+// (rank r = the r-th allowed slot), in MFMA tiles of kNodeTile ranks (node_task),
+// so every bit depends only on the ordered list of the row's allowed (k, v),
+// not on where in the node segment they sit.  Every wave of the workgroup
+// calls it; the partial (m, l, acc) of row p0 + i is left in the node-partial
+// area of LDS, row i, after the closing barrier.
+//   have_pre: the caller issued a resident segment (at most kNodeRes chunks,
+// chunk c into buffer c) and `pre` (node_prefetch), has since waited for those
+// loads (vmcnt 0) and passed a workgroup barrier.  A resident segment the
+// caller did not issue is loaded here; a longer one streams: its maxima come
+// from a pass over K chunk by chunk, its sums from K and V gathered by rank.
+template <int D>
 __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv, int w,
-                                          const NodePre<D, LY::kRes>& pre, bool have_pre) {
+                                          const NodePre<D>& pre, bool have_pre) {
+  using LY = NodeLds<D>;
   constexpr int nw = kWavesA;
-  constexpr int DL = D / 64;
+  constexpr int DT = D / 16;
   const int lane = __lane_id();
   const int NN = A.NN;
   if (NN == 0) return;
-  const int nrd = (rend - p0 - w + nw - 1) / nw;     // rounds of this wave
-  constexpr int RES = LY::kRes;
+  const int nrd = (rend - p0 - w + nw - 1) / nw;   // rows of this wave: p0 + w + 8 i
+  const int nch = (NN + kChunk - 1) / kChunk;
+  const bool res = NN <= kNodeRes * kChunk;
   lds_float* S = (lds_float*)(kv + LY::SOFF);
   lds_float* NP = (lds_float*)(kv + LY::NPOFF);
-  const bool one = NN <= kChunk;
-  const bool res = have_pre && NN <= RES * kChunk;  // every chunk already in buffer c
+  const int GQA = 1 << A.GQS;
+  const int q0 = p0 >> A.GQS;
+  const int ng = ((rend - 1) >> A.GQS) - q0 + 1;  // groups of rows (one query each)
+  bf16x8 qf[D / 32];                               // score fragment of rows p0 + n16
+  if (have_pre) {
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) qf[i] = pre.qf[i];
+  } else {
+    node_q<D>(A, g, p0, rend, qf);
+  }
 
-  if (res && !one) {
-    // Two or more resident chunks: every score at once, then per row the
-    // maximum over all its allowed slots and the sums over chunk 0's slots,
-    // then chunk 1's, ...
-    lds_float* S2 = (lds_float*)(kv + LY::S2OFF);
-    constexpr int SR2 = LY::SROW2;
-    static_assert(RES == 2 || RES == 3, "two or three resident chunks");
-    const int nch = (NN + kChunk - 1) / kChunk;
-    node_scores<D, SR2>(A, g, p0, rend, 0, LY::kbuf(kv, 0), S2, w, nw, pre.qf, true);
-    node_scores<D, SR2>(A, g, p0, rend, kChunk, LY::kbuf(kv, 1), S2 + kChunk, w, nw, pre.qf, true);
-    if (RES > 2 && nch > 2)
-      node_scores<D, SR2>(A, g, p0, rend, 2 * kChunk, LY::kbuf(kv, 2), S2 + 2 * kChunk, w, nw, pre.qf, true);
+  // Maxima, mask words, allowed counts.  The first row of each group in
+  // [p0, rend) records the group's mask words and count.
+  auto row_words = [&](int i, int c, uint32_t mb, float x) {
+    const int r = p0 + w + nw * i;
+    const bool lead = r == p0 || (r & (GQA - 1)) == 0;
+    const uint64_t mm = __builtin_amdgcn_ballot_w64(((mb >> (8 * i)) & 0xff) != 0);
+    if (lead && lane == 0) {
+      const int gl = (r >> A.GQS) - q0;
+      *(__attribute__((address_space(3))) uint64_t*)(kv + LY::MWOFF + (gl * (kMaxNodeSlots / kChunk) + c) * 8) = mm;
+      lds_u32* cnt = (lds_u32*)(kv + LY::CNTOFF + 4 * gl);
+      *cnt = (c == 0 ? 0u : *cnt) + (uint32_t)__builtin_popcountll(mm);
+    }
+    (void)x;
+  };
+  if (res) {
+    uint32_t mb[kNodeRes];
+    if (have_pre) {
+      mb[0] = pre.mb0;
+      mb[1] = pre.mb1;
+      mb[2] = pre.mb2;
+    } else {
+#pragma unroll
+      for (int c = 0; c < kNodeRes; ++c) {
+        mb[c] = 0;
+        if (c < nch) {
+          node_issue<D>(A, g, kChunk * c, kv, c, w, nw, true);
+          mb[c] = node_masks(A, p0, nrd, w, kChunk * c);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      lds_barrier();
+    }
+#pragma unroll
+    for (int c = 0; c < kNodeRes; ++c)
+      if (c < nch) node_scores<D, LY::SR>(A, kChunk * c, LY::kbuf(kv, c), S + kChunk * c, w, qf);
     lds_barrier();
 #pragma unroll 1
     for (int i = 0; i < nrd; ++i) {
       const int row = w + nw * i;
-      const lds_float* sr = S2 + row * SR2;
-      const uint64_t mws[3] = {pre.mb0, pre.mb1, pre.mb2};
-      float sc[RES];
-      bool ok[RES];
       float x = kNegInf;
 #pragma unroll
-      for (int c = 0; c < RES; ++c) {
-        ok[c] = c < nch && ((mws[c] >> (8 * i)) & 0xff) != 0;
-        sc[c] = c < nch ? sr[c * kChunk + lane] : 0.f;
-        x = fmaxf(x, ok[c] ? sc[c] : kNegInf);
+      for (int c = 0; c < kNodeRes; ++c) {
+        if (c < nch) {
+          const bool ok = ((mb[c] >> (8 * i)) & 0xff) != 0;
+          x = fmaxf(x, ok ? S[row * LY::SR + kChunk * c + lane] : kNegInf);
+          row_words(i, c, mb[c], x);
+        }
       }
       const float m = max64(x);
-      float l = 0.f, acc[DL];
-#pragma unroll
-      for (int k = 0; k < DL; ++k) acc[k] = 0.f;
-      // One call per chunk with constant indices (a loop around the inner
-      // while loop stays rolled and would index sc / ok at run time).
-      auto chunk = [&](int c, bool okc, float scc) {
-        if (c < nch) {
-          const float pc = okc ? fexp2(scc - m) : 0.f;
-          node_accumulate<D>(__builtin_amdgcn_ballot_w64(okc), pc, LY::vbuf(kv, c) + DL * 2 * lane, l, acc);
-        }
-      };
-      chunk(0, ok[0], sc[0]);
-      chunk(1, ok[1], sc[1]);
-      if constexpr (RES > 2) chunk(2, ok[2], sc[2]);
-      // The row's scores are in registers; its partial may now overwrite them.
-      lds_float* np = NP + row * LY::NPROW;
-      if (lane == 0) {
-        np[0] = m;
-        np[1] = l;
-      }
-#pragma unroll
-      for (int k = 0; k < DL; ++k) np[4 + DL * lane + k] = acc[k];
+      if (lane == 0) NP[row * LY::NPROW] = m;
     }
-    return;
-  }
-
-  if (!one) {
-    for (int c0 = 0; c0 < NN; c0 += kChunk) {
-      if (c0 > 0) lds_barrier();  // every wave is done with the previous chunk's scores
-      const int b = 0;            // more than one chunk: never resident here
-      uint64_t mb;
-      {
-        node_issue<D, LY>(A, g, c0, kv, 0, w, nw, false);
-        mb = node_masks(A, p0, nrd, w, c0);
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-        lds_barrier();
-      }
-      node_scores<D>(A, g, p0, rend, c0, LY::kbuf(kv, b), S, w, nw, pre.qf, res);
+  } else {
+    for (int c = 0; c < nch; ++c) {
+      if (c > 0) lds_barrier();  // every wave is done with the previous chunk's scores
+      node_issue<D>(A, g, kChunk * c, kv, 0, w, nw, false);
+      const uint32_t mb = node_masks(A, p0, nrd, w, kChunk * c);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      lds_barrier();
+      node_scores<D, LY::SR>(A, kChunk * c, LY::kbuf(kv, 0), S, w, qf);
       lds_barrier();
 #pragma unroll 1
-      for (int i = 0; i < kMaxRounds; ++i) {
-        if (i < nrd) {
-          const int row = w + nw * i;
-          const bool ok = ((mb >> (8 * i)) & 0xff) != 0;
-          const float x = max64(ok ? S[row * LY::SROW + lane] : kNegInf);
-          lds_float* np = NP + row * LY::NPROW;
-          if (lane == 0) np[0] = c0 == 0 ? x : fmaxf(np[0], x);
-        }
+      for (int i = 0; i < nrd; ++i) {
+        const int row = w + nw * i;
+        const bool ok = ((mb >> (8 * i)) & 0xff) != 0;
+        const float x = max64(ok ? S[row * LY::SR + lane] : kNegInf);
+        row_words(i, c, mb, x);
+        if (lane == 0) NP[row * LY::NPROW] = c == 0 ? x : fmaxf(NP[row * LY::NPROW], x);
       }
-    }
-    lds_barrier();
-  }
-
-  for (int c0 = 0; c0 < NN; c0 += kChunk) {
-    if (c0 > 0) lds_barrier();  // every wave is done with the previous chunk
-    const int b = 0;              // a resident segment here is one chunk, in buffer 0
-    uint64_t mb;
-    if (res) {
-      // The caller waited for its loads (vmcnt 0) before a workgroup barrier.
-      // No wait here: a store or atomic it issued since may still be in flight.
-      mb = pre.mb0;
-    } else {
-      node_issue<D, LY>(A, g, c0, kv, 0, w, nw, true);
-      mb = node_masks(A, p0, nrd, w, c0);
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of the chunk is in LDS
-      lds_barrier();                       // and every other wave's part
-    }
-    node_scores<D>(A, g, p0, rend, c0, LY::kbuf(kv, b), S, w, nw, pre.qf, res);
-    lds_barrier();
-    const lds_char* vl = LY::vbuf(kv, b) + DL * 2 * lane;
-
-#pragma unroll 1
-    for (int i = 0; i < nrd; ++i) {
-      const int row = w + nw * i;
-      const bool ok = ((mb >> (8 * i)) & 0xff) != 0;
-      const float s = S[row * LY::SROW + lane];
-      lds_float* np = NP + row * LY::NPROW;
-      const float m = one ? max64(ok ? s : kNegInf) : np[0];
-      const float p = ok ? fexp2(s - m) : 0.f;
-      const uint64_t mm = __builtin_amdgcn_ballot_w64(ok);  // wave-uniform: the row's allowed slots
-      float l = 0.f, acc[DL];
-#pragma unroll
-      for (int k = 0; k < DL; ++k) acc[k] = 0.f;
-      if (c0 > 0) {
-        l = np[1];
-#pragma unroll
-        for (int k = 0; k < DL; ++k) acc[k] = np[4 + DL * lane + k];
-      }
-      node_accumulate<D>(mm, p, vl, l, acc);
-      if (lane == 0) {
-        np[0] = m;
-        np[1] = l;
-      }
-#pragma unroll
-      for (int k = 0; k < DL; ++k) np[4 + DL * lane + k] = acc[k];
     }
   }
+  if (w == 0) {
+    // The zero V row (2 D bytes).
+    for (int b = 4 * lane; b < 2 * D; b += 256) *(lds_u32*)(kv + LY::ZOFF + b) = 0u;
+  }
+  lds_barrier();   // scores, maxima, mask words and counts visible; KB / VB free when streaming
+
+  if (res) {
+    // (group, d-slice) tasks over the waves, at most two per wave.
+    const int ds = ng >= 8 ? 1 : ng >= 4 ? 2 : ng >= 2 ? 4 : 8;
+    const int dsl = ds < DT ? ds : DT;
+    for (int task = w; task < ng * dsl; task += nw) {
+      const int gl = task / dsl, sl = task - gl * dsl;
+      const int nj = DT / dsl;
+      if (nj == DT) node_task<D, true, DT>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
+      else if (nj * 2 == DT) node_task<D, true, DT / 2>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
+      else if (nj * 4 == DT) node_task<D, true, DT / 4>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
+      else node_task<D, true, (DT >= 8 ? DT / 8 : 1)>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
+    }
+  } else if (w < kStageSlots) {
+    for (int gl = w; gl < ng; gl += kStageSlots) node_task<D, false, DT>(A, g, p0, rend, q0 + gl, gl, 0, kv, w, nch, qf);
+  }
+  lds_barrier();   // every row's partial is in NP
 }
 
-// Issues node_rows' loads for a segment of at most LY::kRes chunks
-// (0 < NN <= LY::kRes kChunk, p0 < rend): chunk c into buffer c.
-template <int D, class LY = NodeLds<D>>
+// Issues node_rows' loads of a resident segment (0 < NN <= kNodeRes kChunk,
+// p0 < rend): chunk c into buffer c, the mask bytes and the score fragment.
+template <int D>
 __device__ __forceinline__ void node_prefetch(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv, int w,
-                                              NodePre<D, LY::kRes>& pre) {
+                                              NodePre<D>& pre) {
   constexpr int nw = kWavesA;
   const int nrd = (rend - p0 - w + nw - 1) / nw;
   // One call per chunk with a constant index into pre.mb (a rolled loop
   // would index it at run time and put `pre` in scratch memory).
-  auto chunk = [&](int b) -> uint64_t {
+  auto chunk = [&](int b) -> uint32_t {
     if (b * kChunk >= A.NN) return 0;
-    node_issue<D, LY>(A, g, b * kChunk, kv, b, w, nw, true);
+    node_issue<D>(A, g, b * kChunk, kv, b, w, nw, true);
     return node_masks(A, p0, nrd, w, b * kChunk);
   };
   pre.mb0 = chunk(0);
   pre.mb1 = chunk(1);
-  if constexpr (LY::kRes > 2) pre.mb2 = chunk(2);
-  if (w < 4 * ((rend - p0 + 15) / 16)) node_q<D>(A, g, p0, rend, w >> 2, pre.qf);
+  pre.mb2 = chunk(2);
+  node_q<D>(A, g, p0, rend, pre.qf);
 }
 
 // Final result of row r of kv head g, one row over the wave (lane l: head_dim
@@ -1038,12 +1115,13 @@ __device__ __forceinline__ void merge_row(const TrieAttnArgs& A, int g, int r, f
 
 // The node partial of wave w's round i, left in LDS by node_rows (empty when
 // there are no node slots), merged into row p0 + w + 8 i.
-template <int D, bool COH, class LY = NodeLds<D>>
+template <int D, bool COH>
 __device__ __forceinline__ void merge_rounds(const TrieAttnArgs& A, int g, int p0, int rend, const lds_char* kv,
                                              int w) {
   constexpr int DL = D / 64;
   const int lane = __lane_id();
   const int nrd = (rend - p0 - w + kWavesA - 1) / kWavesA;
+  using LY = NodeLds<D>;
   const lds_float* NP = (const lds_float*)(kv + LY::NPOFF);
 #pragma unroll 1
   for (int i = 0; i < nrd; ++i) {
@@ -1064,27 +1142,27 @@ __device__ __forceinline__ void merge_rounds(const TrieAttnArgs& A, int g, int p
 
 // ------------------------------------------------------------------ kernel B
 // Workgroup (g, c8): rows [8 c8, 8 c8 + 8) of kv head g, row 8 c8 + w on
-// wave w: node partial, then merge.  A node segment of at most three chunks
-// is loaded whole up front (then taken in one pass); a longer one streams.
+// wave w: node partial, then merge.  A node segment of at most kNodeRes chunks
+// is loaded whole up front; a longer one streams.
 template <int D>
 __global__ __launch_bounds__(64 * kWavesA) void node_merge_kernel(TrieAttnArgs A) {
-  using LY = NodeLds3<D>;
-  static_assert(8 <= LY::kRows, "a workgroup's rows fit the node areas");
+  using LY = NodeLds<D>;
+  static_assert(8 <= kNodeRows, "a workgroup's rows fit the node areas");
   __shared__ __attribute__((aligned(16))) char kv[LY::BYTES];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int RC8 = (A.R + 7) / 8;
   const int g = blockIdx.x / RC8;
   const int p0 = 8 * (blockIdx.x - g * RC8);
   const int rend = min(p0 + 8, A.R);
-  NodePre<D, LY::kRes> pre;
-  const bool pf = A.NN > 0 && A.NN <= LY::kRes * kChunk;
+  NodePre<D> pre;
+  const bool pf = A.NN > 0 && A.NN <= kNodeRes * kChunk;
   if (pf) {
-    node_prefetch<D, LY>(A, g, p0, rend, (lds_char*)kv, w, pre);
+    node_prefetch<D>(A, g, p0, rend, (lds_char*)kv, w, pre);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of the segment is in LDS
     lds_barrier();                       // and every other wave's part
   }
-  node_rows<D, LY>(A, g, p0, rend, (lds_char*)kv, w, pre, pf);
-  merge_rounds<D, false, LY>(A, g, p0, rend, (const lds_char*)kv, w);
+  node_rows<D>(A, g, p0, rend, (lds_char*)kv, w, pre, pf);
+  merge_rounds<D, false>(A, g, p0, rend, (const lds_char*)kv, w);
 }
 
 // NaN in every element of rows [p0, rend) of kv head g (row p0 + w + 8 i on
@@ -1130,14 +1208,11 @@ constexpr int kSpinLimit = 1 << 22;
 static int g_spin_limit = kSpinLimit;
 constexpr int kSyncWords = 4096;   // timeout flag + [HK][NRB][2] counters
 
-// RES3: the node areas of NodeLds3 (three resident chunks), for grids whose
-// workgroups merge at most 16 rows each (fused_rows <= 16).
-template <int D, int kRT, bool RES3>
+template <int D, int kRT>
 __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
-  using LY = typename std::conditional<RES3, NodeLds3<D>, NodeLds<D>>::type;
+  using LY = NodeLds<D>;
   constexpr int LB = PromptLds<D, kRT>::BYTES > LY::BYTES + 16 ? PromptLds<D, kRT>::BYTES : LY::BYTES + 16;
   static_assert(LY::BYTES + 16 <= PromptLds<D, kRT>::RINGBYTES, "node LDS and the wait flag inside the ring");
-  static_assert(RES3 || 32 * kRT <= LY::kRows, "a row block fits the node areas");
   __shared__ __attribute__((aligned(16))) char lds[LB];
   const int lane = __lane_id();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1150,22 +1225,25 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   const int rpw = 4 * ((rows_blk / 4 + A.NG - 1) / A.NG);   // rows merged per workgroup (multiple of 4)
   const int r0 = rb * rows_blk + q * rpw;
   const int rend = min(rb * rows_blk + min(rows_blk, (q + 1) * rpw), A.R);
+  const int rend0 = min(rend, r0 + kNodeRows);               // the first batch of node rows
 
-  // A node segment of at most kResident chunks (K/V, score fragment, mask
-  // bytes) is loaded while the group partial is being stored.
-  const bool pf = A.NN > 0 && A.NN <= LY::kRes * kChunk && r0 < rend;
-  NodePre<D, LY::kRes> pre;
+  // A resident node segment (K/V, score fragment, mask bytes of the first
+  // batch) is loaded while the group partial is being stored.
+  const bool pf = A.NN > 0 && A.NN <= kNodeRes * kChunk && r0 < rend;
+  NodePre<D> pre;
   prompt_block<D, kRT, true>(A, lds, g, rb, q, [&] {
-    if (pf) node_prefetch<D, LY>(A, g, r0, rend, (lds_char*)lds, w, pre);
+    if (pf) node_prefetch<D>(A, g, r0, rend0, (lds_char*)lds, w, pre);
   });
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
   lds_barrier();
   if (threadIdx.x == 0) __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
+  // Node rows in batches of at most kNodeRows: the first batch's partials are
+  // computed while the other workgroups of the block finish, then the wait.
+  int* gave_up = reinterpret_cast<int*>(lds + LY::BYTES);  // one LDS word past the node areas
   if (r0 < rend) {
-    node_rows<D, LY>(A, g, r0, rend, (lds_char*)lds, w, pre, pf);
-    int* gave_up = reinterpret_cast<int*>(lds + LY::BYTES);  // one LDS word past the node areas
+    node_rows<D>(A, g, r0, rend0, (lds_char*)lds, w, pre, pf);
     if (w == 0) {
       int v = 0;
       for (int it = 0; it < A.spin; ++it) {
@@ -1180,8 +1258,17 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     }
     lds_barrier();
-    if (__builtin_amdgcn_readfirstlane(*gave_up)) nan_rows<D>(A, g, r0, rend, w);
-    else merge_rounds<D, true, LY>(A, g, r0, rend, (const lds_char*)lds, w);
+    const bool bad = __builtin_amdgcn_readfirstlane(*gave_up);
+    if (bad) nan_rows<D>(A, g, r0, rend0, w);
+    else merge_rounds<D, true>(A, g, r0, rend0, (const lds_char*)lds, w);
+    // Further batches (short prompts: few key groups, many rows per workgroup).
+    for (int b0 = rend0; b0 < rend; b0 += kNodeRows) {
+      const int be = min(rend, b0 + kNodeRows);
+      NodePre<D> none;
+      node_rows<D>(A, g, b0, be, (lds_char*)lds, w, none, false);
+      if (bad) nan_rows<D>(A, g, b0, be, w);
+      else merge_rounds<D, true>(A, g, b0, be, (const lds_char*)lds, w);
+    }
   }
   // Counters back to zero once every workgroup of the block is past its wait.
   lds_barrier();
@@ -1249,8 +1336,7 @@ static int make_plan(int H, int HK, int M, int P, int NN, int D, int rows_per_wa
   return RSPX_OK;
 }
 
-// Workgroups of fused_kernel<D, RT, *> the device holds at once, the smaller
-// of the two node layouts' figures (0 if unknown).
+// Workgroups of fused_kernel<D, RT> the device holds at once (0 if unknown).
 template <int D, int RT>
 static int fused_capacity() {
   static int cap[64];
@@ -1258,20 +1344,17 @@ static int fused_capacity() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   if (!done[dev]) {
-    int a = 0, b = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, fused_kernel<D, RT, false>, 64 * kWavesA, 0) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, fused_kernel<D, RT, true>, 64 * kWavesA, 0) != hipSuccess ||
+    int a = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, fused_kernel<D, RT>, 64 * kWavesA, 0) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-      a = b = cus = 0;
+      a = cus = 0;
     }
-    cap[dev] = (a < b ? a : b) * cus;
+    cap[dev] = a * cus;
     done[dev] = true;
   }
   return cap[dev];
 }
 
-// Rows one workgroup of fused_kernel<D, RT> merges (a multiple of 4).
-static int fused_rows(int RT, int NG) { return 4 * ((32 * RT / 4 + NG - 1) / NG); }
 
 template <int D, int RT>
 static void launch_rt(const TrieAttnArgs& a, const Plan& pl, hipStream_t s, int mode) {
@@ -1279,10 +1362,7 @@ static void launch_rt(const TrieAttnArgs& a, const Plan& pl, hipStream_t s, int 
                      (size_t)a.HK * pl.R * pl.NG * D * sizeof(float) < (size_t(1) << 31) &&
                      pl.prompt_wgs <= fused_capacity<D, RT>();
   if (fused) {
-    if (fused_rows(RT, pl.NG) <= NodeLds3<D>::kRows)
-      hipLaunchKernelGGL((fused_kernel<D, RT, true>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);
-    else
-      hipLaunchKernelGGL((fused_kernel<D, RT, false>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);
+    hipLaunchKernelGGL((fused_kernel<D, RT>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);
     return;
   }
   if (pl.prompt_wgs > 0) hipLaunchKernelGGL((prompt_kernel<D, RT>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);

@@ -352,3 +352,27 @@ def test_mfma_model_against_measured_hardware():
     a, b, c, d = (bf16.from_bits(fx["qk_a"]), bf16.from_bits(fx["qk_b"]), fx["qk_c"], fx["qk_d"])
     rev = [k for g in (3, 2, 1, 0) for k in range(8 * g, 8 * g + 8)]
     assert (A._mfma_acc(a, b, c, rev) == d).mean() < rates["qk"][0] - 0.05
+
+
+@pytest.mark.parametrize("n", [1, 7, 32, 33, 100, 257])
+def test_node_partial_rank_tiles_against_float64(n):
+    """The rank-tiled node sums (p as bf16 hi + lo through the MFMA model) against float64
+    sums of the same fp32 p: l and every acc within 2^-15 of sum |p v| (hi + lo carries
+    p to 2^-16); dropping lo (p rounded to bf16 only) fails the same bound."""
+    rng = np.random.default_rng(n)
+    H, D = 3, 64
+    s = (rng.standard_normal((H, n)) * 3).astype(np.float32)
+    v = bf16.round_bf16(rng.standard_normal((H, n, D)).astype(np.float32))
+    m, l, acc = A._node_partial(s, v)
+    assert np.array_equal(m, s.max(axis=1))
+    p = A._exp2(A._f32(s.astype(np.float64) - m[:, None])).astype(np.float64)
+    l64 = p.sum(axis=1)
+    a64 = np.einsum("hn,hnd->hd", p, v.astype(np.float64))
+    scale = np.einsum("hn,hnd->hd", p, np.abs(v).astype(np.float64))
+    assert (np.abs(l - l64) <= 2.0 ** -15 * l64).all()
+    assert (np.abs(acc - a64) <= 2.0 ** -15 * scale + 1e-30).all()
+    if n > 1:
+        _, l_bad, acc_bad = A._node_partial(s, v, hi_only=True)
+        assert (np.abs(acc_bad - a64) > 2.0 ** -15 * scale).mean() > 0.05
+    if n == 1:
+        assert np.array_equal(acc, v[:, 0]) and (l == 1).all()      # one slot: v exactly
