@@ -621,6 +621,8 @@ template <int D> struct NodeLds {
   static constexpr int NPROW = D + 4;
   static constexpr int NPOFF = SOFF + kNodeRows * SR * 4;
   static constexpr int MWOFF = NPOFF + kNodeRows * NPROW * 4;
+  // A resident segment uses MW instead as each group's rank -> slot table (int16).
+  static_assert(kNodeRows * kNodeRes * kChunk * 2 <= kNodeRows * (kMaxNodeSlots / kChunk) * 8, "rank tables fit MW");
   static constexpr int TOFF = MWOFF + kNodeRows * (kMaxNodeSlots / kChunk) * 8;
   static constexpr int ZOFF = TOFF + kWavesA * kRankTab * 2;
   static constexpr int CNTOFF = ZOFF + 2 * D;
@@ -774,15 +776,18 @@ __device__ __forceinline__ void rank_fill(int& rc, int& rbase, int upto, int nch
 
 // The node sums of one group of rows (the rows of query mq among [p0, rend);
 // MFMA column n16 is row p0 + n16, whose score fragment is qf, and columns of
-// rows outside the group carry p = 0) over d-tiles [NJ sl, NJ sl + NJ) of head_dim,
-// and l when sl = 0.  Ranks in tiles of kNodeTile: per tile, S^T = K Q^T for the
-// tile's slots (the same chain as node_scores), p = 2^(s - m) in fp32 for ranks
-// below the group's allowed count n (0 past it), hi = bf16(p), lo = bf16(p - hi),
-// then acc <- MFMA(V^T, hi, acc), acc <- MFMA(V^T, lo, acc), l likewise with
-// V = 1 -- k-slot 8 g4 + i of the B operand is rank 4 g4 + i (i < 4) or
-// 16 + 4 g4 + i - 4, as the prompt's PV product.  RES: K fragments and V rows
-// are gathered from the resident chunks by slot; otherwise K comes straight from
-// memory and each tile's V rows are copied by rank into this wave's stage.
+// rows outside the group carry p = 0) over d-tiles [NJ sl, NJ sl + NJ) of
+// head_dim, and l when sl = 0.  Ranks in tiles of kNodeTile: per tile the p of
+// the tile's ranks (0 past the group's allowed count n), hi = bf16(p),
+// lo = bf16(p - hi), then acc <- MFMA(V^T, hi, acc), acc <- MFMA(V^T, lo, acc),
+// l likewise with V = 1 -- k-slot 8 g4 + i of the B operand is rank 4 g4 + i
+// (i < 4) or 16 + 4 g4 + i - 4, as the prompt's PV product.  RES: p comes by
+// rank from the score area (node_rows wrote it there) and V rows are gathered
+// from the resident chunks through the group's rank -> slot table.  Otherwise
+// the ranks come from the query's mask words, S^T = K Q^T is recomputed for
+// the tile's slots (the chain of node_scores: the same bits) with K straight
+// from memory, p = 2^(s - m), and the tile's 32 V rows are copied by rank into
+// this wave's stage.
 template <int D, bool RES, int NJ>
 __device__ __forceinline__ void node_task(const TrieAttnArgs& A, int g, int p0, int rend, int mq, int gl, int sl,
                                           lds_char* kv, int w, int nch, const bf16x8 (&qf)[D / 32]) {
@@ -814,40 +819,52 @@ __device__ __forceinline__ void node_task(const TrieAttnArgs& A, int g, int p0, 
 
   int rc = 0, rbase = 0;
   const int ntile = (n + kNodeTile - 1) / kNodeTile;
+  const lds_float* Srow = (const lds_float*)(kv + LY::SOFF) + rl * LY::SR;
   for (int t = 0; t < ntile; ++t) {
     const int r0 = kNodeTile * t;
-    rank_fill(rc, rbase, r0 + kNodeTile, nch, mw, tab);
-    // K fragments of the tile's two 16-rank blocks: lane (n16, g4) rank r0 + 16 kb + n16.
-    u32x4 kf[2][DQ];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const int rk_ = r0 + 16 * kb + n16;
-      const int s = rk_ < n ? tab[rk_ & (kRankTab - 1)] : 0;
-#pragma unroll
-      for (int i = 0; i < DQ; ++i) {
-        if constexpr (RES) {
-          const int ch = s >> 6, sc = s & 63;
-          kf[kb][i] = *(const lds_u32x4*)(LY::kbuf(kv, ch) + ((sc >> 4) * DQ + i) * 1024 + 16 * ((sc & 15) + 16 * g4));
-        } else {
-          kf[kb][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    rk, 2 * (s * A.sknn + 32 * i + 8 * g4), 0, 0));
-        }
-      }
-    }
-    // V rows of the tile's ranks: RES reads them in place; otherwise the 32 rows
-    // are copied by rank into the stage (rows past n read zeros).
+    if constexpr (!RES) rank_fill(rc, rbase, r0 + kNodeTile, nch, mw, tab);
+    float pv[8];   // p of ranks r0 + 16 kb + 4 g4 + j (the B operand's k-slots)
     const lds_char *vrow0, *vrow1;
     int vsw0, vsw1;
     if constexpr (RES) {
+      // p of the row by rank (node_rows wrote them over the row's scores) and
+      // the group's rank -> slot table: four consecutive ranks per read.
+      const f32x4 pa = *(const lds_f32x4*)(Srow + r0 + 4 * g4);
+      const f32x4 pb = *(const lds_f32x4*)(Srow + r0 + 16 + 4 * g4);
+      const lds_i16* tg = (const lds_i16*)(kv + LY::MWOFF) + gl * kNodeRes * kChunk;
+      uint64_t t4[2];
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+        t4[kh] = *(const __attribute__((address_space(3))) uint64_t*)(tg + r0 + 16 * kh + 4 * g4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        pv[j] = col && r0 + 4 * g4 + j < n ? pa[j] : 0.f;
+        pv[4 + j] = col && r0 + 16 + 4 * g4 + j < n ? pb[j] : 0.f;
+      }
+      // V rows of ranks r0 + 16 kh + 4 g4 + e4 (entry e4 of t4[kh]); ranks past
+      // n read the zero row.
       auto vsrc = [&](int kh, const lds_char*& vr, int& sw) {
-        const int rv_ = r0 + 16 * kh + 4 * g4 + e4;
-        const int s = rv_ < n ? tab[rv_ & (kRankTab - 1)] : -1;
-        vr = s >= 0 ? LY::vbuf(kv, s >> 6) + (s & 63) * RB : zrow;
-        sw = s >= 0 ? vswz<D>(s & 63) : 0;
+        const bool on = r0 + 16 * kh + 4 * g4 + e4 < n;
+        const int s = (int)((t4[kh] >> (16 * e4)) & 0xffff);
+        vr = on ? LY::vbuf(kv, s >> 6) + (s & 63) * RB : zrow;
+        sw = on ? vswz<D>(s & 63) : 0;
       };
       vsrc(0, vrow0, vsw0);
       vsrc(1, vrow1, vsw1);
     } else {
+      // K fragments of the tile's two 16-rank blocks (lane (n16, g4): rank
+      // r0 + 16 kb + n16) straight from memory; the 32 V rows copied by rank into
+      // this wave's stage (rows past n read zeros).
+      u32x4 kf[2][DQ];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int rk_ = r0 + 16 * kb + n16;
+        const int s = rk_ < n ? tab[rk_ & (kRankTab - 1)] : 0;
+#pragma unroll
+        for (int i = 0; i < DQ; ++i)
+          kf[kb][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    rk, 2 * (s * A.sknn + 32 * i + 8 * g4), 0, 0));
+      }
       lds_char* st = stage + (t & 1) * (kNodeTile * RB);
 #pragma unroll
       for (int x = 0; x < kNodeTile * RB / 1024; ++x) {
@@ -863,20 +880,19 @@ __device__ __forceinline__ void node_task(const TrieAttnArgs& A, int g, int p0, 
       vsw0 = vswz<D>(rr0);
       vsw1 = vswz<D>(rr1);
       __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): K fragments and this wave's stage rows
-    }
-    // Scores, then p of ranks r0 + 16 kb + 4 g4 + j (the B operand's k-slots).
-    float pv[8];
+      // Scores (the chain of node_scores: the same bits as the resident form).
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      f32x4 sv = {0.f, 0.f, 0.f, 0.f};
+      for (int kb = 0; kb < 2; ++kb) {
+        f32x4 sv = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < DQ; ++i)
-        sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[kb][i]), qf[i], sv, 0, 0, 0);
-      const f32x4 s = sv * A.c;
+        for (int i = 0; i < DQ; ++i)
+          sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[kb][i]), qf[i], sv, 0, 0, 0);
+        const f32x4 sc = sv * A.c;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bool on = col && r0 + 16 * kb + 4 * g4 + j < n;
-        pv[4 * kb + j] = on ? fexp2(s[j] - mcol) : 0.f;
+        for (int j = 0; j < 4; ++j) {
+          const bool on = col && r0 + 16 * kb + 4 * g4 + j < n;
+          pv[4 * kb + j] = on ? fexp2(sc[j] - mcol) : 0.f;
+        }
       }
     }
     u32x4 hw, lw;
@@ -983,20 +999,41 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
     for (int c = 0; c < kNodeRes; ++c)
       if (c < nch) node_scores<D, LY::SR>(A, kChunk * c, LY::kbuf(kv, c), S + kChunk * c, w, qf);
     lds_barrier();
+    // Per row: m, then p = 2^(s - m) of the allowed slots written by rank over
+    // the row's own scores (rank <= slot: every score is in registers first);
+    // the group's first row writes its rank -> slot table and count.
+    lds_i16* TG = (lds_i16*)(kv + LY::MWOFF);
 #pragma unroll 1
     for (int i = 0; i < nrd; ++i) {
       const int row = w + nw * i;
+      const int r = p0 + row;
+      const bool lead = r == p0 || (r & (GQA - 1)) == 0;
+      const int gl = (r >> A.GQS) - q0;
+      float sc[kNodeRes];
+      bool ok[kNodeRes];
       float x = kNegInf;
 #pragma unroll
       for (int c = 0; c < kNodeRes; ++c) {
-        if (c < nch) {
-          const bool ok = ((mb[c] >> (8 * i)) & 0xff) != 0;
-          x = fmaxf(x, ok ? S[row * LY::SR + kChunk * c + lane] : kNegInf);
-          row_words(i, c, mb[c], x);
-        }
+        ok[c] = c < nch && ((mb[c] >> (8 * i)) & 0xff) != 0;
+        sc[c] = c < nch ? S[row * LY::SR + kChunk * c + lane] : 0.f;
+        x = fmaxf(x, ok[c] ? sc[c] : kNegInf);
       }
       const float m = max64(x);
       if (lane == 0) NP[row * LY::NPROW] = m;
+      int base = 0;
+#pragma unroll
+      for (int c = 0; c < kNodeRes; ++c) {
+        if (c < nch) {
+          const uint64_t mm = __builtin_amdgcn_ballot_w64(ok[c]);
+          const int rk = base + lanes_below(mm);
+          if (ok[c]) {
+            S[row * LY::SR + rk] = fexp2(sc[c] - m);
+            if (lead) TG[gl * kNodeRes * kChunk + rk] = (int16_t)(kChunk * c + lane);
+          }
+          base += __builtin_popcountll(mm);
+        }
+      }
+      if (lead && lane == 0) *(lds_u32*)(kv + LY::CNTOFF + 4 * gl) = (uint32_t)base;
     }
   } else {
     for (int c = 0; c < nch; ++c) {
