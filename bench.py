@@ -585,6 +585,30 @@ def bench_sweep(args) -> dict:
             "points": points}
 
 
+COMMITTED = (0, 24, 48, 72, 200, 500)
+
+
+def bench_committed(args) -> dict:
+    """The 8B-shape call with committed slots before the 64-node trie in the node segment
+    (the verify step's attention after earlier steps): µs per call for each count."""
+    from respect_amd.kernels.attention import make_launcher
+    from respect_amd.workloads import AttnWorkload
+
+    points = []
+    for base in COMMITTED:
+        wl = AttnWorkload(sets=16, seed=base, base=base)
+        launchers, keep = [], []
+        for (q, kp, vp, kn, vn) in wl.sets:
+            launch, out = make_launcher(q, kp, vp, kn, vn, wl.msk, wl.sm_scale)
+            launchers.append(launch)
+            keep.append(out)
+        ms = time_launches(launchers, 100, 10)
+        points.append({"committed": base, "node_slots": wl.NN, "us": round(ms * 1e3, 2)})
+        del wl, launchers, keep
+    return {"workload": "8B-shape attention, 3072-token prompt KV, 64-node trie after N committed node slots "
+                        "(16 rotating input sets)", "points": points}
+
+
 def bench_floor(args) -> dict:
     """What the 8B-shape attention launch costs before any arithmetic (rspx_floor_launch):
     its grid (256 x 512 threads, 147 KB LDS) empty; streaming each workgroup's K/V share
@@ -678,6 +702,8 @@ def main() -> int:
         res["extra"]["prefill"] = bench_prefill(args)
         _log("timing the attention sweep (prompt lengths x trie sizes)")
         res["extra"]["attn_sweep"] = bench_sweep(args)
+        _log("timing the call with committed node slots")
+        res["extra"]["attn_committed"] = bench_committed(args)
     if not args.no_decoder:
         dec = bench_decoder(args)
         res["committed_tok_s"] = dec["committed_tok_s"]
