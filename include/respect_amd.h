@@ -203,8 +203,10 @@ int rspx_rmsnorm(const void* x, int64_t sx, const void* w, void* y, int64_t sy, 
  * y = bf16(bf16(x * cos) + bf16(rotate_half(x) * sin))   (replaces
  * respect/system/fused.py:67 rope(x, cos, sin) for bf16 inputs).
  * x: [B, H, L, D] with strides sxb, sxh, sxl; cos/sin: [B, L, D] with strides
- * scb, scl; y: [B, H, L, D] contiguous.  D == 128.  Bitwise equal to PyTorch's
- * bf16 elementwise ops.
+ * scb, scl; y: [B, H, L, D] contiguous.  Any D with D % 16 == 0 and
+ * D <= 512 (RSPX_EUNSUPPORTED otherwise; the reference's kernel masks a
+ * power-of-two tile, fused.py:47-75).  Bitwise equal to PyTorch's bf16
+ * elementwise ops.
  */
 int rspx_rope(const void* x, int64_t sxb, int64_t sxh, int64_t sxl, const void* cos, const void* sin,
               int64_t scb, int64_t scl, void* y, int B, int H, int L, int D, void* stream);

@@ -233,6 +233,43 @@ __global__ __launch_bounds__(256) void rope_kernel(const uint16_t* x, int64_t sx
   *reinterpret_cast<u32x4*>(y + (int64_t)rowid * D + sub * 8) = pack8(o);
 }
 
+// RoPE for any D with D % 16 == 0 and D <= 512: a row's D elements sit on
+// TPR = D / 8 consecutive lanes of a wave (8 each; 64 / TPR rows per wave, the
+// remaining lanes idle), and the rotate-half partner -- D / 2 elements away,
+// TPR / 2 lanes -- comes through ds_bpermute.  The arithmetic of rope_kernel:
+// bf16(x cos) + bf16(rotate_half(x) sin), rounded to bf16 by the store.
+__global__ __launch_bounds__(256) void rope_any_kernel(const uint16_t* x, int64_t sxb, int64_t sxh, int64_t sxl,
+                                                       const uint16_t* cosb, const uint16_t* sinb, int64_t scb,
+                                                       int64_t scl, uint16_t* y, int B, int H, int L, int D) {
+  const int lane = __lane_id();
+  const int TPR = D >> 3, half = TPR >> 1, rpw = 64 / TPR;
+  const int rin = lane / TPR, sub = lane - rin * TPR;
+  const int64_t rowid = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * rpw + rin;
+  const int64_t nrows = (int64_t)B * H * L;
+  const bool act = rin < rpw && rowid < nrows;
+  float xv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, cs[8], sn[8];
+  int64_t yo = 0;
+  if (act) {
+    const int l = (int)(rowid % L);
+    const int h = (int)((rowid / L) % H);
+    const int b = (int)(rowid / ((int64_t)L * H));
+    unpack8(*reinterpret_cast<const u32x4*>(x + b * sxb + h * sxh + (int64_t)l * sxl + sub * 8), xv);
+    unpack8(*reinterpret_cast<const u32x4*>(cosb + b * scb + (int64_t)l * scl + sub * 8), cs);
+    unpack8(*reinterpret_cast<const u32x4*>(sinb + b * scb + (int64_t)l * scl + sub * 8), sn);
+    yo = rowid * D + sub * 8;
+  }
+  // Every lane takes part in the exchange; idle lanes send zeros.
+  const int partner = lane - sub + (sub < half ? sub + half : sub - half);
+  float o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float p = __int_as_float(__builtin_amdgcn_ds_bpermute(partner << 2, __float_as_int(xv[i])));
+    const float rh = sub < half ? -p : p;
+    o[i] = round_bf16(xv[i] * cs[i]) + round_bf16(rh * sn[i]);
+  }
+  if (act) *reinterpret_cast<u32x4*>(y + yo) = pack8(o);
+}
+
 // q/k RMSNorm over head_dim followed by RoPE, D = 128, one launch for q and k.
 // q [T, HQ, D] (token stride sqt, head stride sqh), k [T, HK, D]; wq, wk [D];
 // cos/sin rows per token (stride scs); outputs qo [T, HQ, D], ko [T, HK, D]
@@ -424,13 +461,22 @@ extern "C" int rspx_add_rmsnorm_partials(const void* r, int64_t sr, const float*
 
 extern "C" int rspx_rope(const void* x, int64_t sxb, int64_t sxh, int64_t sxl, const void* cosb, const void* sinb,
                          int64_t scb, int64_t scl, void* y, int B, int H, int L, int D, void* stream) {
-  if (B < 0 || H < 0 || L < 0) return RSPX_EINVAL;
-  if (D != 128) return RSPX_EUNSUPPORTED;
+  if (B < 0 || H < 0 || L < 0 || D <= 0) return RSPX_EINVAL;
+  if (D % 16 != 0 || D > 512) return RSPX_EUNSUPPORTED;
   const int64_t rows = (int64_t)B * H * L;
   if (rows == 0) return RSPX_OK;
   if (!x || !cosb || !sinb || !y) return RSPX_EINVAL;
   if (!al16(x) || !al16(cosb) || !al16(sinb) || !al16(y) || sxb % 8 || sxh % 8 || sxl % 8 || scb % 8 || scl % 8)
     return RSPX_EALIGN;
+  if (D != 128) {
+    const int64_t waves = (rows + 64 / (D / 8) - 1) / (64 / (D / 8));
+    if ((waves + 3) / 4 > 0x7fffffff) return RSPX_EUNSUPPORTED;
+    hipLaunchKernelGGL(rope_any_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), sxb, sxh, sxl,
+                       static_cast<const uint16_t*>(cosb), static_cast<const uint16_t*>(sinb), scb, scl,
+                       static_cast<uint16_t*>(y), B, H, L, D);
+    return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
+  }
   const int64_t threads = rows * 16;
   hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), sxb, sxh, sxl,

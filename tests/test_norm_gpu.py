@@ -117,9 +117,9 @@ def test_kernel_errors():
         rmsnorm(x, torch.ones(100, device="cuda", dtype=torch.bfloat16), 1e-6)
     with pytest.raises(TypeError):
         silu_mul(x.float(), x.float())
-    with pytest.raises(RspxError):
-        c = torch.ones(1, 2, 64, device="cuda", dtype=torch.bfloat16)
-        rope(torch.ones(1, 1, 2, 64, device="cuda", dtype=torch.bfloat16), c, c)
+    with pytest.raises(RspxError):   # head_dim not a multiple of 16
+        c = torch.ones(1, 2, 72, device="cuda", dtype=torch.bfloat16)
+        rope(torch.ones(1, 1, 2, 72, device="cuda", dtype=torch.bfloat16), c, c)
 
 
 @pytest.mark.parametrize("rows,n", [(1, 4096), (7, 4096), (64, 4096), (130, 4096), (9, 256), (64, 12288)])
@@ -152,3 +152,33 @@ def test_rmsnorm_tiled_output(rows, n):
     torch.cuda.synchronize()
     assert torch.equal(from_tiled(out, rows, n), ref)
     assert torch.equal(xo1, xo2)
+
+
+@pytest.mark.parametrize("D", [16, 32, 64, 80, 96, 256, 512])
+def test_rope_any_head_dim_bitwise(D):
+    """rope for head dims other than 128 (the reference's rope takes any D, fused.py:45-75):
+    bitwise equal to the oracle (= PyTorch's bf16 element-wise ops), with strided x and a
+    row count that leaves a partial wave."""
+    from respect_amd.system.fused import rope
+    rng = np.random.default_rng(D)
+    B, H, L = 2, 3, 37
+    x = gen.bf16_normal(rng, (B, H, L, D))
+    pos = rng.integers(0, 4096, (B, L))
+    tabs = [N.rope_tables(pos[b], head_dim=D) for b in range(B)]
+    cos = np.stack([t[0] for t in tabs])
+    sin = np.stack([t[1] for t in tabs])
+    print(f"[rope] D={D}", flush=True)
+    out = _np(rope(_dev(x), _dev(cos), _dev(sin)))
+    assert np.array_equal(out, N.rope(x, cos[:, None], sin[:, None]))
+    xs = _dev(x).transpose(1, 2).contiguous().transpose(1, 2)
+    assert np.array_equal(_np(rope(xs, _dev(cos), _dev(sin))), out)
+
+
+def test_rope_unsupported_head_dims():
+    from respect_amd import _lib
+    from respect_amd.system.fused import rope
+    for D in (8, 24, 528):
+        x = torch.zeros(1, 1, 2, D, dtype=torch.bfloat16, device="cuda")
+        c = torch.zeros(1, 2, D, dtype=torch.bfloat16, device="cuda")
+        with pytest.raises(_lib.RspxError):
+            rope(x, c, c)
