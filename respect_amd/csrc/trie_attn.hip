@@ -998,6 +998,10 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
 #pragma unroll
     for (int c = 0; c < kNodeRes; ++c)
       if (c < nch) node_scores<D, LY::SR>(A, kChunk * c, LY::kbuf(kv, c), S + kChunk * c, w, qf);
+    if (w == 0) {
+      // The zero V row (2 D bytes).
+      for (int b = 4 * lane; b < 2 * D; b += 256) *(lds_u32*)(kv + LY::ZOFF + b) = 0u;
+    }
     lds_barrier();
     // Per row: m, then p = 2^(s - m) of the allowed slots written by rank over
     // the row's own scores (rank <= slot: every score is in registers first);
@@ -1036,27 +1040,56 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
       if (lead && lane == 0) *(lds_u32*)(kv + LY::CNTOFF + 4 * gl) = (uint32_t)base;
     }
   } else {
-    for (int c = 0; c < nch; ++c) {
-      if (c > 0) lds_barrier();  // every wave is done with the previous chunk's scores
-      node_issue<D>(A, g, kChunk * c, kv, 0, w, nw, false);
-      const uint32_t mb = node_masks(A, p0, nrd, w, kChunk * c);
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-      lds_barrier();
-      node_scores<D, LY::SR>(A, kChunk * c, LY::kbuf(kv, 0), S, w, qf);
+    // Streaming: the scores of up to SUP slots at a time into the KB / VB area
+    // ([row][SUP + 4] fp32), from K fragments loaded straight into registers
+    // (16-slot tiles, waves w, w + 8, ...), the rows' mask bits beside them; then
+    // each row's maximum, mask words and count.
+    constexpr int DQ = D / 32;
+    constexpr int SUP = ((2 * kNodeRes * LY::CB) / (kNodeRows * 4) - 4) / kChunk * kChunk;
+    constexpr int SRS = SUP + 4;
+    static_assert(kNodeRows * SRS * 4 <= 2 * kNodeRes * LY::CB && SUP / kChunk <= 32, "super-chunk scores fit KB + VB");
+    lds_float* SS = (lds_float*)(kv + LY::KOFF);
+    const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(A.kn + g * A.sknh, 2 * ((NN - 1) * A.sknn + D));
+    const int n16 = lane & 15, g4 = lane >> 4;
+    for (int s0 = 0; s0 < NN; s0 += SUP) {
+      const int ns = min(SUP, NN - s0);
+      if (s0 > 0) lds_barrier();   // every wave is done with the previous super-chunk's scores
+      uint32_t mbits[kNodeRounds] = {};
+      for (int c = 0; c < ns / kChunk + (ns % kChunk != 0); ++c) {
+        const uint32_t mb = node_masks(A, p0, nrd, w, s0 + kChunk * c);
+#pragma unroll
+        for (int i = 0; i < kNodeRounds; ++i) mbits[i] |= (uint32_t)(((mb >> (8 * i)) & 0xff) != 0) << c;
+      }
+      const int nt = (ns + 15) / 16;
+      for (int tt = w; tt < nt; tt += nw) {
+        const int slot = s0 + 16 * tt + n16;
+        const int sr = slot < NN ? slot : 0;
+        u32x4 kf[DQ];
+#pragma unroll
+        for (int i = 0; i < DQ; ++i)
+          kf[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                rk, 2 * (sr * A.sknn + 32 * i + 8 * g4), 0, 0));
+        f32x4 sv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < DQ; ++i)
+          sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[i]), qf[i], sv, 0, 0, 0);
+        // Lane (n16, g4), element j: slot s0 + 16 tt + 4 g4 + j of row p0 + n16.
+        *(lds_f32x4*)(SS + n16 * SRS + 16 * tt + 4 * g4) = sv * A.c;
+      }
       lds_barrier();
 #pragma unroll 1
       for (int i = 0; i < nrd; ++i) {
         const int row = w + nw * i;
-        const bool ok = ((mb >> (8 * i)) & 0xff) != 0;
-        const float x = max64(ok ? S[row * LY::SR + lane] : kNegInf);
-        row_words(i, c, mb, x);
-        if (lane == 0) NP[row * LY::NPROW] = c == 0 ? x : fmaxf(NP[row * LY::NPROW], x);
+        float x = kNegInf;
+        for (int c = 0; c * kChunk < ns; ++c) {
+          const bool ok = (mbits[i] >> c) & 1;
+          x = fmaxf(x, ok ? SS[row * SRS + kChunk * c + lane] : kNegInf);
+          row_words(i, (s0 / kChunk) + c, ok ? 0xffu << (8 * i) : 0u, x);
+        }
+        const float m = max64(x);
+        if (lane == 0) NP[row * LY::NPROW] = s0 == 0 ? m : fmaxf(NP[row * LY::NPROW], m);
       }
     }
-  }
-  if (w == 0) {
-    // The zero V row (2 D bytes).
-    for (int b = 4 * lane; b < 2 * D; b += 256) *(lds_u32*)(kv + LY::ZOFF + b) = 0u;
   }
   lds_barrier();   // scores, maxima, mask words and counts visible; KB / VB free when streaming
 
