@@ -162,7 +162,7 @@ int rspx_trie_attn_noalloc(const void* q, int64_t sqh, int64_t sqm, const void* 
  * workspace), but node slots reduced tile by tile (BN in {32, 64, 128}) like
  * the prompt, one online-softmax update per tile, bf16 probabilities in every
  * PV product -- so the result depends on where the node slots sit.  D in
- * {64, 128}.  Output row stride and base 8-byte aligned.
+ * {32, 64, 128, 256}.  Output row stride and base 8-byte aligned.
  */
 int rspx_blocked_attn(const void* q, int64_t sqh, int64_t sqm, const void* kp, int64_t skph, int64_t skpn,
                       const void* vp, int64_t svph, int64_t svpn, const void* kn, int64_t sknh, int64_t sknn,

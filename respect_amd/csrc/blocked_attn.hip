@@ -182,7 +182,7 @@ extern "C" int rspx_blocked_attn(const void* q, int64_t sqh, int64_t sqm, const 
                                  int64_t smm, int64_t smn, void* out, int64_t soh, int64_t som, int H, int HK, int M,
                                  int P, int NN, int D, int BN, float sm_scale, void* stream) {
   if (H <= 0 || HK <= 0 || H % HK || M < 0 || P < 0 || NN < 0) return RSPX_EINVAL;
-  if (D != 64 && D != 128) return RSPX_EUNSUPPORTED;
+  if (D != 32 && D != 64 && D != 128 && D != 256) return RSPX_EUNSUPPORTED;
   if (BN != 32 && BN != 64 && BN != 128) return RSPX_EUNSUPPORTED;
   if (!(sm_scale > 0.f) || sm_scale == __builtin_huge_valf()) return RSPX_EINVAL;
   if (M == 0) return RSPX_OK;
@@ -210,15 +210,15 @@ extern "C" int rspx_blocked_attn(const void* q, int64_t sqh, int64_t sqm, const 
   const dim3 grid((M + 15) / 16, H);
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define RSPX_BLOCKED(DD, BB) hipLaunchKernelGGL((blocked::blocked_kernel<DD, BB>), grid, dim3(64), 0, s, a)
-  if (D == 128) {
-    if (BN == 32) RSPX_BLOCKED(128, 32);
-    else if (BN == 64) RSPX_BLOCKED(128, 64);
-    else RSPX_BLOCKED(128, 128);
-  } else {
-    if (BN == 32) RSPX_BLOCKED(64, 32);
-    else if (BN == 64) RSPX_BLOCKED(64, 64);
-    else RSPX_BLOCKED(64, 128);
-  }
+#define RSPX_BLOCKED_BN(DD)             \
+  if (BN == 32) RSPX_BLOCKED(DD, 32);    \
+  else if (BN == 64) RSPX_BLOCKED(DD, 64); \
+  else RSPX_BLOCKED(DD, 128);
+  if (D == 128) { RSPX_BLOCKED_BN(128) }
+  else if (D == 64) { RSPX_BLOCKED_BN(64) }
+  else if (D == 32) { RSPX_BLOCKED_BN(32) }
+  else { RSPX_BLOCKED_BN(256) }
+#undef RSPX_BLOCKED_BN
 #undef RSPX_BLOCKED
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }

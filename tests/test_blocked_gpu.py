@@ -49,9 +49,13 @@ def _check(case, out, BN=64):
     assert r.max() <= 1.0
 
 
-@pytest.mark.parametrize("which,BN", [("cfg1", 64), ("cfg2", 64), ("cfg2", 32), ("cfg2", 128), ("base40", 64)])
+@pytest.mark.parametrize("which,BN", [("cfg1", 64), ("cfg2", 64), ("cfg2", 32), ("cfg2", 128), ("base40", 64),
+                                      ("d32", 64), ("d256", 32), ("d256", 128)])
 def test_blocked_parity(which, BN):
-    c = {"cfg1": gen.cfg1, "cfg2": gen.cfg2, "base40": lambda: gen.cfg2(seed=4, base=40)}[which]()
+    """Every head_dim the reference's fused_attn accepts (reference_blocked.py:89)."""
+    c = {"cfg1": gen.cfg1, "cfg2": gen.cfg2, "base40": lambda: gen.cfg2(seed=4, base=40),
+         "d32": lambda: gen.attn_case(7, 8, 2, 32, 700, 3, 10, 0, 8, 24),
+         "d256": lambda: gen.attn_case(8, 8, 4, 256, 900, 3, 12, 0, 8, 32, kv_scale=256 ** -0.5)}[which]()
     _check(c, _blocked(c, BN), BN)
 
 
