@@ -80,7 +80,8 @@ const char* rspx_version(void);
  * P is explicit (in the reference it is kp.shape[1]).  Strides are in
  * elements; the D axis must have stride 1.  q/k/v/out base pointers and
  * head/row strides must be 16-byte aligned (strides multiple of 8 elements).
- * Head h reads kv head h / (H / HK).  D in {64, 128}; H / HK in {1,2,4,8,16}.
+ * Head h reads kv head h / (H / HK).  D in {32, 64, 128, 256} (the head_dims
+ * of reference_blocked.py:89); H / HK in {1,2,4,8,16}.
  *
  * Result per (head, row): softmax over the P prompt keys and the allowed node
  * slots, fp32 accumulation, one bf16 rounding at the end.  The reduction
@@ -104,7 +105,8 @@ const char* rspx_version(void);
  *
  * rows_per_wave: 0 = automatic (one 16-row tile per wave when that grid
  * fits on the device at once, e.g. 1-token calls; two otherwise), else 1 or
- * 2.  It changes only the work distribution, never the result.
+ * 2.  It changes only the work distribution, never the result.  D = 256
+ * always runs one (2 returns RSPX_EUNSUPPORTED).
  */
 
 int64_t rspx_trie_attn_workspace_bytes(int H, int HK, int M, int P, int D);

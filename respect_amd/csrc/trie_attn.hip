@@ -51,6 +51,11 @@
 //   head's K/V is read once from HBM for all query heads that share it.  With
 //   8 kv heads, workgroup g of kernel A lands on XCD g (round-robin dispatch),
 //   so the row blocks that share a head's K/V meet in one XCD's L2.
+//   head_dim 32, 64, 128 or 256, the arithmetic the same function of D.  The
+//   LDS budget sets the rest: a round of four steps takes 16 / 64 / 128 KB at
+//   D = 32 / 128 / 256, so the ring holds 4 / 2 / 1 rounds; a resident node
+//   segment holds 3 chunks (1 at D = 256), and D = 256 runs one 16-row tile
+//   per wave (two would not fit the registers).
 
 #include <mutex>
 #include <type_traits>
@@ -156,24 +161,32 @@ struct StepGeom {
   static constexpr int KBYTES = KCH * 1024;
   static constexpr int SLOT = CH * 1024;     // bytes per step
   static constexpr int ROUND = kQuarters * SLOT;
-  static constexpr int RING = D == 128 ? 2 : 4;  // rounds in flight
+  static constexpr int RING = D == 256 ? 1 : D == 128 ? 2 : 4;  // rounds in flight (LDS-bound)
   static constexpr int OWN = kQuarters * CH / kWavesA;  // chunks one wave issues per round
 };
 
 // K rows in LDS: 16-byte unit u of key row `key` holds the row's unit
 // u ^ kswz(key), so the 16 lanes of an MFMA A-fragment read (keys n16 of a
-// 16-key block, one 16-byte unit each) fall on 16 different bank groups, while
-// each direct-to-LDS load still copies whole rows (KPV of them, 1 KB).
+// 16-key block, one 16-byte unit each) fall on 16 different bank groups of
+// the 256-byte bank row, while each direct-to-LDS load still copies whole
+// rows (KPV of them, 1 KB).  Rows of at least 256 bytes start in bank group
+// 0, so the key alone picks the group; shorter rows share a bank row with
+// 256 / (2 D) - 1 neighbours and the swizzle changes every 16 / U keys.
 template <int D>
 __device__ __forceinline__ int kswz(int key) {
   constexpr int U = D / 8;
-  return (key / (16 / U)) % U;
+  if constexpr (U >= 16) return key % 16;
+  else return (key / (16 / U)) % U;
 }
 
+// V rows: an even swizzle (units 2 j and 2 j + 1 stay adjacent), so that the
+// 32 lanes of one pass of a transposing read (8 keys x 32 bytes) hit distinct
+// 32-byte bank ranges.
 template <int D>
 __device__ __forceinline__ int vswz(int key) {
   constexpr int U = D / 8;
-  return 2 * ((key / (16 / U)) % (U / 2));
+  if constexpr (U >= 16) return 2 * (key % 8);
+  else return 2 * ((key / (16 / U)) % (U / 2));
 }
 
 // s_waitcnt vmcnt(v) for an immediate v.
@@ -531,14 +544,19 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
   lds_barrier();
   // Group partial: rows RPI x + lane / (D / 4), columns [4 c4, +4): 1 KB per
   // store instruction; ATOMIC: with the coherence of an agent-scope atomic store.
+  // With fewer pieces than waves (D = 32, one row tile) waves past the last
+  // piece store nothing.
   constexpr int RPI = 1024 / (4 * D);
   constexpr int NST = BR / RPI;
-  static_assert(NST % kWavesA == 0, "every wave stores the same number of pieces");
-  constexpr int NSW = NST / kWavesA;
+  static_assert(NST % kWavesA == 0 || NST < kWavesA, "every storing wave stores the same number of pieces");
+  constexpr int NSW = (NST + kWavesA - 1) / kWavesA;
+  const bool stores = NST >= kWavesA || w < NST;
   const int c4 = lane % (D / 4);
   f32x4 sv[NSW];
 #pragma unroll
   for (int jj = 0; jj < NSW; ++jj) {
+    sv[jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (!stores) continue;
     const int rl = (w + kWavesA * jj) * RPI + lane / (D / 4);
     const lds_float* src = qacc + rl * D + 4 * (c4 ^ (rl & 7));
     const f32x4 a0 = *(const lds_f32x4*)(src);
@@ -571,7 +589,7 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
 #pragma unroll
   for (int jj = 0; jj < NSW; ++jj) {
     const int r = row0 + (w + kWavesA * jj) * RPI + lane / (D / 4);
-    if (r < A.R) {
+    if (stores && r < A.R) {
       const size_t off = (((size_t)g * A.R + r) * A.NG + q) * D + 4 * c4;
       if constexpr (ATOMIC) __builtin_amdgcn_raw_buffer_store_b128(sv[jj], racc, (int)(off * 4), 0, 16);
       else *reinterpret_cast<f32x4*>(A.gp_acc + off) = sv[jj];
@@ -591,38 +609,40 @@ __global__ __launch_bounds__(512) void prompt_kernel(TrieAttnArgs A) {
 constexpr int kChunk = 64;       // node slots staged in LDS at a time
 constexpr int kNodeTile = 32;    // ranks per MFMA tile of the node sums
 constexpr int kNodeRows = 16;    // rows of one node_rows call (at most one MFMA tile of columns)
-constexpr int kNodeRes = 3;      // chunks a resident node segment holds
 constexpr int kRankTab = 128;    // entries of a wave's rolling rank -> slot table
-constexpr int kStageSlots = 6;   // waves with a double-buffered V stage when streaming
 static_assert(kMaxNodeSlots % kChunk == 0, "whole mask words");
 
 // Node LDS, for at most kNodeRows rows:
-//   KB   kNodeRes chunks of K as score fragments -- 1 KB per 16-slot tile kt and
+//   KB   RES chunks of K as score fragments -- 1 KB per 16-slot tile kt and
 //        32-wide head_dim step i; lane (n16, g4)'s 16 bytes are K[16 kt + n16][32 i +
 //        8 g4, +8), one ds_read_b128;
-//   VB   kNodeRes chunks of V rows, 2 D bytes per slot; 16-byte unit u of row r holds
+//   VB   RES chunks of V rows, 2 D bytes per slot; 16-byte unit u of row r holds
 //        the row's unit u ^ vswz(r), so the transposing reads of four rows hit
 //        distinct banks.  When the segment streams, KB and VB hold instead
-//        kStageSlots double-buffered V stages of kNodeTile rows (same row layout);
+//        STAGES double-buffered V stages of kNodeTile rows (same row layout);
 //   S    fp32 scores (times c) of the rows x the resident slots (or one chunk);
 //   NP   the node partial of each row: m, l, pad, pad, acc[D];
 //   MW   per group of rows, the 64-bit allowed-slot mask word of every chunk;
 //   TAB  per wave, kRankTab int16: the slot of rank r at r % kRankTab;
 //   Z    2 D bytes of zeros (the V row of a rank past the row's allowed count);
 //   CNT  per group, the number of allowed slots.
+//   RES chunks (192 slots up to D = 128, 64 at D = 256) make a resident
+//   segment; STAGES waves stream a longer one.
 template <int D> struct NodeLds {
+  static constexpr int RES = D <= 128 ? 3 : 1;        // chunks a resident node segment holds
+  static constexpr int STAGES = D <= 128 ? 6 : 2;     // waves with a double-buffered V stage when streaming
   static constexpr int CB = kChunk * 2 * D;   // one chunk's K (or V)
   static constexpr int KOFF = 0;
-  static constexpr int VOFF = kNodeRes * CB;
+  static constexpr int VOFF = RES * CB;
   static constexpr int STAGE = 2 * kNodeTile * 2 * D;   // one wave's double-buffered V stage
-  static_assert(kStageSlots * STAGE <= 2 * kNodeRes * CB, "stages fit KB + VB");
-  static constexpr int SR = kNodeRes * kChunk + 4;      // floats per score row
-  static constexpr int SOFF = 2 * kNodeRes * CB;
+  static_assert(STAGES * STAGE <= 2 * RES * CB, "stages fit KB + VB");
+  static constexpr int SR = RES * kChunk + 4;      // floats per score row
+  static constexpr int SOFF = 2 * RES * CB;
   static constexpr int NPROW = D + 4;
   static constexpr int NPOFF = SOFF + kNodeRows * SR * 4;
   static constexpr int MWOFF = NPOFF + kNodeRows * NPROW * 4;
   // A resident segment uses MW instead as each group's rank -> slot table (int16).
-  static_assert(kNodeRows * kNodeRes * kChunk * 2 <= kNodeRows * (kMaxNodeSlots / kChunk) * 8, "rank tables fit MW");
+  static_assert(kNodeRows * RES * kChunk * 2 <= kNodeRows * (kMaxNodeSlots / kChunk) * 8, "rank tables fit MW");
   static constexpr int TOFF = MWOFF + kNodeRows * (kMaxNodeSlots / kChunk) * 8;
   static constexpr int ZOFF = TOFF + kWavesA * kRankTab * 2;
   static constexpr int CNTOFF = ZOFF + 2 * D;
@@ -655,7 +675,7 @@ typedef __attribute__((address_space(3))) uint32_t lds_u32;
 constexpr int kNodeRounds = kNodeRows / kWavesA;  // rows per wave in one node_rows call
 
 // Loads a caller may issue ahead of node_rows for a resident node segment (at
-// most kNodeRes chunks): every chunk's K/V in LDS, the score fragment of the
+// most NodeLds<D>::RES chunks): every chunk's K/V in LDS, the score fragment of the
 // wave's first task and the mask bytes of the wave's rows.
 template <int D> struct NodePre {
   bf16x8 qf[D / 32];
@@ -831,7 +851,7 @@ __device__ __forceinline__ void node_task(const TrieAttnArgs& A, int g, int p0, 
       // the group's rank -> slot table: four consecutive ranks per read.
       const f32x4 pa = *(const lds_f32x4*)(Srow + r0 + 4 * g4);
       const f32x4 pb = *(const lds_f32x4*)(Srow + r0 + 16 + 4 * g4);
-      const lds_i16* tg = (const lds_i16*)(kv + LY::MWOFF) + gl * kNodeRes * kChunk;
+      const lds_i16* tg = (const lds_i16*)(kv + LY::MWOFF) + gl * LY::RES * kChunk;
       uint64_t t4[2];
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh)
@@ -933,7 +953,7 @@ __device__ __forceinline__ void node_task(const TrieAttnArgs& A, int g, int p0, 
 // not on where in the node segment they sit.  Every wave of the workgroup
 // calls it; the partial (m, l, acc) of row p0 + i is left in the node-partial
 // area of LDS, row i, after the closing barrier.
-//   have_pre: the caller issued a resident segment (at most kNodeRes chunks,
+//   have_pre: the caller issued a resident segment (at most RES chunks,
 // chunk c into buffer c) and `pre` (node_prefetch), has since waited for those
 // loads (vmcnt 0) and passed a workgroup barrier.  A resident segment the
 // caller did not issue is loaded here; a longer one streams: its maxima come
@@ -949,7 +969,7 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
   if (NN == 0) return;
   const int nrd = (rend - p0 - w + nw - 1) / nw;   // rows of this wave: p0 + w + 8 i
   const int nch = (NN + kChunk - 1) / kChunk;
-  const bool res = NN <= kNodeRes * kChunk;
+  const bool res = NN <= LY::RES * kChunk;
   lds_float* S = (lds_float*)(kv + LY::SOFF);
   lds_float* NP = (lds_float*)(kv + LY::NPOFF);
   const int GQA = 1 << A.GQS;
@@ -978,14 +998,15 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
     (void)x;
   };
   if (res) {
-    uint32_t mb[kNodeRes];
+    uint32_t mb[LY::RES];
     if (have_pre) {
+      static_assert(LY::RES <= 3, "NodePre holds the mask bytes of three chunks");
       mb[0] = pre.mb0;
-      mb[1] = pre.mb1;
-      mb[2] = pre.mb2;
+      if constexpr (LY::RES > 1) mb[1] = pre.mb1;
+      if constexpr (LY::RES > 2) mb[2] = pre.mb2;
     } else {
 #pragma unroll
-      for (int c = 0; c < kNodeRes; ++c) {
+      for (int c = 0; c < LY::RES; ++c) {
         mb[c] = 0;
         if (c < nch) {
           node_issue<D>(A, g, kChunk * c, kv, c, w, nw, true);
@@ -996,7 +1017,7 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
       lds_barrier();
     }
 #pragma unroll
-    for (int c = 0; c < kNodeRes; ++c)
+    for (int c = 0; c < LY::RES; ++c)
       if (c < nch) node_scores<D, LY::SR>(A, kChunk * c, LY::kbuf(kv, c), S + kChunk * c, w, qf);
     if (w == 0) {
       // The zero V row (2 D bytes).
@@ -1013,11 +1034,11 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
       const int r = p0 + row;
       const bool lead = r == p0 || (r & (GQA - 1)) == 0;
       const int gl = (r >> A.GQS) - q0;
-      float sc[kNodeRes];
-      bool ok[kNodeRes];
+      float sc[LY::RES];
+      bool ok[LY::RES];
       float x = kNegInf;
 #pragma unroll
-      for (int c = 0; c < kNodeRes; ++c) {
+      for (int c = 0; c < LY::RES; ++c) {
         ok[c] = c < nch && ((mb[c] >> (8 * i)) & 0xff) != 0;
         sc[c] = c < nch ? S[row * LY::SR + kChunk * c + lane] : 0.f;
         x = fmaxf(x, ok[c] ? sc[c] : kNegInf);
@@ -1026,13 +1047,13 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
       if (lane == 0) NP[row * LY::NPROW] = m;
       int base = 0;
 #pragma unroll
-      for (int c = 0; c < kNodeRes; ++c) {
+      for (int c = 0; c < LY::RES; ++c) {
         if (c < nch) {
           const uint64_t mm = __builtin_amdgcn_ballot_w64(ok[c]);
           const int rk = base + lanes_below(mm);
           if (ok[c]) {
             S[row * LY::SR + rk] = fexp2(sc[c] - m);
-            if (lead) TG[gl * kNodeRes * kChunk + rk] = (int16_t)(kChunk * c + lane);
+            if (lead) TG[gl * LY::RES * kChunk + rk] = (int16_t)(kChunk * c + lane);
           }
           base += __builtin_popcountll(mm);
         }
@@ -1045,9 +1066,9 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
     // (16-slot tiles, waves w, w + 8, ...), the rows' mask bits beside them; then
     // each row's maximum, mask words and count.
     constexpr int DQ = D / 32;
-    constexpr int SUP = ((2 * kNodeRes * LY::CB) / (kNodeRows * 4) - 4) / kChunk * kChunk;
+    constexpr int SUP = ((2 * LY::RES * LY::CB) / (kNodeRows * 4) - 4) / kChunk * kChunk;
     constexpr int SRS = SUP + 4;
-    static_assert(kNodeRows * SRS * 4 <= 2 * kNodeRes * LY::CB && SUP / kChunk <= 32, "super-chunk scores fit KB + VB");
+    static_assert(kNodeRows * SRS * 4 <= 2 * LY::RES * LY::CB && SUP / kChunk <= 32, "super-chunk scores fit KB + VB");
     lds_float* SS = (lds_float*)(kv + LY::KOFF);
     const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(A.kn + g * A.sknh, 2 * ((NN - 1) * A.sknn + D));
     const int n16 = lane & 15, g4 = lane >> 4;
@@ -1101,17 +1122,21 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
       const int gl = task / dsl, sl = task - gl * dsl;
       const int nj = DT / dsl;
       if (nj == DT) node_task<D, true, DT>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
-      else if (nj * 2 == DT) node_task<D, true, DT / 2>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
-      else if (nj * 4 == DT) node_task<D, true, DT / 4>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
+      else if (nj * 2 == DT) node_task<D, true, (DT >= 2 ? DT / 2 : 1)>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
+      else if (nj * 4 == DT) node_task<D, true, (DT >= 4 ? DT / 4 : 1)>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
       else node_task<D, true, (DT >= 8 ? DT / 8 : 1)>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
     }
-  } else if (w < kStageSlots) {
-    for (int gl = w; gl < ng; gl += kStageSlots) node_task<D, false, DT>(A, g, p0, rend, q0 + gl, gl, 0, kv, w, nch, qf);
+  } else if (w < LY::STAGES) {
+    // D = 256: two d-slices per group (each recomputes the same scores), so a
+    // task's accumulators and K fragments fit the registers.
+    constexpr int SL = D >= 256 ? 2 : 1;
+    for (int task = w; task < ng * SL; task += LY::STAGES)
+      node_task<D, false, DT / SL>(A, g, p0, rend, q0 + task / SL, task / SL, task % SL, kv, w, nch, qf);
   }
   lds_barrier();   // every row's partial is in NP
 }
 
-// Issues node_rows' loads of a resident segment (0 < NN <= kNodeRes kChunk,
+// Issues node_rows' loads of a resident segment (0 < NN <= RES kChunk,
 // p0 < rend): chunk c into buffer c, the mask bytes and the score fragment.
 template <int D>
 __device__ __forceinline__ void node_prefetch(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv, int w,
@@ -1121,7 +1146,7 @@ __device__ __forceinline__ void node_prefetch(const TrieAttnArgs& A, int g, int 
   // One call per chunk with a constant index into pre.mb (a rolled loop
   // would index it at run time and put `pre` in scratch memory).
   auto chunk = [&](int b) -> uint32_t {
-    if (b * kChunk >= A.NN) return 0;
+    if (b >= NodeLds<D>::RES || b * kChunk >= A.NN) return 0;
     node_issue<D>(A, g, b * kChunk, kv, b, w, nw, true);
     return node_masks(A, p0, nrd, w, b * kChunk);
   };
@@ -1131,14 +1156,19 @@ __device__ __forceinline__ void node_prefetch(const TrieAttnArgs& A, int g, int 
   node_q<D>(A, g, p0, rend, pre.qf);
 }
 
-// Final result of row r of kv head g, one row over the wave (lane l: head_dim
-// [DL l, +DL)): the group partials combined in group order, then the node
-// partial (m, l, acc); bf16 store.
+// Columns per lane when one wave merges one row (D = 32: half the wave).
+template <int D> constexpr int merge_cols() { return D >= 64 ? D / 64 : 1; }
+
+// Final result of row r of kv head g, one row over the wave (lane l < D / DL:
+// head_dim [DL l, +DL)): the group partials combined in group order, then the
+// node partial (m, l, acc); bf16 store.
 template <int D, bool COH = false>
 __device__ __forceinline__ void merge_row(const TrieAttnArgs& A, int g, int r, float m, float l,
-                                          const float (&acc)[D / 64]) {
-  constexpr int DL = D / 64;
+                                          const float (&acc)[merge_cols<D>()]) {
+  constexpr int DL = merge_cols<D>();
   const int lane = __lane_id();
+  const bool on = DL * lane < D;
+  const int ln = on ? lane : 0;   // lanes past the row read lane 0's columns and store nothing
   const RowRef R = row_ref(A, g, r, r);
   const int NG = A.NG;
   float gm[kGroupTarget], gl[kGroupTarget], ga[kGroupTarget][DL];
@@ -1149,13 +1179,17 @@ __device__ __forceinline__ void merge_row(const TrieAttnArgs& A, int g, int r, f
 #pragma unroll
   for (int qq = 0; qq < kGroupTarget; ++qq) {
     if (qq < NG) {
-      const size_t ao = (gbase + qq) * D + DL * lane;
+      const size_t ao = (gbase + qq) * D + DL * ln;
       if constexpr (COH) {
         // sc1 (cache policy 16): the coherence of an agent-scope atomic load.
         const f32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(rml, (int)((gbase + qq) * 8), 0, 16);
         gm[qq] = ml.x;
         gl[qq] = ml.y;
-        if constexpr (DL == 2) {
+        if constexpr (DL == 4) {
+          const f32x4 a = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(racc, (int)(ao * 4), 0, 16));
+#pragma unroll
+          for (int k = 0; k < 4; ++k) ga[qq][k] = a[k];
+        } else if constexpr (DL == 2) {
           const f32x2 a = __builtin_amdgcn_raw_buffer_load_b64(racc, (int)(ao * 4), 0, 16);
           ga[qq][0] = a.x;
           ga[qq][1] = a.y;
@@ -1178,8 +1212,11 @@ __device__ __forceinline__ void merge_row(const TrieAttnArgs& A, int g, int r, f
   for (int qq = 0; qq < kGroupTarget; ++qq)
     if (qq < NG) combine<DL>(fm, fl, facc, gm[qq], gl[qq], ga[qq]);
   combine<DL>(fm, fl, facc, m, l, acc);
+  if (!on) return;
   uint16_t* o = A.out + (R.hd * A.soh + R.mq * A.som + DL * lane);
-  if constexpr (DL == 2) *reinterpret_cast<uint32_t*>(o) = pack_bf16x2(facc[0] / fl, facc[1] / fl);
+  if constexpr (DL == 4)
+    *reinterpret_cast<u32x2*>(o) = u32x2{pack_bf16x2(facc[0] / fl, facc[1] / fl), pack_bf16x2(facc[2] / fl, facc[3] / fl)};
+  else if constexpr (DL == 2) *reinterpret_cast<uint32_t*>(o) = pack_bf16x2(facc[0] / fl, facc[1] / fl);
   else *o = f32_to_bf16_rne(facc[0] / fl);
 }
 
@@ -1188,8 +1225,9 @@ __device__ __forceinline__ void merge_row(const TrieAttnArgs& A, int g, int r, f
 template <int D, bool COH>
 __device__ __forceinline__ void merge_rounds(const TrieAttnArgs& A, int g, int p0, int rend, const lds_char* kv,
                                              int w) {
-  constexpr int DL = D / 64;
+  constexpr int DL = merge_cols<D>();
   const int lane = __lane_id();
+  const int ln = DL * lane < D ? lane : 0;
   const int nrd = (rend - p0 - w + kWavesA - 1) / kWavesA;
   using LY = NodeLds<D>;
   const lds_float* NP = (const lds_float*)(kv + LY::NPOFF);
@@ -1204,7 +1242,7 @@ __device__ __forceinline__ void merge_rounds(const TrieAttnArgs& A, int g, int p
       m = np[0];
       l = np[1];
 #pragma unroll
-      for (int k = 0; k < DL; ++k) acc[k] = np[4 + DL * lane + k];
+      for (int k = 0; k < DL; ++k) acc[k] = np[4 + DL * ln + k];
     }
     merge_row<D, COH>(A, g, p0 + row, m, l, acc);
   }
@@ -1212,7 +1250,7 @@ __device__ __forceinline__ void merge_rounds(const TrieAttnArgs& A, int g, int p
 
 // ------------------------------------------------------------------ kernel B
 // Workgroup (g, c8): rows [8 c8, 8 c8 + 8) of kv head g, row 8 c8 + w on
-// wave w: node partial, then merge.  A node segment of at most kNodeRes chunks
+// wave w: node partial, then merge.  A node segment of at most RES chunks
 // is loaded whole up front; a longer one streams.
 template <int D>
 __global__ __launch_bounds__(64 * kWavesA) void node_merge_kernel(TrieAttnArgs A) {
@@ -1225,7 +1263,7 @@ __global__ __launch_bounds__(64 * kWavesA) void node_merge_kernel(TrieAttnArgs A
   const int p0 = 8 * (blockIdx.x - g * RC8);
   const int rend = min(p0 + 8, A.R);
   NodePre<D> pre;
-  const bool pf = A.NN > 0 && A.NN <= kNodeRes * kChunk;
+  const bool pf = A.NN > 0 && A.NN <= LY::RES * kChunk;
   if (pf) {
     node_prefetch<D>(A, g, p0, rend, (lds_char*)kv, w, pre);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of the segment is in LDS
@@ -1239,12 +1277,14 @@ __global__ __launch_bounds__(64 * kWavesA) void node_merge_kernel(TrieAttnArgs A
 // wave w): the output of a workgroup whose wait for the group partials gave up.
 template <int D>
 __device__ __forceinline__ void nan_rows(const TrieAttnArgs& A, int g, int p0, int rend, int w) {
-  constexpr int DL = D / 64;
+  constexpr int DL = merge_cols<D>();
   const int lane = __lane_id();
+  if (DL * lane >= D) return;
   for (int r = p0 + w; r < rend; r += kWavesA) {
     const RowRef R = row_ref(A, g, r, r);
     uint16_t* o = A.out + (R.hd * A.soh + R.mq * A.som + DL * lane);
-    if constexpr (DL == 2) *reinterpret_cast<uint32_t*>(o) = 0x7fc07fc0u;
+    if constexpr (DL == 4) *reinterpret_cast<u32x2*>(o) = u32x2{0x7fc07fc0u, 0x7fc07fc0u};
+    else if constexpr (DL == 2) *reinterpret_cast<uint32_t*>(o) = 0x7fc07fc0u;
     else *o = (uint16_t)0x7fc0;
   }
 }
@@ -1299,7 +1339,7 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
 
   // A resident node segment (K/V, score fragment, mask bytes of the first
   // batch) is loaded while the group partial is being stored.
-  const bool pf = A.NN > 0 && A.NN <= kNodeRes * kChunk && r0 < rend;
+  const bool pf = A.NN > 0 && A.NN <= LY::RES * kChunk && r0 < rend;
   NodePre<D> pre;
   prompt_block<D, kRT, true>(A, lds, g, rb, q, [&] {
     if (pf) node_prefetch<D>(A, g, r0, rend0, (lds_char*)lds, w, pre);
@@ -1367,7 +1407,7 @@ static int fused_capacity();
 static int make_plan(int H, int HK, int M, int P, int NN, int D, int rows_per_wave, Plan* pl) {
   if (H <= 0 || HK <= 0 || M < 0 || P < 0 || NN < 0 || H % HK != 0) return RSPX_EINVAL;
   if (NN > kMaxNodeSlots) return RSPX_EINVAL;
-  if (D != 64 && D != 128) return RSPX_EUNSUPPORTED;
+  if (D != 32 && D != 64 && D != 128 && D != 256) return RSPX_EUNSUPPORTED;
   const int GQA = H / HK;
   if (GQA != 1 && GQA != 2 && GQA != 4 && GQA != 8 && GQA != 16) return RSPX_EUNSUPPORTED;
   pl->GQA = GQA;
@@ -1385,11 +1425,16 @@ static int make_plan(int H, int HK, int M, int P, int NN, int D, int rows_per_wa
   if (rt == 0) {
     // One 16-row tile per wave while that grid (twice as many row blocks)
     // still fits on the device at once, else two: the same bits either way.
+    // D = 256 always takes one (two tiles of 256 columns exceed the registers).
     const int nrb1 = (pl->R + 31) / 32;
-    const int cap1 = D == 128 ? fused_capacity<128, 1>() : fused_capacity<64, 1>();
-    rt = (pl->NG > 0 && HK * nrb1 * pl->NG <= cap1) ? 1 : 2;
+    const int cap1 = D == 256 ? 0
+                     : D == 128 ? fused_capacity<128, 1>()
+                     : D == 64  ? fused_capacity<64, 1>()
+                                : fused_capacity<32, 1>();
+    rt = (D == 256 || (pl->NG > 0 && HK * nrb1 * pl->NG <= cap1)) ? 1 : 2;
   }
   if (rt != 1 && rt != 2) return RSPX_EINVAL;
+  if (D == 256 && rt != 1) return RSPX_EUNSUPPORTED;
   pl->RT = rt;
   pl->NRB = (pl->R + 32 * rt - 1) / (32 * rt);
   pl->prompt_wgs = HK * pl->NRB * pl->NG;
@@ -1441,7 +1486,8 @@ static void launch_rt(const TrieAttnArgs& a, const Plan& pl, hipStream_t s, int 
 
 template <int D>
 static void launch_all(const TrieAttnArgs& a, const Plan& pl, hipStream_t s, int mode) {
-  if (pl.RT == 1) launch_rt<D, 1>(a, pl, s, mode);
+  if constexpr (D == 256) launch_rt<D, 1>(a, pl, s, mode);
+  else if (pl.RT == 1) launch_rt<D, 1>(a, pl, s, mode);
   else launch_rt<D, 2>(a, pl, s, mode);
 }
 
@@ -1510,8 +1556,12 @@ static int trie_attn_impl(const void* q, int64_t sqh, int64_t sqm, const void* k
   a.spin = g_spin_limit;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (D == 128) launch_all<128>(a, pl, s, mode);
-  else launch_all<64>(a, pl, s, mode);
+  switch (D) {
+    case 32: launch_all<32>(a, pl, s, mode); break;
+    case 64: launch_all<64>(a, pl, s, mode); break;
+    case 128: launch_all<128>(a, pl, s, mode); break;
+    default: launch_all<256>(a, pl, s, mode); break;
+  }
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }
 

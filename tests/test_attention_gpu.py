@@ -235,6 +235,46 @@ def test_gqa_and_head_dims(H, HK, D):
     assert torch.equal(_run(gen.path_case(c, i))[:, 0], full[:, i])
 
 
+HEAD_DIM_CASES = {
+    # resident node segments (at most 192 slots at D = 32, 64 at D = 256)
+    "d32": lambda: gen.attn_case(7, 8, 2, 32, 700, 3, 9, 0, 6, None),
+    "d256": lambda: gen.attn_case(8, 16, 8, 256, 900, 3, 10, 0, 6, None, kv_scale=256 ** -0.5),
+    # streamed node segments
+    "d32_b200": lambda: gen.attn_case(9, 8, 2, 32, 1500, 3, 12, 0, 6, None, base=200),
+    "d256_b60": lambda: gen.attn_case(10, 16, 8, 256, 1200, 3, 12, 0, 6, None, kv_scale=256 ** -0.5, base=60),
+    # 8B-like trie at D = 256 (512 prompt workgroups: two launches) and a
+    # 128-node trie at D = 32 (two row tiles per wave)
+    "d256_n64": lambda: gen.attn_case(11, 32, 8, 256, 3072, 4, 24, 0, 16, 64, kv_scale=256 ** -0.5),
+    "d32_n128": lambda: gen.attn_case(12, 32, 8, 32, 3072, 8, 32, 0, 32, 128, kv_scale=32 ** -0.5),
+}
+
+
+@pytest.mark.parametrize("which", list(HEAD_DIM_CASES))
+def test_head_dims_32_and_256(which):
+    """head_dim 32 and 256 (the other sizes the reference's kernels take): per-element
+    parity with the kernel-tree restatement and the fp64 bound, trie rows bitwise equal
+    to their 1-token calls, and the same bits from one and two launches and (D = 32)
+    from one and two row tiles per wave.  D = 256 runs one row tile per wave only."""
+    from respect_amd import _lib
+    c = HEAD_DIM_CASES[which]()
+    H, M, D = c.q.shape
+    print(f"[head_dim] {which} M={M} NN={c.kn.shape[1]}", flush=True)
+    full = _run(c)
+    _check_parity(c, full)
+    n = len(c.tree.nodes)
+    for i in sorted({0, n // 2, n - 1}):
+        assert torch.equal(_run(gen.path_case(c, i))[:, 0], full[:, i])
+    assert torch.equal(_run(c, launches=2), full)
+    assert torch.equal(_run(c, launches=1), full)
+    if D == 32:
+        assert torch.equal(_run(c, rows_per_wave=1), full)
+        assert torch.equal(_run(c, rows_per_wave=2), full)
+    else:
+        assert torch.equal(_run(c, rows_per_wave=1), full)
+        with pytest.raises(_lib.RspxError):
+            _run(c, rows_per_wave=2)
+
+
 def test_no_node_slots_and_no_prompt():
     c = gen.cfg1()
     # NN = 0: prompt only
