@@ -1318,39 +1318,31 @@ constexpr int kSpinLimit = 1 << 22;
 static int g_spin_limit = kSpinLimit;
 constexpr int kSyncWords = 4096;   // timeout flag + [HK][NRB][2] counters
 
+// Rows [r0, rend) merged by workgroup (g, rb, q) of a fused launch: its share
+// of the row block, a multiple of 4 rows.
+template <int kRT>
+__device__ __forceinline__ void merge_share(const TrieAttnArgs& A, int rb, int q, int& r0, int& rend) {
+  const int rows_blk = 32 * kRT;
+  const int rpw = 4 * ((rows_blk / 4 + A.NG - 1) / A.NG);
+  r0 = rb * rows_blk + q * rpw;
+  rend = min(rb * rows_blk + min(rows_blk, (q + 1) * rpw), A.R);
+}
+
+// After workgroup (g, rb, q) has counted its group partial of row block rb:
+// the node partials of its merge rows in batches of at most kNodeRows (the
+// first batch while the block's other workgroups finish, then the bounded
+// wait), the merge, and the block's counters back to zero once every
+// workgroup of the block is past its wait.  pre / pf: node_rows' first batch.
 template <int D, int kRT>
-__global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
+__device__ __forceinline__ void block_tail(const TrieAttnArgs& A, char* lds, int g, int rb, int q,
+                                           const NodePre<D>& pre, bool pf) {
   using LY = NodeLds<D>;
-  constexpr int LB = PromptLds<D, kRT>::BYTES > LY::BYTES + 16 ? PromptLds<D, kRT>::BYTES : LY::BYTES + 16;
-  static_assert(LY::BYTES + 16 <= PromptLds<D, kRT>::RINGBYTES, "node LDS and the wait flag inside the ring");
-  __shared__ __attribute__((aligned(16))) char lds[LB];
   const int lane = __lane_id();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g = blockIdx.x % A.HK;
-  const int rest = blockIdx.x / A.HK;
-  const int rb = rest % A.NRB;
-  const int q = rest / A.NRB;
   int* cnt = A.sync + 1 + 2 * (g * A.NRB + rb);
-  const int rows_blk = 32 * kRT;
-  const int rpw = 4 * ((rows_blk / 4 + A.NG - 1) / A.NG);   // rows merged per workgroup (multiple of 4)
-  const int r0 = rb * rows_blk + q * rpw;
-  const int rend = min(rb * rows_blk + min(rows_blk, (q + 1) * rpw), A.R);
-  const int rend0 = min(rend, r0 + kNodeRows);               // the first batch of node rows
-
-  // A resident node segment (K/V, score fragment, mask bytes of the first
-  // batch) is loaded while the group partial is being stored.
-  const bool pf = A.NN > 0 && A.NN <= LY::RES * kChunk && r0 < rend;
-  NodePre<D> pre;
-  prompt_block<D, kRT, true>(A, lds, g, rb, q, [&] {
-    if (pf) node_prefetch<D>(A, g, r0, rend0, (lds_char*)lds, w, pre);
-  });
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
-  lds_barrier();
-  if (threadIdx.x == 0) __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-
-  // Node rows in batches of at most kNodeRows: the first batch's partials are
-  // computed while the other workgroups of the block finish, then the wait.
+  int r0, rend;
+  merge_share<kRT>(A, rb, q, r0, rend);
+  const int rend0 = min(rend, r0 + kNodeRows);
   int* gave_up = reinterpret_cast<int*>(lds + LY::BYTES);  // one LDS word past the node areas
   if (r0 < rend) {
     node_rows<D>(A, g, r0, rend0, (lds_char*)lds, w, pre, pf);
@@ -1391,6 +1383,69 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   }
 }
 
+// The group partial is complete in memory (each wave waited for its own
+// stores): count it in the row block's counter.
+__device__ __forceinline__ void count_partial(const TrieAttnArgs& A, int g, int rb) {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
+  lds_barrier();
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(A.sync + 1 + 2 * (g * A.NRB + rb), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int D, int kRT>
+__global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
+  using LY = NodeLds<D>;
+  constexpr int LB = PromptLds<D, kRT>::BYTES > LY::BYTES + 16 ? PromptLds<D, kRT>::BYTES : LY::BYTES + 16;
+  static_assert(LY::BYTES + 16 <= PromptLds<D, kRT>::RINGBYTES, "node LDS and the wait flag inside the ring");
+  __shared__ __attribute__((aligned(16))) char lds[LB];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = blockIdx.x % A.HK;
+  const int rest = blockIdx.x / A.HK;
+  const int rb = rest % A.NRB;
+  const int q = rest / A.NRB;
+  int r0, rend;
+  merge_share<kRT>(A, rb, q, r0, rend);
+  const int rend0 = min(rend, r0 + kNodeRows);               // the first batch of node rows
+
+  // A resident node segment (K/V, score fragment, mask bytes of the first
+  // batch) is loaded while the group partial is being stored.
+  const bool pf = A.NN > 0 && A.NN <= LY::RES * kChunk && r0 < rend;
+  NodePre<D> pre;
+  prompt_block<D, kRT, true>(A, lds, g, rb, q, [&] {
+    if (pf) node_prefetch<D>(A, g, r0, rend0, (lds_char*)lds, w, pre);
+  });
+  count_partial(A, g, rb);
+  block_tail<D, kRT>(A, lds, g, rb, q, pre, pf);
+}
+
+// The same work as fused_kernel for grids twice as large as the device holds
+// at once (e.g. 128-node tries at 8B heads: 512 rows per kv head): workgroup
+// (g, rbw, q) runs the prompt groups of row blocks rbw and rbw + NRBW
+// (NRBW = ceil(NRB / 2)) one after the other, counting each, then the node
+// partials and merges of both.  Every count precedes every wait, so the waits
+// end as in fused_kernel; the arithmetic of every row is the same: the same
+// bits.
+template <int D, int kRT>
+__global__ __launch_bounds__(512) void fused2_kernel(TrieAttnArgs A) {
+  using LY = NodeLds<D>;
+  constexpr int LB = PromptLds<D, kRT>::BYTES > LY::BYTES + 16 ? PromptLds<D, kRT>::BYTES : LY::BYTES + 16;
+  __shared__ __attribute__((aligned(16))) char lds[LB];
+  const int g = blockIdx.x % A.HK;
+  const int rest = blockIdx.x / A.HK;
+  const int NRBW = (A.NRB + 1) / 2;
+  const int rbw = rest % NRBW;
+  const int q = rest / NRBW;
+  const int nb = rbw + NRBW < A.NRB ? 2 : 1;
+  for (int b = 0; b < nb; ++b) {
+    const int rb = rbw + NRBW * b;
+    prompt_block<D, kRT, true>(A, lds, g, rb, q, [] {});
+    count_partial(A, g, rb);
+  }
+  NodePre<D> none;
+  for (int b = 0; b < nb; ++b) block_tail<D, kRT>(A, lds, g, rbw + NRBW * b, q, none, false);
+}
+
 // ------------------------------------------------------------------ host side
 
 struct Plan {
@@ -1400,7 +1455,7 @@ struct Plan {
 
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-template <int D, int RT>
+template <int D, int RT, bool TWO = false>
 static int fused_capacity();
 
 // Steps per group S = 4 NR and the group count NG <= 8 depend on P only.
@@ -1451,8 +1506,9 @@ static int make_plan(int H, int HK, int M, int P, int NN, int D, int rows_per_wa
   return RSPX_OK;
 }
 
-// Workgroups of fused_kernel<D, RT> the device holds at once (0 if unknown).
-template <int D, int RT>
+// Workgroups of fused_kernel<D, RT> (TWO: fused2_kernel<D, RT>) the device
+// holds at once (0 if unknown).
+template <int D, int RT, bool TWO>
 static int fused_capacity() {
   static int cap[64];
   static bool done[64];
@@ -1460,8 +1516,10 @@ static int fused_capacity() {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   if (!done[dev]) {
     int a = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, fused_kernel<D, RT>, 64 * kWavesA, 0) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    hipError_t e;
+    if constexpr (TWO) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, fused2_kernel<D, RT>, 64 * kWavesA, 0);
+    else e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, fused_kernel<D, RT>, 64 * kWavesA, 0);
+    if (e != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
       a = cus = 0;
     }
     cap[dev] = a * cus;
@@ -1473,11 +1531,17 @@ static int fused_capacity() {
 
 template <int D, int RT>
 static void launch_rt(const TrieAttnArgs& a, const Plan& pl, hipStream_t s, int mode) {
-  const bool fused = pl.NG > 0 && mode != 2 && 1 + 2 * pl.NRB * a.HK <= kSyncWords &&
-                     (size_t)a.HK * pl.R * pl.NG * D * sizeof(float) < (size_t(1) << 31) &&
-                     pl.prompt_wgs <= fused_capacity<D, RT>();
-  if (fused) {
+  const bool one = pl.NG > 0 && mode != 2 && 1 + 2 * pl.NRB * a.HK <= kSyncWords &&
+                   (size_t)a.HK * pl.R * pl.NG * D * sizeof(float) < (size_t(1) << 31);
+  const int cap = one ? fused_capacity<D, RT>() : 0;
+  if (one && pl.prompt_wgs <= cap) {
     hipLaunchKernelGGL((fused_kernel<D, RT>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);
+    return;
+  }
+  // Two row blocks per workgroup (fused2_kernel) when that grid fits.
+  const int wgs2 = a.HK * ((pl.NRB + 1) / 2) * pl.NG;
+  if (one && pl.NRB > 1 && wgs2 <= fused_capacity<D, RT, true>()) {
+    hipLaunchKernelGGL((fused2_kernel<D, RT>), dim3(wgs2), dim3(64 * kWavesA), 0, s, a);
     return;
   }
   if (pl.prompt_wgs > 0) hipLaunchKernelGGL((prompt_kernel<D, RT>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);

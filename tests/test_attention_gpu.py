@@ -319,13 +319,14 @@ def _status(case, ws):
 
 
 @pytest.mark.parametrize("which", ["cfg1", "cfg2", "base37", "base100", "n64b40", "long", "gqa2", "d64",
-                                   "d64b90"])
+                                   "d64b90", "n128b70"])
 def test_one_and_two_launches_equal(which):
     """The one-kernel path (prompt groups, node partials and merge with workgroups
     waiting on per-row-block counters) and the two-kernel path give the same
     bits; the counters are back at zero after each call (repeat calls on one
     workspace stay equal) and no wait ran out.  base100 / n64b40 / d64b90 put
-    65-128 slots in the node segment (two chunks, loaded whole by both paths)."""
+    65-128 slots in the node segment (two chunks, loaded whole by both paths); long /
+    n128b70 have 512 rows per kv head, two row blocks per workgroup in one launch."""
     from respect_amd import _lib
     c = {"cfg1": gen.cfg1, "cfg2": gen.cfg2, "base37": lambda: gen.cfg2(seed=4, base=37),
          "base100": lambda: gen.cfg2(seed=4, base=100),
@@ -333,7 +334,9 @@ def test_one_and_two_launches_equal(which):
          "long": lambda: gen.attn_case(8, 32, 8, 128, 16384, 8, 32, 0, 32, 128, kv_scale=128 ** -0.5),
          "gqa2": lambda: gen.attn_case(7, 16, 8, 128, 700, 3, 9, 0, 6, None),
          "d64": lambda: gen.attn_case(7, 16, 2, 64, 3086, 3, 9, 0, 6, None),
-         "d64b90": lambda: gen.attn_case(7, 16, 2, 64, 3086, 3, 9, 0, 6, None, base=90)}[which]()
+         "d64b90": lambda: gen.attn_case(7, 16, 2, 64, 3086, 3, 9, 0, 6, None, base=90),
+         "n128b70": lambda: gen.attn_case(10, 32, 8, 128, 3072, 8, 32, 0, 32, 128, kv_scale=128 ** -0.5,
+                                          base=70)}[which]()
     print(f"[one/two launches] {which} NN={c.kn.shape[1]}", flush=True)
     H, M, D = c.q.shape
     HK, P, _ = c.kp.shape
@@ -388,7 +391,7 @@ def test_one_launch_workspace_shared_by_shapes():
     assert _status(cases[0], ws) == 0
 
 
-@pytest.mark.parametrize("which", ["cfg2", "cfg1"])
+@pytest.mark.parametrize("which", ["cfg2", "cfg1", "n128"])
 def test_wait_that_gives_up_poisons_its_rows(which):
     """One-launch path with the counter wait forced to give up at once (the spin limit
     lowered through the test hook, so every workgroup still exits normally): every row
@@ -397,7 +400,9 @@ def test_wait_that_gives_up_poisons_its_rows(which):
     default limit restored the same workspace gives the two-launch bits again (the
     counters were left at zero)."""
     from respect_amd import _lib
-    c = gen.cfg2(seed=6) if which == "cfg2" else gen.cfg1()
+    c = {"cfg2": lambda: gen.cfg2(seed=6), "cfg1": gen.cfg1,
+         # 512 rows per kv head: two row blocks per workgroup in the one-launch path
+         "n128": lambda: gen.attn_case(9, 32, 8, 128, 3072, 8, 32, 0, 32, 128, kv_scale=128 ** -0.5)}[which]()
     H, M, D = c.q.shape
     HK, P, _ = c.kp.shape
     L = _lib.lib()
