@@ -647,9 +647,37 @@ template <int D> struct NodeLds {
   static constexpr int ZOFF = TOFF + kWavesA * kRankTab * 2;
   static constexpr int CNTOFF = ZOFF + 2 * D;
   static constexpr int BYTES = CNTOFF + kNodeRows * 4;
+  static constexpr int TGOFF = MWOFF;             // rank -> slot tables of a resident segment
   static __device__ __forceinline__ lds_char* kbuf(lds_char* kv, int b) { return kv + KOFF + b * CB; }
   static __device__ __forceinline__ lds_char* vbuf(lds_char* kv, int b) { return kv + VOFF + b * CB; }
 };
+
+template <int D> struct VResLds;
+
+// Node LDS of a V-resident segment (RES < chunks <= VRES): only V stays in
+// LDS (VRES chunks), the scores come from K fragments loaded into registers.
+// The same roles and row layouts as NodeLds with VRES resident chunks.
+template <int D> struct VResLds {
+  static constexpr int RES = D <= 128 ? 5 : 1;    // chunks of the segment (320 slots up to D = 128; none at 256)
+  static constexpr int CB = kChunk * 2 * D;
+  static constexpr int VOFF = 0;
+  static constexpr int SR = RES * kChunk + 4;
+  static constexpr int SOFF = RES * CB;
+  static constexpr int NPROW = D + 4;
+  static constexpr int NPOFF = SOFF + kNodeRows * SR * 4;
+  static constexpr int TGOFF = NPOFF + kNodeRows * NPROW * 4;
+  static constexpr int ZOFF = TGOFF + kNodeRows * RES * kChunk * 2;
+  static constexpr int CNTOFF = ZOFF + 2 * D;
+  static constexpr int BYTES = CNTOFF + kNodeRows * 4;
+  // Unused by a resident segment (streaming only), kept for node_task's signature.
+  static constexpr int MWOFF = 0, TOFF = 0, KOFF = 0, STAGE = 0;
+  static __device__ __forceinline__ lds_char* vbuf(lds_char* kv, int b) { return kv + VOFF + b * CB; }
+};
+
+// Bytes of LDS the node phase may use (either layout).
+template <int D> constexpr int node_area_bytes() {
+  return NodeLds<D>::BYTES > VResLds<D>::BYTES ? NodeLds<D>::BYTES : VResLds<D>::BYTES;
+}
 
 // Where a row's result goes: row r of kv head g is query r / GQA of head
 // g GQA + r % GQA.  Rows past R shadow a valid row and are never stored.
@@ -808,10 +836,9 @@ __device__ __forceinline__ void rank_fill(int& rc, int& rbase, int upto, int nch
 // the tile's slots (the chain of node_scores: the same bits) with K straight
 // from memory, p = 2^(s - m), and the tile's 32 V rows are copied by rank into
 // this wave's stage.
-template <int D, bool RES, int NJ>
+template <int D, bool RES, int NJ, class LY = NodeLds<D>>
 __device__ __forceinline__ void node_task(const TrieAttnArgs& A, int g, int p0, int rend, int mq, int gl, int sl,
                                           lds_char* kv, int w, int nch, const bf16x8 (&qf)[D / 32]) {
-  using LY = NodeLds<D>;
   constexpr int DQ = D / 32, RB = 2 * D;
   const int lane = __lane_id();
   const int n16 = lane & 15, g4 = lane >> 4, e4 = n16 >> 2, c4 = n16 & 3;
@@ -851,7 +878,7 @@ __device__ __forceinline__ void node_task(const TrieAttnArgs& A, int g, int p0, 
       // the group's rank -> slot table: four consecutive ranks per read.
       const f32x4 pa = *(const lds_f32x4*)(Srow + r0 + 4 * g4);
       const f32x4 pb = *(const lds_f32x4*)(Srow + r0 + 16 + 4 * g4);
-      const lds_i16* tg = (const lds_i16*)(kv + LY::MWOFF) + gl * LY::RES * kChunk;
+      const lds_i16* tg = (const lds_i16*)(kv + LY::TGOFF) + gl * LY::RES * kChunk;
       uint64_t t4[2];
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh)
@@ -945,6 +972,77 @@ __device__ __forceinline__ void node_task(const TrieAttnArgs& A, int g, int p0, 
   }
 }
 
+// The per-row pass of a resident segment, rows p0 + w + 8 i (i < nrd) of this
+// wave, after the scores S of every resident chunk are in LDS: m (the exact
+// maximum over the row's allowed slots) into NP, then p = 2^(s - m) of the
+// allowed slots written by rank over the row's own scores (rank <= slot: every
+// score is in registers first); the group's first row writes its rank -> slot
+// table and count.  mb[c]: the rows' mask bytes of chunk c (byte i: round i).
+template <int D, class LY>
+__device__ __forceinline__ void node_rank_rows(const TrieAttnArgs& A, int p0, int nrd, lds_char* kv, int w, int nch,
+                                               const uint32_t (&mb)[LY::RES]) {
+  constexpr int nw = kWavesA;
+  const int lane = __lane_id();
+  const int GQA = 1 << A.GQS;
+  const int q0 = p0 >> A.GQS;
+  lds_float* S = (lds_float*)(kv + LY::SOFF);
+  lds_float* NP = (lds_float*)(kv + LY::NPOFF);
+  lds_i16* TG = (lds_i16*)(kv + LY::TGOFF);
+#pragma unroll 1
+  for (int i = 0; i < nrd; ++i) {
+    const int row = w + nw * i;
+    const int r = p0 + row;
+    const bool lead = r == p0 || (r & (GQA - 1)) == 0;
+    const int gl = (r >> A.GQS) - q0;
+    float sc[LY::RES];
+    bool ok[LY::RES];
+    float x = kNegInf;
+#pragma unroll
+    for (int c = 0; c < LY::RES; ++c) {
+      ok[c] = c < nch && ((mb[c] >> (8 * i)) & 0xff) != 0;
+      sc[c] = c < nch ? S[row * LY::SR + kChunk * c + lane] : 0.f;
+      x = fmaxf(x, ok[c] ? sc[c] : kNegInf);
+    }
+    const float m = max64(x);
+    if (lane == 0) NP[row * LY::NPROW] = m;
+    int base = 0;
+#pragma unroll
+    for (int c = 0; c < LY::RES; ++c) {
+      if (c < nch) {
+        const uint64_t mm = __builtin_amdgcn_ballot_w64(ok[c]);
+        const int rk = base + lanes_below(mm);
+        if (ok[c]) {
+          S[row * LY::SR + rk] = fexp2(sc[c] - m);
+          if (lead) TG[gl * LY::RES * kChunk + rk] = (int16_t)(kChunk * c + lane);
+        }
+        base += __builtin_popcountll(mm);
+      }
+    }
+    if (lead && lane == 0) *(lds_u32*)(kv + LY::CNTOFF + 4 * gl) = (uint32_t)base;
+  }
+}
+
+// The node sums of a resident segment for rows [p0, rend): (group, d-slice)
+// tasks over the waves, at most two per wave.
+template <int D, class LY>
+__device__ __forceinline__ void node_res_tasks(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv, int w,
+                                               int nch, const bf16x8 (&qf)[D / 32]) {
+  constexpr int nw = kWavesA;
+  constexpr int DT = D / 16;
+  const int q0 = p0 >> A.GQS;
+  const int ng = ((rend - 1) >> A.GQS) - q0 + 1;  // groups of rows (one query each)
+  const int ds = ng >= 8 ? 1 : ng >= 4 ? 2 : ng >= 2 ? 4 : 8;
+  const int dsl = ds < DT ? ds : DT;
+  for (int task = w; task < ng * dsl; task += nw) {
+    const int gl = task / dsl, sl = task - gl * dsl;
+    const int nj = DT / dsl;
+    if (nj == DT) node_task<D, true, DT, LY>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
+    else if (nj * 2 == DT) node_task<D, true, (DT >= 2 ? DT / 2 : 1), LY>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
+    else if (nj * 4 == DT) node_task<D, true, (DT >= 4 ? DT / 4 : 1), LY>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
+    else node_task<D, true, (DT >= 8 ? DT / 8 : 1), LY>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
+  }
+}
+
 // Node partials of rows [p0, rend) of kv head g (at most kNodeRows) over each
 // row's allowed node slots (attention.py:52-67): m is the exact maximum score
 // over the allowed slots; the sums run over the allowed slots in slot order
@@ -959,17 +1057,19 @@ __device__ __forceinline__ void node_task(const TrieAttnArgs& A, int g, int p0, 
 // caller did not issue is loaded here; a longer one streams: its maxima come
 // from a pass over K chunk by chunk, its sums from K and V gathered by rank.
 template <int D>
-__device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv, int w,
-                                          const NodePre<D>& pre, bool have_pre) {
+__device__ __forceinline__ const lds_float* node_rows(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv,
+                                                     int w, const NodePre<D>& pre, bool have_pre) {
   using LY = NodeLds<D>;
   constexpr int nw = kWavesA;
   constexpr int DT = D / 16;
   const int lane = __lane_id();
   const int NN = A.NN;
-  if (NN == 0) return;
+  if (NN == 0) return (const lds_float*)(kv + LY::NPOFF);
   const int nrd = (rend - p0 - w + nw - 1) / nw;   // rows of this wave: p0 + w + 8 i
   const int nch = (NN + kChunk - 1) / kChunk;
   const bool res = NN <= LY::RES * kChunk;
+  constexpr bool kVRes = VResLds<D>::RES > LY::RES;
+  const bool vres = kVRes && !res && NN <= VResLds<D>::RES * kChunk;
   lds_float* S = (lds_float*)(kv + LY::SOFF);
   lds_float* NP = (lds_float*)(kv + LY::NPOFF);
   const int GQA = 1 << A.GQS;
@@ -1024,42 +1124,56 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
       for (int b = 4 * lane; b < 2 * D; b += 256) *(lds_u32*)(kv + LY::ZOFF + b) = 0u;
     }
     lds_barrier();
-    // Per row: m, then p = 2^(s - m) of the allowed slots written by rank over
-    // the row's own scores (rank <= slot: every score is in registers first);
-    // the group's first row writes its rank -> slot table and count.
-    lds_i16* TG = (lds_i16*)(kv + LY::MWOFF);
-#pragma unroll 1
-    for (int i = 0; i < nrd; ++i) {
-      const int row = w + nw * i;
-      const int r = p0 + row;
-      const bool lead = r == p0 || (r & (GQA - 1)) == 0;
-      const int gl = (r >> A.GQS) - q0;
-      float sc[LY::RES];
-      bool ok[LY::RES];
-      float x = kNegInf;
+    node_rank_rows<D, LY>(A, p0, nrd, kv, w, nch, mb);
+  } else if (kVRes && vres) {
+    using VL = VResLds<D>;
+    // V-resident: every chunk's V rows DMA'd into LDS, the scores of the
+    // wave's 16-slot tiles (w, w + 8, ...) from K fragments loaded into
+    // registers -- all loads issued before the first wait.
+    constexpr int DQ = D / 32, RB = 2 * D, VX = VL::CB / 1024;
+    constexpr int MT = (VL::RES * kChunk / 16 + nw - 1) / nw;   // tiles per wave
+    const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(A.kn + g * A.sknh, 2 * ((NN - 1) * A.sknn + D));
+    const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(A.vn + g * A.svnh, 2 * ((NN - 1) * A.svnn + D));
+    const int n16 = lane & 15, g4 = lane >> 4;
+    const int nt = (NN + 15) / 16;
+    u32x4 kf[MT][DQ];
 #pragma unroll
-      for (int c = 0; c < LY::RES; ++c) {
-        ok[c] = c < nch && ((mb[c] >> (8 * i)) & 0xff) != 0;
-        sc[c] = c < nch ? S[row * LY::SR + kChunk * c + lane] : 0.f;
-        x = fmaxf(x, ok[c] ? sc[c] : kNegInf);
-      }
-      const float m = max64(x);
-      if (lane == 0) NP[row * LY::NPROW] = m;
-      int base = 0;
+    for (int j = 0; j < MT; ++j) {
+      const int slot = 16 * (w + nw * j) + n16;   // slots past NN read zeros
 #pragma unroll
-      for (int c = 0; c < LY::RES; ++c) {
-        if (c < nch) {
-          const uint64_t mm = __builtin_amdgcn_ballot_w64(ok[c]);
-          const int rk = base + lanes_below(mm);
-          if (ok[c]) {
-            S[row * LY::SR + rk] = fexp2(sc[c] - m);
-            if (lead) TG[gl * LY::RES * kChunk + rk] = (int16_t)(kChunk * c + lane);
-          }
-          base += __builtin_popcountll(mm);
-        }
-      }
-      if (lead && lane == 0) *(lds_u32*)(kv + LY::CNTOFF + 4 * gl) = (uint32_t)base;
+      for (int i = 0; i < DQ; ++i)
+        kf[j][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rk, w + nw * j < nt ? 2 * (slot * A.sknn + 32 * i + 8 * g4) : 0x7ffffff0,
+                                                  0, 0));
     }
+    for (int x = w; x < nch * VX; x += nw) {
+      const int c = x / VX;
+      const int byte = (x - c * VX) * 1024 + 16 * lane;
+      const int row = byte / RB, u = (byte % RB) / 16;
+      bdma16(rv, 2 * (kChunk * c + row) * A.svnn + 16 * (u ^ vswz<D>(row)), VL::vbuf(kv, c) + (x - c * VX) * 1024);
+    }
+    uint32_t mb[VL::RES];
+#pragma unroll
+    for (int c = 0; c < VL::RES; ++c) mb[c] = c < nch ? node_masks(A, p0, nrd, w, kChunk * c) : 0u;
+    lds_float* SV = (lds_float*)(kv + VL::SOFF);
+#pragma unroll
+    for (int j = 0; j < MT; ++j) {
+      const int tt = w + nw * j;
+      if (tt < nt) {
+        f32x4 sv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < DQ; ++i)
+          sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[j][i]), qf[i], sv, 0, 0, 0);
+        // Lane (n16, g4), element j: slot 16 tt + 4 g4 + j of row p0 + n16 (the chain of node_scores).
+        *(lds_f32x4*)(SV + n16 * VL::SR + 16 * tt + 4 * g4) = sv * A.c;
+      }
+    }
+    if (w == 0) {
+      for (int b = 4 * lane; b < 2 * D; b += 256) *(lds_u32*)(kv + VL::ZOFF + b) = 0u;
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's V rows
+    lds_barrier();
+    node_rank_rows<D, VL>(A, p0, nrd, kv, w, nch, mb);
   } else {
     // Streaming: the scores of up to SUP slots at a time into the KB / VB area
     // ([row][SUP + 4] fp32), from K fragments loaded straight into registers
@@ -1115,17 +1229,9 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
   lds_barrier();   // scores, maxima, mask words and counts visible; KB / VB free when streaming
 
   if (res) {
-    // (group, d-slice) tasks over the waves, at most two per wave.
-    const int ds = ng >= 8 ? 1 : ng >= 4 ? 2 : ng >= 2 ? 4 : 8;
-    const int dsl = ds < DT ? ds : DT;
-    for (int task = w; task < ng * dsl; task += nw) {
-      const int gl = task / dsl, sl = task - gl * dsl;
-      const int nj = DT / dsl;
-      if (nj == DT) node_task<D, true, DT>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
-      else if (nj * 2 == DT) node_task<D, true, (DT >= 2 ? DT / 2 : 1)>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
-      else if (nj * 4 == DT) node_task<D, true, (DT >= 4 ? DT / 4 : 1)>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
-      else node_task<D, true, (DT >= 8 ? DT / 8 : 1)>(A, g, p0, rend, q0 + gl, gl, sl, kv, w, nch, qf);
-    }
+    node_res_tasks<D, LY>(A, g, p0, rend, kv, w, nch, qf);
+  } else if (kVRes && vres) {
+    node_res_tasks<D, VResLds<D>>(A, g, p0, rend, kv, w, nch, qf);
   } else if (w < LY::STAGES) {
     // D = 256: two d-slices per group (each recomputes the same scores), so a
     // task's accumulators and K fragments fit the registers.
@@ -1134,6 +1240,7 @@ __device__ __forceinline__ void node_rows(const TrieAttnArgs& A, int g, int p0, 
       node_task<D, false, DT / SL>(A, g, p0, rend, q0 + task / SL, task / SL, task % SL, kv, w, nch, qf);
   }
   lds_barrier();   // every row's partial is in NP
+  return (const lds_float*)(kv + (vres ? VResLds<D>::NPOFF : LY::NPOFF));
 }
 
 // Issues node_rows' loads of a resident segment (0 < NN <= RES kChunk,
@@ -1220,17 +1327,17 @@ __device__ __forceinline__ void merge_row(const TrieAttnArgs& A, int g, int r, f
   else *o = f32_to_bf16_rne(facc[0] / fl);
 }
 
-// The node partial of wave w's round i, left in LDS by node_rows (empty when
-// there are no node slots), merged into row p0 + w + 8 i.
+// The node partial of wave w's round i, left in LDS by node_rows in the rows
+// NP[i][D + 4] = (m, l, pad, pad, acc) (empty when there are no node slots),
+// merged into row p0 + w + 8 i.
 template <int D, bool COH>
-__device__ __forceinline__ void merge_rounds(const TrieAttnArgs& A, int g, int p0, int rend, const lds_char* kv,
+__device__ __forceinline__ void merge_rounds(const TrieAttnArgs& A, int g, int p0, int rend, const lds_float* NP,
                                              int w) {
   constexpr int DL = merge_cols<D>();
   const int lane = __lane_id();
   const int ln = DL * lane < D ? lane : 0;
   const int nrd = (rend - p0 - w + kWavesA - 1) / kWavesA;
   using LY = NodeLds<D>;
-  const lds_float* NP = (const lds_float*)(kv + LY::NPOFF);
 #pragma unroll 1
   for (int i = 0; i < nrd; ++i) {
     const int row = w + kWavesA * i;
@@ -1256,7 +1363,7 @@ template <int D>
 __global__ __launch_bounds__(64 * kWavesA) void node_merge_kernel(TrieAttnArgs A) {
   using LY = NodeLds<D>;
   static_assert(8 <= kNodeRows, "a workgroup's rows fit the node areas");
-  __shared__ __attribute__((aligned(16))) char kv[LY::BYTES];
+  __shared__ __attribute__((aligned(16))) char kv[node_area_bytes<D>()];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int RC8 = (A.R + 7) / 8;
   const int g = blockIdx.x / RC8;
@@ -1269,8 +1376,8 @@ __global__ __launch_bounds__(64 * kWavesA) void node_merge_kernel(TrieAttnArgs A
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of the segment is in LDS
     lds_barrier();                       // and every other wave's part
   }
-  node_rows<D>(A, g, p0, rend, (lds_char*)kv, w, pre, pf);
-  merge_rounds<D, false>(A, g, p0, rend, (const lds_char*)kv, w);
+  const lds_float* np = node_rows<D>(A, g, p0, rend, (lds_char*)kv, w, pre, pf);
+  merge_rounds<D, false>(A, g, p0, rend, np, w);
 }
 
 // NaN in every element of rows [p0, rend) of kv head g (row p0 + w + 8 i on
@@ -1343,9 +1450,9 @@ __device__ __forceinline__ void block_tail(const TrieAttnArgs& A, char* lds, int
   int r0, rend;
   merge_share<kRT>(A, rb, q, r0, rend);
   const int rend0 = min(rend, r0 + kNodeRows);
-  int* gave_up = reinterpret_cast<int*>(lds + LY::BYTES);  // one LDS word past the node areas
+  int* gave_up = reinterpret_cast<int*>(lds + node_area_bytes<D>());  // one LDS word past the node areas
   if (r0 < rend) {
-    node_rows<D>(A, g, r0, rend0, (lds_char*)lds, w, pre, pf);
+    const lds_float* np = node_rows<D>(A, g, r0, rend0, (lds_char*)lds, w, pre, pf);
     if (w == 0) {
       int v = 0;
       for (int it = 0; it < A.spin; ++it) {
@@ -1362,14 +1469,14 @@ __device__ __forceinline__ void block_tail(const TrieAttnArgs& A, char* lds, int
     lds_barrier();
     const bool bad = __builtin_amdgcn_readfirstlane(*gave_up);
     if (bad) nan_rows<D>(A, g, r0, rend0, w);
-    else merge_rounds<D, true>(A, g, r0, rend0, (const lds_char*)lds, w);
+    else merge_rounds<D, true>(A, g, r0, rend0, np, w);
     // Further batches (short prompts: few key groups, many rows per workgroup).
     for (int b0 = rend0; b0 < rend; b0 += kNodeRows) {
       const int be = min(rend, b0 + kNodeRows);
       NodePre<D> none;
-      node_rows<D>(A, g, b0, be, (lds_char*)lds, w, none, false);
+      const lds_float* npb = node_rows<D>(A, g, b0, be, (lds_char*)lds, w, none, false);
       if (bad) nan_rows<D>(A, g, b0, be, w);
-      else merge_rounds<D, true>(A, g, b0, be, (const lds_char*)lds, w);
+      else merge_rounds<D, true>(A, g, b0, be, npb, w);
     }
   }
   // Counters back to zero once every workgroup of the block is past its wait.
@@ -1396,8 +1503,9 @@ __device__ __forceinline__ void count_partial(const TrieAttnArgs& A, int g, int 
 template <int D, int kRT>
 __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   using LY = NodeLds<D>;
-  constexpr int LB = PromptLds<D, kRT>::BYTES > LY::BYTES + 16 ? PromptLds<D, kRT>::BYTES : LY::BYTES + 16;
-  static_assert(LY::BYTES + 16 <= PromptLds<D, kRT>::RINGBYTES, "node LDS and the wait flag inside the ring");
+  constexpr int NB = node_area_bytes<D>() + 16;
+  constexpr int LB = PromptLds<D, kRT>::BYTES > NB ? PromptLds<D, kRT>::BYTES : NB;
+  static_assert(NB <= PromptLds<D, kRT>::RINGBYTES, "node LDS and the wait flag inside the ring");
   __shared__ __attribute__((aligned(16))) char lds[LB];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = blockIdx.x % A.HK;
@@ -1429,7 +1537,8 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
 template <int D, int kRT>
 __global__ __launch_bounds__(512) void fused2_kernel(TrieAttnArgs A) {
   using LY = NodeLds<D>;
-  constexpr int LB = PromptLds<D, kRT>::BYTES > LY::BYTES + 16 ? PromptLds<D, kRT>::BYTES : LY::BYTES + 16;
+  constexpr int NB = node_area_bytes<D>() + 16;
+  constexpr int LB = PromptLds<D, kRT>::BYTES > NB ? PromptLds<D, kRT>::BYTES : NB;
   __shared__ __attribute__((aligned(16))) char lds[LB];
   const int g = blockIdx.x % A.HK;
   const int rest = blockIdx.x / A.HK;
