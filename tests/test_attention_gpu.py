@@ -138,10 +138,12 @@ def test_trie_rows_equal_one_token_paths(cfg):
         assert torch.equal(one[:, 0], full[:, i]), f"node {i}"
 
 
-@pytest.mark.parametrize("base", [1, 7, 37, 100])
+@pytest.mark.parametrize("base", [1, 7, 37, 100, 150, 200, 300])
 def test_committed_offset_rows_equal_paths(base):
     """Trie placed after `base` committed slots (all rows see them); tile edges of the
-    node segment fall mid-trie.  Each row equals its 1-token path call."""
+    node segment fall mid-trie.  Each row equals its 1-token path call.  base 150 / 200 /
+    300 put 224 / 288 / 384 slots in the node segment (V resident, V resident, streamed),
+    their 1-token calls at most 192 / 224 / 352 (resident, V resident, streamed)."""
     c = gen.cfg2(seed=4, base=base)
     _check_parity(c, full := _run(c))
     rng = np.random.default_rng(base)
