@@ -392,7 +392,7 @@ def test_one_launch_workspace_shared_by_shapes():
     assert _status(cases[0], ws) == 0
 
 
-@pytest.mark.parametrize("which", ["cfg2", "cfg1", "n128"])
+@pytest.mark.parametrize("which", ["cfg2", "cfg1", "n128", "one"])
 def test_wait_that_gives_up_poisons_its_rows(which):
     """One-launch path with the counter wait forced to give up at once (the spin limit
     lowered through the test hook, so every workgroup still exits normally): every row
@@ -403,7 +403,9 @@ def test_wait_that_gives_up_poisons_its_rows(which):
     from respect_amd import _lib
     c = {"cfg2": lambda: gen.cfg2(seed=6), "cfg1": gen.cfg1,
          # 512 rows per kv head: two row blocks per workgroup in the one-launch path
-         "n128": lambda: gen.attn_case(9, 32, 8, 128, 3072, 8, 32, 0, 32, 128, kv_scale=128 ** -0.5)}[which]()
+         "n128": lambda: gen.attn_case(9, 32, 8, 128, 3072, 8, 32, 0, 32, 128, kv_scale=128 ** -0.5),
+         # one query row (4 rows per kv head, one row tile per wave)
+         "one": lambda: gen.path_case(gen.cfg2(seed=6), 5)}[which]()
     H, M, D = c.q.shape
     HK, P, _ = c.kp.shape
     L = _lib.lib()
