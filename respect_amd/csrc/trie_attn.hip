@@ -21,12 +21,14 @@
 //            scaled to the row's maximum M over them (2^(m_k - M), 0 for an
 //            empty quarter) and summed as (q0 + q1) + (q2 + q3), l likewise.
 //   node     score q.k c from a bf16 MFMA chain; m = the maximum over the
-//            row's allowed node slots; p = 2^(s - m) in fp32; l and acc
-//            summed over the allowed slots one at a time in slot order (the
-//            reference's node loop, attention.py:52-67, forms the same sums
-//            with an online maximum).  Masked slots are skipped; in the
-//            reference they are exact no-ops, so only the sequence of
-//            allowed slots matters.
+//            row's allowed node slots; p = 2^(s - m) in fp32, split as
+//            hi = bf16(p) and lo = bf16(p - hi); the allowed slots taken in
+//            slot order (rank r = the r-th allowed slot) in tiles of 32
+//            ranks, each tile summed on the MFMA as acc += V^T hi, then
+//            acc += V^T lo (l likewise with V = 1).  The reference's node loop
+//            (attention.py:52-67) forms the same sums with an online maximum.
+//            Masked slots are skipped; in the reference they are exact
+//            no-ops, so only the sequence of allowed slots matters.
 //   final    the NG groups left to right, then the node partial.
 //
 // S and NG depend on P only.  Which wave computes what changes with the number
@@ -44,9 +46,10 @@
 // step 4i + k of round i for its 16 RT rows; the four quarters are combined
 // through LDS and the group partial (m, l, acc) is stored; the workgroup then
 // counts itself, computes the node partials of its share of the block's rows
-// (MFMA scores, one row per wave) and, once the block's groups are all
-// counted, merges its rows.  When the grid cannot be resident at once the
-// same work runs as prompt_kernel then node_merge_kernel -- the same bits.
+// (MFMA scores and rank-tiled MFMA sums) and, once the block's groups are all
+// counted, merges its rows.  A grid up to twice what the device holds at once
+// runs as fused2_kernel (two row blocks per workgroup, one after the other);
+// a larger one as prompt_kernel then node_merge_kernel -- the same bits.
 //   Rows are packed GQA-wise (row = query * GQA + head-in-group), so a kv
 //   head's K/V is read once from HBM for all query heads that share it.  With
 //   8 kv heads, workgroup g of kernel A lands on XCD g (round-robin dispatch),
