@@ -8,10 +8,10 @@ msk [M, NN] bool (True = the row may attend to that slot); returns a new
 num_stages) are accepted for compatibility; only ``NN % BNB == 0`` is still
 checked, as the reference does.
 
-The HIP kernel (respect_amd/csrc/trie_attn.hip) folds every row's allowed node
-slots one at a time in slot order and reduces the prompt in a fixed tree set
-by NP alone, so a row's bits do not depend on M, on where its ancestors sit in
-the node segment, or on the other rows.
+The HIP kernel (respect_amd/csrc/trie_attn.hip) sums every row's allowed node
+slots in slot order, in MFMA tiles of 32 ranks, and reduces the prompt in a
+fixed tree set by NP alone, so a row's bits do not depend on M, on where its
+ancestors sit in the node segment, or on the other rows.
 """
 from __future__ import annotations
 
