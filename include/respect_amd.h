@@ -99,9 +99,9 @@ const char* rspx_version(void);
  * NN <= 4096 (the node-slot limit of the reference dispatcher, NMAX).
  *
  * Launches: one (prompt groups, node partials and merge in one kernel whose
- * workgroups wait for each other; used when the grid fits on the device at
- * once) or two (prompt groups, then node partials and merge).  Both give the
- * same bits.
+ * workgroups wait for each other; used when the grid, or half of it with two
+ * row blocks per workgroup, fits on the device at once) or two (prompt
+ * groups, then node partials and merge).  All give the same bits.
  *
  * rows_per_wave: 0 = automatic (one 16-row tile per wave when that grid
  * fits on the device at once, e.g. 1-token calls; two otherwise), else 1 or
