@@ -107,6 +107,14 @@ __device__ __forceinline__ uint16_t* out_at(uint16_t* y, int64_t sy, int row, in
 template <int TPR, int VPL, int MODE, int SC>
 __device__ __forceinline__ void rms_row_wave(const RowIn& in, int row, const uint16_t* w, uint16_t* y, int64_t sy,
                                              int sub, int n, float eps) {
+  // The weights are requested first: after the row's stores and the
+  // reduction they would be one more dependent memory round trip.
+  u32x4 wraw[VPL];
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int c = (v * TPR + sub) * 8;
+    wraw[v] = c < n ? *reinterpret_cast<const u32x4*>(w + c) : u32x4{0u, 0u, 0u, 0u};
+  }
   float xv[VPL][8];
   float ss = 0.f;
 #pragma unroll
@@ -128,7 +136,7 @@ __device__ __forceinline__ void rms_row_wave(const RowIn& in, int row, const uin
     const int c = (v * TPR + sub) * 8;
     if (c < n) {
       float wv[8], o[8];
-      unpack8(*reinterpret_cast<const u32x4*>(w + c), wv);
+      unpack8(wraw[v], wv);
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i] = wv[i] * round_bf16(xv[v][i] * r);
       *reinterpret_cast<u32x4*>(out_at(y, sy, row, c, n)) = pack8(o);
@@ -157,6 +165,13 @@ __global__ __launch_bounds__(256) void rmsnorm_row_kernel(RowIn in, const uint16
   __shared__ float part[4];
   const int row = blockIdx.x;
   const int t = threadIdx.x, lane = __lane_id(), wv = t >> 6;
+  // The weights are requested first (see rms_row_wave).
+  u32x4 wraw[VPL];
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int c = (v * 256 + t) * 8;
+    wraw[v] = c < n ? *reinterpret_cast<const u32x4*>(w + c) : u32x4{0u, 0u, 0u, 0u};
+  }
   float xv[VPL][8];
   float ss = 0.f;
 #pragma unroll
@@ -181,7 +196,7 @@ __global__ __launch_bounds__(256) void rmsnorm_row_kernel(RowIn in, const uint16
     const int c = (v * 256 + t) * 8;
     if (c < n) {
       float wvv[8], o[8];
-      unpack8(*reinterpret_cast<const u32x4*>(w + c), wvv);
+      unpack8(wraw[v], wvv);
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i] = wvv[i] * round_bf16(xv[v][i] * r);
       *reinterpret_cast<u32x4*>(out_at(y, sy, row, c, n)) = pack8(o);
@@ -336,6 +351,12 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(const uint16_t* qkv
   else if (rowid < nq + nk) { kind = 1; t = (rowid - nq) / HK; hh = rowid - nq - t * HK; }
   else { kind = 2; t = (rowid - nq - nk) / HK; hh = rowid - nq - nk - t * HK; }
   const int col = (kind == 0 ? hh * D : kind == 1 ? (HQ + hh) * D : (HQ + HK + hh) * D) + sub * 8;
+  // Norm weights and rotary rows are requested with the projection values
+  // (v rows load them unused): after the reduction they would be one more
+  // dependent memory round trip.
+  const u32x4 wraw = *reinterpret_cast<const u32x4*>((kind == 0 ? wq : wk) + sub * 8);
+  const u32x4 craw = *reinterpret_cast<const u32x4*>(cosb + (int64_t)t * scs + sub * 8);
+  const u32x4 sraw = *reinterpret_cast<const u32x4*>(sinb + (int64_t)t * scs + sub * 8);
   u32x4 raw;
   if (qp) {  // the projection's fp32 chunk partials, summed and rounded as rspx_linear would
     const float* p = qp + (int64_t)t * sqkv + col;
@@ -361,11 +382,11 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(const uint16_t* qkv
   ss = lane_group_sum<16>(ss);
   const float rr = rsqrt_rn(ss / (float)D + eps);
   float wv[8], nv[8], cs[8], sn[8], o[8];
-  unpack8(*reinterpret_cast<const u32x4*>((kind == 0 ? wq : wk) + sub * 8), wv);
+  unpack8(wraw, wv);
 #pragma unroll
   for (int i = 0; i < 8; ++i) nv[i] = round_bf16(wv[i] * round_bf16(xv[i] * rr));
-  unpack8(*reinterpret_cast<const u32x4*>(cosb + (int64_t)t * scs + sub * 8), cs);
-  unpack8(*reinterpret_cast<const u32x4*>(sinb + (int64_t)t * scs + sub * 8), sn);
+  unpack8(craw, cs);
+  unpack8(sraw, sn);
   rope_vec(nv, cs, sn, sub, o);
   uint16_t* dst = kind == 0 ? qo + ((int64_t)t * HQ + hh) * D : ck + hh * skh + (int64_t)slot * skn;
   if (!slot_ok) {
