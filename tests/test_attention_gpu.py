@@ -321,14 +321,16 @@ def _status(case, ws):
 
 
 @pytest.mark.parametrize("which", ["cfg1", "cfg2", "base37", "base100", "n64b40", "long", "gqa2", "d64",
-                                   "d64b90", "n128b70"])
+                                   "d64b90", "n128b70", "n72", "n100b30"])
 def test_one_and_two_launches_equal(which):
     """The one-kernel path (prompt groups, node partials and merge with workgroups
     waiting on per-row-block counters) and the two-kernel path give the same
     bits; the counters are back at zero after each call (repeat calls on one
     workspace stay equal) and no wait ran out.  base100 / n64b40 / d64b90 put
     65-128 slots in the node segment (two chunks, loaded whole by both paths); long /
-    n128b70 have 512 rows per kv head, two row blocks per workgroup in one launch."""
+    n128b70 have 512 rows per kv head, two row blocks per workgroup in one launch;
+    n72 / n100b30 (288 / 400 rows, 5 / 7 row blocks) leave the last workgroups of
+    that launch a single block."""
     from respect_amd import _lib
     c = {"cfg1": gen.cfg1, "cfg2": gen.cfg2, "base37": lambda: gen.cfg2(seed=4, base=37),
          "base100": lambda: gen.cfg2(seed=4, base=100),
@@ -338,7 +340,10 @@ def test_one_and_two_launches_equal(which):
          "d64": lambda: gen.attn_case(7, 16, 2, 64, 3086, 3, 9, 0, 6, None),
          "d64b90": lambda: gen.attn_case(7, 16, 2, 64, 3086, 3, 9, 0, 6, None, base=90),
          "n128b70": lambda: gen.attn_case(10, 32, 8, 128, 3072, 8, 32, 0, 32, 128, kv_scale=128 ** -0.5,
-                                          base=70)}[which]()
+                                          base=70),
+         "n72": lambda: gen.attn_case(14, 32, 8, 128, 3072, 4, 24, 0, 16, 72, kv_scale=128 ** -0.5),
+         "n100b30": lambda: gen.attn_case(13, 32, 8, 128, 3072, 6, 24, 0, 16, 100, kv_scale=128 ** -0.5,
+                                          base=30)}[which]()
     print(f"[one/two launches] {which} NN={c.kn.shape[1]}", flush=True)
     H, M, D = c.q.shape
     HK, P, _ = c.kp.shape
