@@ -277,6 +277,33 @@ def test_head_dims_32_and_256(which):
             _run(c, rows_per_wave=2)
 
 
+GQA_CASES = {
+    # one q head per kv head (multi-head attention) and sixteen
+    "gqa1": lambda: gen.attn_case(15, 8, 8, 128, 900, 3, 10, 0, 6, None, kv_scale=128 ** -0.5, base=20),
+    "gqa16": lambda: gen.attn_case(16, 32, 2, 128, 1100, 3, 10, 0, 6, None, kv_scale=128 ** -0.5, base=50),
+}
+
+
+@pytest.mark.parametrize("which", list(GQA_CASES))
+def test_gqa_1_and_16(which):
+    """The outer q-heads-per-kv-head ratios the plan accepts: per-element parity with
+    the kernel-tree restatement and the fp64 bound, trie rows bitwise equal to their
+    1-token calls, and the same bits from one and two launches and from one and two
+    row tiles per wave."""
+    c = GQA_CASES[which]()
+    H, M, D = c.q.shape
+    print(f"[gqa] {which} H={H} HK={c.kp.shape[0]} M={M} NN={c.kn.shape[1]}", flush=True)
+    full = _run(c)
+    _check_parity(c, full)
+    n = len(c.tree.nodes)
+    for i in sorted({0, n // 2, n - 1}):
+        assert torch.equal(_run(gen.path_case(c, i))[:, 0], full[:, i])
+    assert torch.equal(_run(c, launches=2), full)
+    assert torch.equal(_run(c, launches=1), full)
+    assert torch.equal(_run(c, rows_per_wave=1), full)
+    assert torch.equal(_run(c, rows_per_wave=2), full)
+
+
 def test_no_node_slots_and_no_prompt():
     c = gen.cfg1()
     # NN = 0: prompt only
