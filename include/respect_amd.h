@@ -239,7 +239,9 @@ int rspx_silu_mul(const void* g, int64_t sg, const void* u, int64_t su, void* y,
  * bf16 (out_fp32 = 0) or fp32 (out_fp32 = 1) (replaces
  * respect/kernels/gemm.py:30 linear(x, w, ..., out_dtype); bias is the
  * caller's, as in the reference).  Row strides sx, sw, so in elements; rows
- * 16-byte aligned; sx may be RSPX_TILED.  N % 16 == 0, K % 256 == 0.
+ * 16-byte aligned; sx may be RSPX_TILED, and so may sw: w is then in the
+ * tiled weight layout rspx_linear_tile_weight writes (same results, bit for
+ * bit).  N % 16 == 0, K % 256 == 0.
  *
  * Reduction order: K is cut into rspx_linear_splits(N, K) equal chunks (a
  * function of N and K only); each chunk is a fixed chain of bf16 MFMAs in
@@ -274,6 +276,21 @@ int rspx_linear_silu(const void* x, int64_t sx, const void* w, int64_t sw, void*
  */
 int rspx_linear_partials(const void* x, int64_t sx, const void* w, int64_t sw, float* part, int M, int N, int K,
                          void* stream);
+
+/* The tiled weight layout (no counterpart in the reference, whose weights stay
+ * nn.Linear's row-major [N, K]): w [N, K] (row stride sw >= K, a multiple of
+ * 8; 16-byte aligned) copied into out, which holds
+ * rspx_linear_tiled_weight_elems(N, K) bf16 elements: 16-row slabs of
+ * 16 K + 64 elements (the last 64 zero), slab n / 16 holding the K / 32
+ * tiles of 16 x 32 elements of its rows in order of k, element (n, k) at
+ * (n % 16 + 16 ((k % 32) / 8)) 8 + k % 8 inside its tile.  Pass out with row
+ * stride RSPX_TILED as the w of rspx_linear, rspx_linear_silu and
+ * rspx_linear_partials: each wave then reads one 1 KB tile per k-block, in
+ * one piece per round.  N % 16 == 0, K % 32 == 0 (-1 / RSPX_EUNSUPPORTED
+ * otherwise).
+ */
+int64_t rspx_linear_tiled_weight_elems(int N, int K);
+int rspx_linear_tile_weight(const void* w, int64_t sw, int N, int K, void* out, void* stream);
 
 /* ---------------------------------------------------------------- residual add + RMSNorm
  * xo[r] = bf16(r[r] + h[r]) (PyTorch's bf16 add), y[r] = rmsnorm(xo[r], w, eps)

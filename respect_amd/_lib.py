@@ -14,8 +14,8 @@ import torch  # noqa: F401  (loads the HIP runtime the library will share)
 
 LIB_PATH = Path(__file__).resolve().with_name("librespect_amd.so")
 
-# Row stride value naming the tiled activation layout (RSPX_TILED of
-# include/respect_amd.h).
+# Row stride value naming the tiled activation layout of x / y and the tiled
+# weight layout of w (RSPX_TILED of include/respect_amd.h).
 RSPX_TILED = -1
 
 _c_p = ctypes.c_void_p
@@ -77,6 +77,8 @@ SIGNATURES: dict[str, tuple] = {
     "rspx_argmax_rows": (_i32, [_c_p, _i64, _i32, _i32, _i32, _i32, _c_p, _c_p, _i64, _c_p]),
     "rspx_linear_partials": (_i32, [_c_p, _i64, _c_p, _i64, _c_p, _i32, _i32, _i32, _c_p]),
     "rspx_linear_silu": (_i32, [_c_p, _i64, _c_p, _i64, _c_p, _i64, _i32, _i32, _i32, _c_p]),
+    "rspx_linear_tiled_weight_elems": (_i64, [_i32, _i32]),
+    "rspx_linear_tile_weight": (_i32, [_c_p, _i64, _i32, _i32, _c_p, _c_p]),
     "rspx_add_rmsnorm_partials": (_i32, [_c_p, _i64, _c_p, _i32, _c_p, _c_p, _i64, _c_p, _i64, _i32, _i32, _f32,
                                          _c_p]),
     "rspx_qkv_rope_cache_partials": (_i32, [_c_p, _i32, _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i32, _c_p, _i64, _i64, _c_p,

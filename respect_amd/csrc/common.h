@@ -69,7 +69,8 @@ __device__ __forceinline__ int64_t tiled_offset(int m, int k, int K) {
          (k & 7);
 }
 
-// Row stride value that names the tiled layout (RSPX_TILED of the C ABI).
+
+// Row stride value that names the tiled layouts (RSPX_TILED of the C ABI).
 constexpr int64_t kTiled = -1;
 
 // The output of a K-split linear layer: the fp32 chunk partials of one

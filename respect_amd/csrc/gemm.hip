@@ -31,6 +31,18 @@
 //
 // S > 1 writes fp32 chunk partials [S][M][N] into the caller's workspace and
 // a second kernel sums them in chunk order and rounds.
+//
+// W may also come in a tiled layout (row stride RSPX_TILED; written by
+// rspx_linear_tile_weight from the row-major matrix): 16-row slabs of
+// 16 K + kWSlabPad elements, slab n / 16 holding the K / 32 tiles of its rows
+// one after the other, tile k / 32 holding element (n, k) at
+// (n % 16 + 16 ((k % 32) / 8)) 8 + k % 8 -- lane n % 16 + 16 g of a wave
+// loads its MFMA A operand (row n % 16, k 8 g .. 8 g + 7) as 16 contiguous
+// bytes of one 1 KB tile.  The TCP (vector L1) then handles one 8 KB piece per
+// wave and round instead of 16 rows of 512 bytes on 16 pages (q/k/v, o,
+// gate/up, down at 64 rows: 14.1 / 10.4 / 40.2 / 23.4 us instead of 14.6 /
+// 11.1 / 42.0 / 24.6; one row 11.0 / 7.9 / 34.9 / 18.7 instead of 11.3 / 8.5 /
+// 34.4 / 19.5).  The same bits as the row-major W.
 
 #include "common.h"
 #include "respect_amd.h"
@@ -68,6 +80,13 @@ struct Args {
 };
 
 constexpr int kXResRounds = 4;   // X-resident blocks: K chunks of at most 4 rounds (128 KB of LDS)
+// Elements after each 16-row slab of a tiled W.  Slabs of 4096 or 12288
+// columns are a multiple of 128 KB long, so without it every wave's stream
+// starts at the same offset modulo the memory-channel interleave; 128 bytes
+// spread them (on MI355X, 64 rows: gate/up [24576, 4096] 40.2 instead of 41.7
+// us with no pad, down [4096, 12288] 23.4 vs 24.1, vocabulary 238 vs 250; pads
+// of 32, 128, 256, 512, 1024 and 2048 elements measured no better).
+constexpr int kWSlabPad = 64;
 constexpr int kOOB = 0x7ffffff0;  // a buffer offset past any descriptor: loads return 0, touch nothing
 constexpr int kOOBRow = 0x40000000;  // the same for a whole lane chunk (k-block steps added stay below 2^31)
 
@@ -124,12 +143,15 @@ __device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t rx, const int (&x
   }
   asm volatile("" ::: "memory");
 }
+// WKB: bytes between a lane's consecutive k-blocks of W (64 row-major, 1024
+// tiled).
+template <int WKB>
 __device__ __forceinline__ void issue_w(__amdgpu_buffer_rsrc_t rw, int woff, int rr, int nr, u32x4 (&wf)[kRoundKB]) {
   const bool live = rr < nr;
 #pragma unroll
   for (int kb = 0; kb < kRoundKB; ++kb)
     wf[kb] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                           rw, live ? woff + 2 * (rr * kRoundK + 32 * kb) : kOOB, 0, 0));
+                                           rw, live ? woff + WKB * (rr * kRoundKB + kb) : kOOB, 0, 0));
   asm volatile("" ::: "memory");
 }
 
@@ -217,8 +239,14 @@ __device__ __forceinline__ void vm_wait_n(int n) {
 // front (NR x 32 KB), so the main loop streams W with no X loads and no
 // barriers.  The LDS image and the MFMA chain are those of the two-buffer
 // form: the same bits.
-template <int MT, int NR, int W, bool XRES = false>
+//
+// WT: W in the tiled layout (w row stride RSPX_TILED): a wave's 16 bytes per
+// lane of a k-block are one 1 KB tile and its k-blocks follow each other, so
+// a round of W is 8 KB in one piece instead of 16 rows x 512 bytes.  The MFMA
+// operands, and so every bit, are the same.
+template <int MT, int NR, int W, bool XRES = false, bool WT = false>
 __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
+  constexpr int WKB = WT ? 1024 : 64;
   static_assert(!XRES || (NR > 0 && NR <= kXResRounds), "X-resident blocks hold at most kXResRounds rounds");
   constexpr int kCols = 16 * W;
   __shared__ __attribute__((aligned(16))) char xs[XRES ? NR : 2][kRoundKB * 4 * 1024];  // 32 KB each
@@ -270,8 +298,10 @@ __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
     for (int t = 0; t < 4; ++t) xoff[t] = tile_off(t);
   }
   const __amdgpu_buffer_rsrc_t rw =
-      rsrc(A.w + (int64_t)(has_cols ? col : 0) * A.sw + k0, has_cols ? 2 * (15 * A.sw + A.KC) : 0);
-  const int woff = 2 * (n16 * (int)A.sw + 8 * g4);
+      WT ? rsrc(A.w + (int64_t)(has_cols ? col / 16 : 0) * ((A.K / 32) * 512 + kWSlabPad) + (k0 / 32) * 512,
+                has_cols ? A.KC * 32 : 0)
+         : rsrc(A.w + (int64_t)(has_cols ? col : 0) * A.sw + k0, has_cols ? 2 * (15 * A.sw + A.KC) : 0);
+  const int woff = WT ? 16 * lane : 2 * (n16 * (int)A.sw + 8 * g4);
 
   lds_char_t* xl = (lds_char_t*)xs[0];
   f32x4 acc[4];
@@ -282,14 +312,14 @@ __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
     u32x4 wbuf[4][kRoundKB];
 #pragma unroll
     for (int rr = 0; rr < NR; ++rr) issue_x<W>(rx, xoff, xkb, rr, nr, xl + rr * XB, w);
-    issue_w(rw, woff, 0, nr, wbuf[0]);
-    if constexpr (NR > 1) issue_w(rw, woff, 1, nr, wbuf[1]);
-    if constexpr (NR > 2) issue_w(rw, woff, 2, nr, wbuf[2]);
+    issue_w<WKB>(rw, woff, 0, nr, wbuf[0]);
+    if constexpr (NR > 1) issue_w<WKB>(rw, woff, 1, nr, wbuf[1]);
+    if constexpr (NR > 2) issue_w<WKB>(rw, woff, 2, nr, wbuf[2]);
     vm_wait_n(8 * (1 + (1 < NR) + (2 < NR)));  // every X chunk (issued before the W rounds) landed
     raw_barrier();
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      if (r + 3 < NR) issue_w(rw, woff, r + 3, nr, wbuf[(r + 3) & 3]);
+      if (r + 3 < NR) issue_w<WKB>(rw, woff, r + 3, nr, wbuf[(r + 3) & 3]);
       vm_wait_n(8 * ((r + 1 < NR) + (r + 2 < NR) + (r + 3 < NR)));  // W(r) landed
       round_compute<MT>(xl + r * XB, wbuf[r & 3], acc, lane);
     }
@@ -299,13 +329,13 @@ __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
     // loads issued after the later of X(r) and W(r).
     u32x4 wbuf[4][kRoundKB];
     issue_x<W>(rx, xoff, xkb, 0, nr, xl, w);
-    issue_w(rw, woff, 0, nr, wbuf[0]);
-    if constexpr (NR > 1) issue_w(rw, woff, 1, nr, wbuf[1]);
-    if constexpr (NR > 2) issue_w(rw, woff, 2, nr, wbuf[2]);
+    issue_w<WKB>(rw, woff, 0, nr, wbuf[0]);
+    if constexpr (NR > 1) issue_w<WKB>(rw, woff, 1, nr, wbuf[1]);
+    if constexpr (NR > 2) issue_w<WKB>(rw, woff, 2, nr, wbuf[2]);
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       if (r + 1 < NR) issue_x<W>(rx, xoff, xkb, r + 1, nr, xl + ((r + 1) & 1) * XB, w);
-      if (r + 3 < NR) issue_w(rw, woff, r + 3, nr, wbuf[(r + 3) & 3]);
+      if (r + 3 < NR) issue_w<WKB>(rw, woff, r + 3, nr, wbuf[(r + 3) & 3]);
       const int younger = r == 0 ? 8 * ((1 < NR) + (2 < NR) + (3 < NR)) + XPW * (1 < NR)
                                  : 8 * ((r + 2 < NR) + (r + 3 < NR)) + XPW * (r + 1 < NR);
       vm_wait_n(younger);
@@ -316,17 +346,17 @@ __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
   } else {
     u32x4 wa[kRoundKB], wb[kRoundKB];
     issue_x<W>(rx, xoff, xkb, 0, nr, xl, w);
-    issue_w(rw, woff, 0, nr, wa);
+    issue_w<WKB>(rw, woff, 0, nr, wa);
     for (int r = 0; r < nr; r += 2) {
       issue_x<W>(rx, xoff, xkb, r + 1, nr, xl + XB, w);
-      issue_w(rw, woff, r + 1, nr, wb);
+      issue_w<WKB>(rw, woff, r + 1, nr, wb);
       vm_wait_n(8 + XPW);
       raw_barrier();
       round_compute<MT>(xl, wa, acc, lane);
       raw_barrier();
       if (r + 1 >= nr) break;
       issue_x<W>(rx, xoff, xkb, r + 2, nr, xl, w);
-      issue_w(rw, woff, r + 2, nr, wa);
+      issue_w<WKB>(rw, woff, r + 2, nr, wa);
       vm_wait_n(8 + XPW);
       raw_barrier();
       round_compute<MT>(xl + XB, wb, acc, lane);
@@ -394,9 +424,46 @@ static int linear_splits(int N, int K) {
   return S;
 }
 
+// W [N, K] (row stride sw) into the tiled layout: one thread per 16 bytes of
+// the output, the slab pads written as zeros.
+__global__ __launch_bounds__(256) void tile_weight_kernel(const uint16_t* w, int64_t sw, int N, int K,
+                                                         uint16_t* out) {
+  const int64_t slab = (int64_t)K * 16 + gemm::kWSlabPad;   // elements per slab
+  const int64_t per = slab / 8;                              // 16-byte units per slab
+  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (u >= (int64_t)(N / 16) * per) return;
+  const int s = (int)(u / per);
+  const int64_t j = u - s * per;                             // unit inside the slab
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (j < (int64_t)K * 2) {
+    const int t = (int)(j >> 6), lane = (int)(j & 63);
+    const int n = 16 * s + (lane & 15), k = 32 * t + 8 * (lane >> 4);
+    v = *reinterpret_cast<const u32x4*>(w + (int64_t)n * sw + k);
+  }
+  *reinterpret_cast<u32x4*>(out + u * 8) = v;
+}
+
 }  // namespace rspx
 
 using namespace rspx;
+
+extern "C" int64_t rspx_linear_tiled_weight_elems(int N, int K) {
+  if (N <= 0 || K <= 0 || N % 16 != 0 || K % 32 != 0) return -1;
+  return (int64_t)(N / 16) * ((int64_t)K * 16 + gemm::kWSlabPad);
+}
+
+extern "C" int rspx_linear_tile_weight(const void* w, int64_t sw, int N, int K, void* out, void* stream) {
+  if (N <= 0 || K <= 0 || !w || !out || sw < K) return RSPX_EINVAL;
+  if (N % 16 != 0 || K % 32 != 0) return RSPX_EUNSUPPORTED;
+  if ((reinterpret_cast<uintptr_t>(w) & 15u) || (reinterpret_cast<uintptr_t>(out) & 15u) || sw % 8)
+    return RSPX_EALIGN;
+  const int64_t units = rspx_linear_tiled_weight_elems(N, K) / 8;
+  if ((units + 255) / 256 > 0x7fffffff) return RSPX_EUNSUPPORTED;
+  hipLaunchKernelGGL(tile_weight_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(w), sw, N, K,
+                     static_cast<uint16_t*>(out));
+  return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
+}
 
 extern "C" int rspx_linear_splits(int N, int K) {
   if (N <= 0 || K <= 0 || K % gemm::kRoundK != 0) return -1;
@@ -445,29 +512,33 @@ static int linear_launch(const void* x, int64_t sx, const void* w, int64_t sw, v
   const bool xres = waves >= 6 && M >= 32;
   const int nr = a.KC / gemm::kRoundK;
   const dim3 g((unsigned)grid), b(64 * waves);
-#define RSPX_GEMM_NR(MTV, WV)                                                                     \
-  switch (nr) {                                                                                  \
-    case 1: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 1, WV>), g, b, 0, s, a); break;           \
-    case 2: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 2, WV>), g, b, 0, s, a); break;           \
-    case 3: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 3, WV>), g, b, 0, s, a); break;           \
-    case 4:                                                                                      \
-      if (xres) hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 4, WV, true>), g, b, 0, s, a);        \
-      else hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 4, WV>), g, b, 0, s, a);                   \
-      break;                                                                                     \
-    case 6: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 6, WV>), g, b, 0, s, a); break;           \
-    case 8: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 8, WV>), g, b, 0, s, a); break;           \
-    case 12: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 12, WV>), g, b, 0, s, a); break;         \
-    case 16: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 16, WV>), g, b, 0, s, a); break;         \
-    default: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 0, WV>), g, b, 0, s, a); break;          \
+#define RSPX_GEMM_NR(MTV, WV, WTV)                                                                       \
+  switch (nr) {                                                                                          \
+    case 1: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 1, WV, false, WTV>), g, b, 0, s, a); break;       \
+    case 2: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 2, WV, false, WTV>), g, b, 0, s, a); break;       \
+    case 3: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 3, WV, false, WTV>), g, b, 0, s, a); break;       \
+    case 4:                                                                                              \
+      if (xres) hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 4, WV, true, WTV>), g, b, 0, s, a);           \
+      else hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 4, WV, false, WTV>), g, b, 0, s, a);               \
+      break;                                                                                             \
+    case 6: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 6, WV, false, WTV>), g, b, 0, s, a); break;       \
+    case 8: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 8, WV, false, WTV>), g, b, 0, s, a); break;       \
+    case 12: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 12, WV, false, WTV>), g, b, 0, s, a); break;     \
+    case 16: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 16, WV, false, WTV>), g, b, 0, s, a); break;     \
+    default: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 0, WV, false, WTV>), g, b, 0, s, a); break;      \
   }
-#define RSPX_GEMM_MT(WV)                 \
-  if (mt == 4) { RSPX_GEMM_NR(4, WV) }   \
-  else if (mt == 3) { RSPX_GEMM_NR(3, WV) } \
-  else if (mt == 2) { RSPX_GEMM_NR(2, WV) } \
-  else { RSPX_GEMM_NR(1, WV) }
-  if (waves == 6) { RSPX_GEMM_MT(6) }
-  else if (waves == 8) { RSPX_GEMM_MT(8) }
-  else { RSPX_GEMM_MT(4) }
+#define RSPX_GEMM_MT(WV, WTV)                                                                            \
+  if (mt == 4) { RSPX_GEMM_NR(4, WV, WTV) }                                                              \
+  else if (mt == 3) { RSPX_GEMM_NR(3, WV, WTV) }                                                         \
+  else if (mt == 2) { RSPX_GEMM_NR(2, WV, WTV) }                                                         \
+  else { RSPX_GEMM_NR(1, WV, WTV) }
+#define RSPX_GEMM_W(WV)                                                                                  \
+  if (sw == kTiled) { RSPX_GEMM_MT(WV, true) }                                                           \
+  else { RSPX_GEMM_MT(WV, false) }
+  if (waves == 6) { RSPX_GEMM_W(6) }
+  else if (waves == 8) { RSPX_GEMM_W(8) }
+  else { RSPX_GEMM_W(4) }
+#undef RSPX_GEMM_W
 #undef RSPX_GEMM_MT
 #undef RSPX_GEMM_NR
   if (S > 1 && !to_part) {
@@ -484,11 +555,11 @@ static int linear_check(const void* x, int64_t sx, const void* w, int64_t sw, in
   if (N % 16 != 0 || K % gemm::kRoundK != 0) return RSPX_EUNSUPPORTED;
   if (M == 0) return RSPX_OK;
   if (!x || !w) return RSPX_EINVAL;
-  const bool xt = sx == kTiled;
-  if ((!xt && sx < K) || sw < K) return RSPX_EINVAL;
+  const bool xt = sx == kTiled, wt = sw == kTiled;
+  if ((!xt && sx < K) || (!wt && sw < K)) return RSPX_EINVAL;
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-  if (!al(x) || !al(w) || (!xt && sx % 8) || sw % 8) return RSPX_EALIGN;
-  if ((!xt && (int64_t)64 * sx * 2 >= (1ll << 31)) || (int64_t)16 * sw * 2 >= (1ll << 31) ||
+  if (!al(x) || !al(w) || (!xt && sx % 8) || (!wt && sw % 8)) return RSPX_EALIGN;
+  if ((!xt && (int64_t)64 * sx * 2 >= (1ll << 31)) || (!wt && (int64_t)16 * sw * 2 >= (1ll << 31)) ||
       (int64_t)K * 128 >= (1ll << 30))
     return RSPX_EUNSUPPORTED;
   return RSPX_OK;

@@ -22,8 +22,10 @@ rspx_linear would store -- so no separate reduction launch is needed.
     logits = y . Wlm^T (fp32)                        rspx_linear
 
 The normalised rows y and the SwiGLU output m, read only by linear layers,
-stay in the tiled activation layout (RSPX_TILED): the linear layers then load
-their x operand a whole MFMA tile per instruction, with the same result bits.
+stay in the tiled activation layout (RSPX_TILED), and every weight matrix is
+held in the tiled weight layout (kernels.gemm.tile_weight): the linear layers
+then load both operands a whole MFMA tile per instruction, with the same
+result bits as from row-major operands.
 
 Each kernel computes a row with arithmetic that does not depend on how many
 rows the call carries, and attention folds a row's node slots in slot order,
@@ -40,6 +42,7 @@ import torch
 
 from .. import _lib
 from ..kernels.attention import trie_attn
+from ..kernels.gemm import TiledWeight, tile_weight
 from ..system.fused import rope_tables
 from .acceptance import greedy_token
 
@@ -67,60 +70,59 @@ class DecoderConfig:
         return 2 * (self.layers * per_layer + V * H + H)
 
 
-# Extra elements at the end of every weight row (the kernels take the row
-# stride).  Rows of 4096 or 12288 bf16 are a multiple of 8 KB apart, so the 16
-# rows one MFMA weight fragment reads sit at the same offset modulo 8 KB and
-# land on few memory channels; 128 bytes more per row spread them: on MI355X
-# the 1-row gate/up projection [24576, 4096] runs in 36.0 us instead of 41.3,
-# the vocabulary projection [151936, 4096] in 206 instead of 219 (64 rows:
-# 51.2 vs 53.2 and 272 vs 280 us); the other layers are unchanged.
-WEIGHT_ROW_PAD = 64
-
-
-def row_padded(w: torch.Tensor, pad: int = WEIGHT_ROW_PAD) -> torch.Tensor:
-    """``w`` [N, K] copied into storage of row stride K + pad; returns the
-    [N, K] view (same values, rows ``pad`` elements further apart)."""
-    N, K = w.shape
-    buf = torch.empty((N, K + pad), dtype=w.dtype, device=w.device)
-    buf[:, :K].copy_(w)
-    return buf[:, :K]
-
-
 class Layer:
+    """One decoder layer.  The projections are held tiled (``t*``, what the
+    kernels read); ``wqkv``, ``wo``, ``wgu`` and ``wd`` give them back as
+    row-major [N, K] copies for references and tests."""
+
     def __init__(self, cfg: DecoderConfig, g: torch.Generator, device, std: float):
         H, D, F = cfg.hidden, cfg.head_dim, cfg.ffn
 
-        def w(*shape, pad=True):
-            t = (torch.randn(*shape, generator=g, device=device) * std).to(torch.bfloat16)
-            return row_padded(t) if pad else t
+        def w(*shape):
+            return (torch.randn(*shape, generator=g, device=device) * std).to(torch.bfloat16)
 
         def norm_w(n):
             return (1.0 + torch.randn(n, generator=g, device=device) * std).to(torch.bfloat16)
 
         self.in_norm = norm_w(H)
-        self.wqkv = w(cfg.qkv_rows, H)              # [q | k | v] rows
+        self.tqkv = tile_weight(w(cfg.qkv_rows, H))  # [q | k | v] rows
         self.q_norm = norm_w(D)
         self.k_norm = norm_w(D)
-        self.wo = w(H, cfg.heads * D)
+        self.to = tile_weight(w(H, cfg.heads * D))
         self.post_norm = norm_w(H)
-        wgu = w(2 * F, H, pad=False)                # [gate | up] rows
-        self.wd = w(H, F)
+        wgu = w(2 * F, H)                            # [gate | up] rows
+        self.td = tile_weight(w(H, F))
         # With one K chunk the gate/up product carries SwiGLU in its epilogue
         # (rspx_linear_silu), which wants the rows interleaved: 2i gate i, 2i + 1 up i.
         self.gu_fused = _lib.lib().rspx_linear_splits(2 * F, H) == 1
-        self._wgu = row_padded(wgu.view(2, F, H).transpose(0, 1).reshape(2 * F, H) if self.gu_fused else wgu)
+        self.tgu = tile_weight(wgu.view(2, F, H).transpose(0, 1).reshape(2 * F, H) if self.gu_fused else wgu)
+
+    @property
+    def wqkv(self) -> torch.Tensor:
+        return self.tqkv.dense()
+
+    @property
+    def wo(self) -> torch.Tensor:
+        return self.to.dense()
+
+    @property
+    def wd(self) -> torch.Tensor:
+        return self.td.dense()
 
     @property
     def wgu(self) -> torch.Tensor:
-        """Gate/up weight as [gate | up] rows (a copy when stored interleaved)."""
+        """Gate/up weight as [gate | up] rows (a copy)."""
+        t = self.tgu.dense()
         if not self.gu_fused:
-            return self._wgu
-        F2, H = self._wgu.shape
-        return self._wgu.view(F2 // 2, 2, H).transpose(0, 1).reshape(F2, H)
+            return t
+        F2, H = t.shape
+        return t.view(F2 // 2, 2, H).transpose(0, 1).reshape(F2, H)
 
 
 class Decoder:
-    """Random-initialised decoder; weights ~ N(0, std), norm weights 1 + N(0, std)."""
+    """Random-initialised decoder; weights ~ N(0, std), norm weights 1 + N(0, std).
+    The vocabulary projection is held tiled (``t_lm_head``); ``lm_head`` gives it
+    back row-major (a copy)."""
 
     def __init__(self, cfg: DecoderConfig = DecoderConfig(), device="cuda", seed: int = 0, std: float = 0.02):
         self.cfg = cfg
@@ -130,13 +132,17 @@ class Decoder:
         self.embed = (torch.randn(cfg.vocab, cfg.hidden, generator=g, device=self.device) * std).to(torch.bfloat16)
         self.layers = [Layer(cfg, g, self.device, std) for _ in range(cfg.layers)]
         self.final_norm = (1.0 + torch.randn(cfg.hidden, generator=g, device=self.device) * std).to(torch.bfloat16)
-        self.lm_head = row_padded(
+        self.t_lm_head = tile_weight(
             (torch.randn(cfg.vocab, cfg.hidden, generator=g, device=self.device) * std).to(torch.bfloat16))
         self.sm_scale = cfg.head_dim ** -0.5
         self._ws = {}
         self._ws_retired = []   # outgrown buffers: a captured graph may still point at them
         self._rope = None       # (cos, sin) [positions, head_dim] bf16 tables
         self._graphs: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
+
+    @property
+    def lm_head(self) -> torch.Tensor:
+        return self.t_lm_head.dense()
 
     def _workspace(self, name: str, nbytes: int) -> torch.Tensor:
         """Scratch owned by the model, grown (never while a graph is being
@@ -169,7 +175,7 @@ class Decoder:
         idx = positions.clamp(0, t[0].shape[0] - 1)
         return t[0].index_select(0, idx), t[1].index_select(0, idx)
 
-    def _linear(self, x: int, sx: int, M: int, w: torch.Tensor, out_dtype=torch.bfloat16) -> torch.Tensor:
+    def _linear(self, x: int, sx: int, M: int, w: TiledWeight, out_dtype=torch.bfloat16) -> torch.Tensor:
         """x (device pointer, row stride sx or RSPX_TILED, M rows) . w^T."""
         L = _lib.lib()
         N, K = w.shape
@@ -181,7 +187,7 @@ class Decoder:
             1 if out_dtype == torch.float32 else 0, ws.data_ptr(), ws.numel(), _lib.stream_ptr(self.device)))
         return out
 
-    def _partials(self, x: int, sx: int, M: int, w: torch.Tensor) -> tuple[int, int]:
+    def _partials(self, x: int, sx: int, M: int, w: TiledWeight) -> tuple[int, int]:
         """x (device pointer, row stride sx or RSPX_TILED, M rows) . w^T left as
         fp32 chunk partials in the model's partial buffer; returns (pointer,
         chunk count) for a consumer that sums them."""
@@ -227,34 +233,34 @@ class Decoder:
         ws_attn = self._workspace("attn", L.rspx_trie_attn_workspace_bytes(HQ, HK, T, P, D))
         for li, lay in enumerate(self.layers):
             ck, cv = cache.k[li], cache.v[li]
-            qkvp, S = self._partials(y.data_ptr(), TILED, T, lay.wqkv)
+            qkvp, S = self._partials(y.data_ptr(), TILED, T, lay.tqkv)
             _lib.check("rspx_qkv_rope_cache_partials", L.rspx_qkv_rope_cache_partials(
                 qkvp, S, lay.q_norm.data_ptr(), lay.k_norm.data_ptr(), cos.data_ptr(),
                 sin.data_ptr(), cos.stride(0), slots32.data_ptr(), cache.cap, ck.data_ptr(), ck.stride(0), ck.stride(1),
                 cv.data_ptr(), cv.stride(0), cv.stride(1), qo.data_ptr(), T, HQ, HK, D, cfg.eps, s))
             trie_attn(qo.permute(1, 0, 2), ck[:, :P], cv[:, :P], ck[:, P:P + NN], cv[:, P:P + NN], msk,
                       self.sm_scale, out=att.permute(1, 0, 2), workspace=ws_attn)
-            hp, S = self._partials(att.data_ptr(), HQ * D, T, lay.wo)
+            hp, S = self._partials(att.data_ptr(), HQ * D, T, lay.to)
             _lib.check("rspx_add_rmsnorm_partials", L.rspx_add_rmsnorm_partials(
                 x.data_ptr(), Hd, hp, S, lay.post_norm.data_ptr(), x.data_ptr(), Hd, y.data_ptr(), TILED,
                 T, Hd, cfg.eps, s))
             F = cfg.ffn
             if lay.gu_fused:
                 _lib.check("rspx_linear_silu", L.rspx_linear_silu(
-                    y.data_ptr(), TILED, lay._wgu.data_ptr(), lay._wgu.stride(0), mlp.data_ptr(),
+                    y.data_ptr(), TILED, lay.tgu.data_ptr(), lay.tgu.stride(0), mlp.data_ptr(),
                     TILED, T, 2 * F, Hd, s))
                 msx = TILED
             else:
-                gu = self._linear(y.data_ptr(), TILED, T, lay.wgu)
+                gu = self._linear(y.data_ptr(), TILED, T, lay.tgu)
                 _lib.check("rspx_silu_mul", L.rspx_silu_mul(gu.data_ptr(), gu.stride(0), gu.data_ptr() + 2 * F,
                                                             gu.stride(0), mlp.data_ptr(), F, T, F, s))
                 msx = F
-            hp, S = self._partials(mlp.data_ptr(), msx, T, lay.wd)
+            hp, S = self._partials(mlp.data_ptr(), msx, T, lay.td)
             nxt = self.layers[li + 1].in_norm if li + 1 < len(self.layers) else self.final_norm
             _lib.check("rspx_add_rmsnorm_partials", L.rspx_add_rmsnorm_partials(
                 x.data_ptr(), Hd, hp, S, nxt.data_ptr(), x.data_ptr(), Hd, y.data_ptr(), TILED,
                 T, Hd, cfg.eps, s))
-        return self._linear(y.data_ptr(), TILED, T, self.lm_head, out_dtype=torch.float32)
+        return self._linear(y.data_ptr(), TILED, T, self.t_lm_head, out_dtype=torch.float32)
 
     # ------------------------------------------------------------------ prompt
     @torch.no_grad()

@@ -264,3 +264,96 @@ def test_linear_silu_tiled_in_and_out(M):
     assert torch.equal(from_tiled(out, M, F), ref)
     # rows past M were not written
     assert torch.isnan(out.float()).sum().item() == (-(-M // 64) * 64 - M) * F
+
+
+def _tiled_weight_numpy(w, pad=64):
+    """The tiled weight layout of include/respect_amd.h (rspx_linear_tile_weight),
+    element by element: slab n // 16 of 16 K + pad elements, tile k // 32 of it,
+    (n % 16 + 16 ((k % 32) // 8)) 8 + k % 8 inside the tile."""
+    N, K = w.shape
+    out = np.zeros((N // 16) * (16 * K + pad), dtype=w.dtype)
+    n, k = np.meshgrid(np.arange(N), np.arange(K), indexing="ij")
+    off = (n // 16) * (16 * K + pad) + (k // 32) * 512 + ((n % 16) + 16 * ((k % 32) // 8)) * 8 + k % 8
+    out[off.ravel()] = w.ravel()
+    return out
+
+
+@pytest.mark.parametrize("N,K", [(16, 256), (48, 768), (6144, 4096)])
+def test_tile_weight_layout(N, K):
+    """rspx_linear_tile_weight places every element where the layout says, the slab
+    pads are zero, and TiledWeight.dense() gives the matrix back; row-padded input too."""
+    from respect_amd import _lib
+    from respect_amd.kernels.gemm import tile_weight
+    rng = np.random.default_rng(N + K)
+    w = rng.integers(-30000, 30000, (N, K)).astype(np.int16)
+    wd = torch.from_numpy(w).cuda().view(torch.bfloat16)
+    assert _lib.lib().rspx_linear_tiled_weight_elems(N, K) == (N // 16) * (16 * K + 64)
+    for src in (wd, torch.nn.functional.pad(wd.view(torch.int16), (0, 64)).view(torch.bfloat16)[:, :K]):
+        t = tile_weight(src)
+        got = t.buf.view(torch.int16).cpu().numpy()
+        assert np.array_equal(got, _tiled_weight_numpy(w))
+        assert torch.equal(t.dense().view(torch.int16), wd.view(torch.int16))
+
+
+def test_tile_weight_errors():
+    from respect_amd import _lib
+    L = _lib.lib()
+    w = torch.zeros((64, 512), dtype=torch.bfloat16, device="cuda")
+    out = torch.empty(L.rspx_linear_tiled_weight_elems(64, 512), dtype=torch.bfloat16, device="cuda")
+    s = _lib.stream_ptr(w.device)
+    assert L.rspx_linear_tiled_weight_elems(40, 512) == -1
+    assert L.rspx_linear_tiled_weight_elems(64, 500) == -1
+    assert L.rspx_linear_tile_weight(w.data_ptr(), 512, 40, 512, out.data_ptr(), s) == -2   # N % 16
+    assert L.rspx_linear_tile_weight(w.data_ptr(), 500, 64, 512, out.data_ptr(), s) == -1   # sw < K
+    assert L.rspx_linear_tile_weight(w.data_ptr() + 2, 512, 64, 480, out.data_ptr(), s) == -4   # alignment
+    assert L.rspx_linear_tile_weight(w.data_ptr(), 512, 64, 512, out.data_ptr(), s) == 0
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (7, 1024, 4096), (64, 6144, 4096), (130, 512, 768),
+                                   (64, 24576, 4096), (200, 256, 12288), (64, 16384, 4096)])
+def test_linear_tiled_w_is_bitwise_row_major(M, N, K):
+    """w in the tiled weight layout (TiledWeight, row stride RSPX_TILED) gives the
+    row-major result bit for bit: rspx_linear (bf16 and fp32 out, row-major and
+    tiled x) and rspx_linear_partials."""
+    from _tiled import to_tiled
+    from respect_amd import _lib
+    from respect_amd.kernels.gemm import linear, tile_weight
+    print(f"[linear tiled w] M={M} N={N} K={K}", flush=True)
+    L = _lib.lib()
+    x, w = _xw(M * 5 + N, M, N, K)
+    xd, wd = _dev(x), _dev(w)
+    wt = tile_weight(wd)
+    for dt in (torch.bfloat16, torch.float32):
+        assert torch.equal(linear(xd, wt, out_dtype=dt), linear(xd, wd, out_dtype=dt))
+    s = _lib.stream_ptr(xd.device)
+    S = L.rspx_linear_splits(N, K)
+    xt = to_tiled(xd, fill=float("nan"))
+    parts = []
+    for xp, sx, wp, sw in ((xd, K, wd, K), (xd, K, wt, _lib.RSPX_TILED), (xt, _lib.RSPX_TILED, wt, _lib.RSPX_TILED)):
+        part = torch.empty((S, M, N), dtype=torch.float32, device="cuda")
+        _lib.check("rspx_linear_partials", L.rspx_linear_partials(xp.data_ptr(), sx, wp.data_ptr(), sw,
+                                                                  part.data_ptr(), M, N, K, s))
+        parts.append(part)
+    torch.cuda.synchronize()
+    assert torch.equal(parts[0], parts[1]) and torch.equal(parts[0], parts[2])
+
+
+@pytest.mark.parametrize("M", [1, 64, 130])
+def test_linear_silu_tiled_w(M):
+    """rspx_linear_silu with the interleaved gate/up rows tiled equals the row-major call."""
+    from respect_amd import _lib
+    from respect_amd.kernels.gemm import tile_weight
+    F, K = 8192, 512
+    L = _lib.lib()
+    x, w = _xw(M + 303, M, 2 * F, K)
+    xd, wd = _dev(x), _dev(w)
+    wt = tile_weight(wd)
+    s = _lib.stream_ptr(xd.device)
+    outs = []
+    for wp, sw in ((wd, K), (wt, _lib.RSPX_TILED)):
+        o = torch.empty((M, F), dtype=torch.bfloat16, device="cuda")
+        _lib.check("rspx_linear_silu", L.rspx_linear_silu(xd.data_ptr(), K, wp.data_ptr(), sw, o.data_ptr(), F,
+                                                           M, 2 * F, K, s))
+        outs.append(o)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
