@@ -114,35 +114,39 @@ __device__ __forceinline__ void round_compute(const lds_char_t* xb, const u32x4 
   }
 }
 
-// X chunks of round rr into LDS buffer xb: the 32 chunks c = 4 kb + t
-// (k-block kb, row tile t: rows 16 t + n16, k [8 g4, +8) of the block) of a
-// round are spread over the W waves, wave w taking c = w, w + W, ...; xo[t]
-// is this lane's offset of row tile t.  W loads of round rr into registers.
-// Rounds past the chunk and rows past M use out-of-range offsets: zeros, no
-// memory traffic.  Wave w issues the same ceil((32 - w) / W) X chunks and 8
-// W loads per round on every path, so the waits below are exact counts.
-// xkb: bytes between consecutive k-blocks of one lane's chunk (64 row-major,
-// 4096 tiled).
-template <int W>
+// X chunks of round rr into LDS buffer xb: the NC = 8 MT chunks c of a round
+// (k-block kb = c / MT, row tile t = c % MT: rows 16 t + n16, k [8 g4, +8) of
+// the block; only the MT row tiles the block computes) are spread over the W
+// waves, wave w taking c = w, w + W, ...; chunk (kb, t) lands at
+// (4 kb + t) KB of the buffer whatever MT is; xo[t] is this lane's offset of
+// row tile t.  Rounds past the chunk and rows past M use out-of-range
+// offsets: zeros, no memory traffic.  Wave w issues the same
+// ceil((NC - w) / W) X chunks and 8 W loads per round on every path, so the
+// waits below are exact counts.  xkb: bytes between consecutive k-blocks of
+// one lane's chunk (64 row-major, 4096 tiled).
+template <int W, int MT>
 __device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t rx, const int (&xo)[4], int xkb, int rr, int nr,
                                         lds_char_t* xb, int w) {
+  constexpr int NC = 8 * MT;
   const bool live = rr < nr;
-  if constexpr (32 % W == 0) {
-    // Every chunk of wave w is row tile w % 4, whose offset the caller put in xo[0].
+  if constexpr (NC % W == 0 && W % MT == 0) {
+    // Every chunk of wave w is row tile w % MT, whose offset the caller put in xo[0].
 #pragma unroll
-    for (int j = 0; j < 32 / W; ++j) {
-      const int kb = (w >> 2) + (W / 4) * j;
-      x_dma16(rx, live ? xo[0] + xkb * (rr * kRoundKB + kb) : kOOB, xb + (kb * 4 + (w & 3)) * 1024);
+    for (int j = 0; j < NC / W; ++j) {
+      const int kb = w / MT + (W / MT) * j;
+      x_dma16(rx, live ? xo[0] + xkb * (rr * kRoundKB + kb) : kOOB, xb + (kb * 4 + w % MT) * 1024);
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < (32 + W - 1) / W; ++j) {
-      const int c = w + W * j;                  // chunk: k-block c / 4, row tile c % 4
-      if (c < 32) x_dma16(rx, live ? xo[c & 3] + xkb * (rr * kRoundKB + (c >> 2)) : kOOB, xb + c * 1024);
+    for (int j = 0; j < (NC + W - 1) / W; ++j) {
+      const int c = w + W * j;
+      const int kb = c / MT, t = c % MT;
+      if (c < NC) x_dma16(rx, live ? xo[t] + xkb * (rr * kRoundKB + kb) : kOOB, xb + (kb * 4 + t) * 1024);
     }
   }
   asm volatile("" ::: "memory");
 }
+
 // WKB: bytes between a lane's consecutive k-blocks of W (64 row-major, 1024
 // tiled).
 template <int WKB>
@@ -253,10 +257,11 @@ __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
   constexpr int XB = kRoundKB * 4 * 1024;
   const int lane = __lane_id();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // X chunks this wave issues per round: a constant when W divides 32, so every
-  // wait count below is one too (a run-time count leaves the compiler's own
-  // waits for the W registers conservative).
-  const int XPW = 32 % W == 0 ? 32 / W : (32 - w + W - 1) / W;
+  // X chunks this wave issues per round: a constant when W divides 8 MT, so
+  // every wait count below is one too (a run-time count leaves the compiler's
+  // own waits for the W registers conservative).
+  constexpr int NC = 8 * MT;
+  const int XPW = NC % W == 0 ? NC / W : (NC - w + W - 1) / W;
   const int n16 = lane & 15, g4 = lane >> 4;
   const int NT = (A.N + kCols - 1) / kCols;
   const int nt = blockIdx.x % NT;
@@ -275,8 +280,8 @@ __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
   // a wave whose tile lies past M loads nothing (rows past M inside a tile are
   // read but only reach output rows that are never stored).
   const int mrows = min(kRows, A.M - row0);
-  // xoff[t]: this lane's offset of row tile t; when W divides 32 a wave only
-  // loads its own tile w % 4, kept in xoff[0].
+  // xoff[t]: this lane's offset of row tile t; when every chunk of a wave is
+  // one row tile (issue_x), only its offset, kept in xoff[0].
   __amdgpu_buffer_rsrc_t rx;
   int xoff[4], xkb;
   auto tile_off = [&](int t) {
@@ -290,8 +295,8 @@ __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
     rx = rsrc(A.x + (int64_t)row0 * A.sx + k0, 2 * ((int64_t)(mrows - 1) * A.sx + (A.K - k0)));
     xkb = 64;
   }
-  if constexpr (32 % W == 0) {
-    xoff[0] = tile_off(w & 3);
+  if constexpr (NC % W == 0 && W % MT == 0) {
+    xoff[0] = tile_off(w % MT);
     xoff[1] = xoff[2] = xoff[3] = 0;
   } else {
 #pragma unroll
@@ -311,7 +316,7 @@ __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
   if constexpr (XRES) {
     u32x4 wbuf[4][kRoundKB];
 #pragma unroll
-    for (int rr = 0; rr < NR; ++rr) issue_x<W>(rx, xoff, xkb, rr, nr, xl + rr * XB, w);
+    for (int rr = 0; rr < NR; ++rr) issue_x<W, MT>(rx, xoff, xkb, rr, nr, xl + rr * XB, w);
     issue_w<WKB>(rw, woff, 0, nr, wbuf[0]);
     if constexpr (NR > 1) issue_w<WKB>(rw, woff, 1, nr, wbuf[1]);
     if constexpr (NR > 2) issue_w<WKB>(rw, woff, 2, nr, wbuf[2]);
@@ -328,13 +333,13 @@ __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
     // others and the counts below would be off).  Exact wait per round: the
     // loads issued after the later of X(r) and W(r).
     u32x4 wbuf[4][kRoundKB];
-    issue_x<W>(rx, xoff, xkb, 0, nr, xl, w);
+    issue_x<W, MT>(rx, xoff, xkb, 0, nr, xl, w);
     issue_w<WKB>(rw, woff, 0, nr, wbuf[0]);
     if constexpr (NR > 1) issue_w<WKB>(rw, woff, 1, nr, wbuf[1]);
     if constexpr (NR > 2) issue_w<WKB>(rw, woff, 2, nr, wbuf[2]);
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      if (r + 1 < NR) issue_x<W>(rx, xoff, xkb, r + 1, nr, xl + ((r + 1) & 1) * XB, w);
+      if (r + 1 < NR) issue_x<W, MT>(rx, xoff, xkb, r + 1, nr, xl + ((r + 1) & 1) * XB, w);
       if (r + 3 < NR) issue_w<WKB>(rw, woff, r + 3, nr, wbuf[(r + 3) & 3]);
       const int younger = r == 0 ? 8 * ((1 < NR) + (2 < NR) + (3 < NR)) + XPW * (1 < NR)
                                  : 8 * ((r + 2 < NR) + (r + 3 < NR)) + XPW * (r + 1 < NR);
@@ -345,17 +350,17 @@ __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
     }
   } else {
     u32x4 wa[kRoundKB], wb[kRoundKB];
-    issue_x<W>(rx, xoff, xkb, 0, nr, xl, w);
+    issue_x<W, MT>(rx, xoff, xkb, 0, nr, xl, w);
     issue_w<WKB>(rw, woff, 0, nr, wa);
     for (int r = 0; r < nr; r += 2) {
-      issue_x<W>(rx, xoff, xkb, r + 1, nr, xl + XB, w);
+      issue_x<W, MT>(rx, xoff, xkb, r + 1, nr, xl + XB, w);
       issue_w<WKB>(rw, woff, r + 1, nr, wb);
       vm_wait_n(8 + XPW);
       raw_barrier();
       round_compute<MT>(xl, wa, acc, lane);
       raw_barrier();
       if (r + 1 >= nr) break;
-      issue_x<W>(rx, xoff, xkb, r + 2, nr, xl, w);
+      issue_x<W, MT>(rx, xoff, xkb, r + 2, nr, xl, w);
       issue_w<WKB>(rw, woff, r + 2, nr, wa);
       vm_wait_n(8 + XPW);
       raw_barrier();
