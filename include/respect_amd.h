@@ -47,7 +47,8 @@ extern "C" {
 /* Tiled activation layout.  Passed as the row stride of a bf16 activation
  * matrix A[M, K] with K % 32 == 0 -- x of rspx_linear, rspx_linear_silu and
  * rspx_linear_partials; y of rspx_rmsnorm, rspx_add_rmsnorm and
- * rspx_add_rmsnorm_partials; out of rspx_linear_silu -- RSPX_TILED names
+ * rspx_add_rmsnorm_partials; out of rspx_linear_silu; out of rspx_trie_attn
+ * as the [M, H D] matrix (som = RSPX_TILED, soh = D) -- RSPX_TILED names
  * this layout instead of row-major: element (m, k) sits at
  *   ((((m / 64) * (K / 32) + k / 32) * 4 + (m % 64) / 16) * 64
  *      + m % 16 + 16 * ((k % 32) / 8)) * 8 + k % 8,
@@ -107,6 +108,11 @@ const char* rspx_version(void);
  * fits on the device at once, e.g. 1-token calls; two otherwise), else 1 or
  * 2.  It changes only the work distribution, never the result.  D = 256
  * always runs one (2 returns RSPX_EUNSUPPORTED).
+ *
+ * out: element (head h, row m, d) at h soh + m som + d; or, with som =
+ * RSPX_TILED and soh = D (no counterpart in the reference), column h D + d of
+ * row m of the [M, H D] matrix in the tiled activation layout (ceil(M / 64) 64
+ * H D elements), the x the o projection of the decoder step reads fastest.
  */
 
 int64_t rspx_trie_attn_workspace_bytes(int H, int HK, int M, int P, int D);

@@ -77,6 +77,10 @@ constexpr int kWavesA = 8;       // waves per prompt workgroup
 
 // Strides are in elements; the host checks that every element offset of a
 // tensor fits 30 bits, so offsets (and byte offsets) are 32-bit arithmetic.
+// Kept at 184 bytes: one more int field (192 bytes of kernel arguments) made
+// the compiler read pointers of this struct from memory as generic pointers,
+// so the group-partial stores became flat stores, whose counters forced
+// extra waits everywhere (the 8B-shape call 18.4 -> 34 us, same bits).
 struct TrieAttnArgs {
   const uint16_t* q;  int sqh, sqm;
   const uint16_t* kp; int skph, skpn;
@@ -84,7 +88,7 @@ struct TrieAttnArgs {
   const uint16_t* kn; int sknh, sknn;
   const uint16_t* vn; int svnh, svnn;
   const uint8_t* msk; int smm, smn;
-  uint16_t* out;      int soh, som;
+  uint16_t* out;      int soh, som;   // soh < 0: out is [M, H D] in the tiled activation layout
   int HK, GQS, M, P, NN;   // GQS = log2(query heads per kv head)
   int R, NRB, NG, S;  // rows per kv head, row blocks, groups, steps per group
   float c;            // sm_scale * log2(e)
@@ -695,6 +699,14 @@ __device__ __forceinline__ RowRef row_ref(const TrieAttnArgs& A, int g, int r, i
   x.mq = x.rr >> A.GQS;
   x.hd = (g << A.GQS) + (x.rr & ((1 << A.GQS) - 1));
   return x;
+}
+
+// Element offset of (head R.hd, query R.mq, head_dim d) in out: strided, or
+// column R.hd D + d of row R.mq of the tiled [M, H D] matrix (d a multiple
+// of 4, so a lane's 2 or 4 elements stay contiguous in either layout).
+template <int D>
+__device__ __forceinline__ int64_t out_offset(int soh, int som, int heads, int hd, int mq, int d) {
+  return soh < 0 ? tiled_offset(mq, hd * D + d, heads * D) : (int64_t)hd * soh + (int64_t)mq * som + d;
 }
 
 typedef __attribute__((address_space(3))) float lds_float;
@@ -1323,7 +1335,7 @@ __device__ __forceinline__ void merge_row(const TrieAttnArgs& A, int g, int r, f
     if (qq < NG) combine<DL>(fm, fl, facc, gm[qq], gl[qq], ga[qq]);
   combine<DL>(fm, fl, facc, m, l, acc);
   if (!on) return;
-  uint16_t* o = A.out + (R.hd * A.soh + R.mq * A.som + DL * lane);
+  uint16_t* o = A.out + out_offset<D>(A.soh, A.som, A.HK << A.GQS, R.hd, R.mq, DL * lane);
   if constexpr (DL == 4)
     *reinterpret_cast<u32x2*>(o) = u32x2{pack_bf16x2(facc[0] / fl, facc[1] / fl), pack_bf16x2(facc[2] / fl, facc[3] / fl)};
   else if constexpr (DL == 2) *reinterpret_cast<uint32_t*>(o) = pack_bf16x2(facc[0] / fl, facc[1] / fl);
@@ -1392,7 +1404,7 @@ __device__ __forceinline__ void nan_rows(const TrieAttnArgs& A, int g, int p0, i
   if (DL * lane >= D) return;
   for (int r = p0 + w; r < rend; r += kWavesA) {
     const RowRef R = row_ref(A, g, r, r);
-    uint16_t* o = A.out + (R.hd * A.soh + R.mq * A.som + DL * lane);
+    uint16_t* o = A.out + out_offset<D>(A.soh, A.som, A.HK << A.GQS, R.hd, R.mq, DL * lane);
     if constexpr (DL == 4) *reinterpret_cast<u32x2*>(o) = u32x2{0x7fc07fc0u, 0x7fc07fc0u};
     else if constexpr (DL == 2) *reinterpret_cast<uint32_t*>(o) = 0x7fc07fc0u;
     else *o = (uint16_t)0x7fc0;
@@ -1696,7 +1708,12 @@ static int trie_attn_impl(const void* q, int64_t sqh, int64_t sqm, const void* k
   const void* ptrs[] = {q, kp, vp, kn, vn, out, workspace};
   for (const void* p : ptrs)
     if (p && !aligned16(p)) return RSPX_EALIGN;
-  const int64_t strides[] = {sqh, sqm, skph, skpn, svph, svpn, sknh, sknn, svnh, svnn, soh, som};
+  // som == RSPX_TILED: out is the [M, H D] matrix (query m, column h D + d)
+  // in the tiled activation layout, ceil(M / 64) 64 H D elements; soh must
+  // then be D.
+  const bool out_tiled = som == kTiled;
+  if (out_tiled && soh != D) return RSPX_EINVAL;
+  const int64_t strides[] = {sqh, sqm, skph, skpn, svph, svpn, sknh, sknn, svnh, svnn, soh, out_tiled ? 8 : som};
   for (int64_t s : strides) {
     if (s < 0) return RSPX_EINVAL;
     if (s % 8 != 0) return RSPX_EALIGN;
@@ -1708,7 +1725,9 @@ static int trie_attn_impl(const void* q, int64_t sqh, int64_t sqm, const void* k
   auto span = [](int64_t n0, int64_t s0, int64_t n1, int64_t s1, int64_t last) {
     return (n0 > 0 ? (n0 - 1) * s0 : 0) + (n1 > 0 ? (n1 - 1) * s1 : 0) + last;
   };
-  if (span(H, sqh, M, sqm, D) >= lim || span(H, soh, M, som, D) >= lim) return RSPX_EUNSUPPORTED;
+  if (span(H, sqh, M, sqm, D) >= lim) return RSPX_EUNSUPPORTED;
+  if (out_tiled ? (int64_t)((M + 63) / 64) * 64 * H * D >= lim : span(H, soh, M, som, D) >= lim)
+    return RSPX_EUNSUPPORTED;
   if (P > 0 && (span(HK, skph, P, skpn, D) >= lim || span(HK, svph, P, svpn, D) >= lim)) return RSPX_EUNSUPPORTED;
   if (NN > 0 && (span(HK, sknh, NN, sknn, D) >= lim || span(HK, svnh, NN, svnn, D) >= lim ||
                  span(M, smm, NN, smn, 1) >= lim))
@@ -1721,7 +1740,7 @@ static int trie_attn_impl(const void* q, int64_t sqh, int64_t sqm, const void* k
   a.kn = static_cast<const uint16_t*>(kn); a.sknh = (int)sknh; a.sknn = (int)sknn;
   a.vn = static_cast<const uint16_t*>(vn); a.svnh = (int)svnh; a.svnn = (int)svnn;
   a.msk = msk; a.smm = (int)smm; a.smn = (int)smn;
-  a.out = static_cast<uint16_t*>(out); a.soh = (int)soh; a.som = (int)som;
+  a.out = static_cast<uint16_t*>(out); a.soh = out_tiled ? -1 : (int)soh; a.som = out_tiled ? 0 : (int)som;
   a.HK = HK; a.GQS = __builtin_ctz(pl.GQA); a.M = M; a.P = P; a.NN = NN;
   a.R = pl.R; a.NRB = pl.NRB; a.NG = pl.NG; a.S = pl.S;
   a.c = (float)((double)sm_scale * 1.4426950408889634);

@@ -21,11 +21,12 @@ the epilogue adds them in chunk order and rounds to bf16 -- the exact value
 rspx_linear would store -- so no separate reduction launch is needed.
     logits = y . Wlm^T (fp32)                        rspx_linear
 
-The normalised rows y and the SwiGLU output m, read only by linear layers,
-stay in the tiled activation layout (RSPX_TILED), and every weight matrix is
-held in the tiled weight layout (kernels.gemm.tile_weight): the linear layers
-then load both operands a whole MFMA tile per instruction, with the same
-result bits as from row-major operands.
+The normalised rows y, the attention output and the SwiGLU output m, read
+only by linear layers, stay in the tiled activation layout (RSPX_TILED), and
+every weight matrix is held in the tiled weight layout
+(kernels.gemm.tile_weight): the linear layers then load both operands a whole
+MFMA tile per instruction, with the same result bits as from row-major
+operands.
 
 Each kernel computes a row with arithmetic that does not depend on how many
 rows the call carries, and attention folds a row's node slots in slot order,
@@ -228,7 +229,7 @@ class Decoder:
         cos, sin = self._rope_rows(positions, cache.cap)
         slots32 = slots.to(torch.int32)
         qo = torch.empty((T, HQ, D), dtype=bf, device=dev)
-        att = torch.empty((T, HQ, D), dtype=bf, device=dev)
+        att = torch.empty(rows * HQ * D, dtype=bf, device=dev)   # attention output [T, HQ D], tiled
         mlp = torch.empty(rows * cfg.ffn, dtype=bf, device=dev)  # SwiGLU output [T, F], tiled when fused
         ws_attn = self._workspace("attn", L.rspx_trie_attn_workspace_bytes(HQ, HK, T, P, D))
         for li, lay in enumerate(self.layers):
@@ -239,8 +240,8 @@ class Decoder:
                 sin.data_ptr(), cos.stride(0), slots32.data_ptr(), cache.cap, ck.data_ptr(), ck.stride(0), ck.stride(1),
                 cv.data_ptr(), cv.stride(0), cv.stride(1), qo.data_ptr(), T, HQ, HK, D, cfg.eps, s))
             trie_attn(qo.permute(1, 0, 2), ck[:, :P], cv[:, :P], ck[:, P:P + NN], cv[:, P:P + NN], msk,
-                      self.sm_scale, out=att.permute(1, 0, 2), workspace=ws_attn)
-            hp, S = self._partials(att.data_ptr(), HQ * D, T, lay.to)
+                      self.sm_scale, out=att, workspace=ws_attn, out_tiled=True)
+            hp, S = self._partials(att.data_ptr(), TILED, T, lay.to)
             _lib.check("rspx_add_rmsnorm_partials", L.rspx_add_rmsnorm_partials(
                 x.data_ptr(), Hd, hp, S, lay.post_norm.data_ptr(), x.data_ptr(), Hd, y.data_ptr(), TILED,
                 T, Hd, cfg.eps, s))

@@ -22,12 +22,14 @@ from ._tensor import as_kernel_input
 
 
 def trie_attn(q, kp, vp, kn, vn, msk, sm_scale=None, out=None, rows_per_wave: int = 0, workspace=None,
-              launches: int = 0):
+              launches: int = 0, out_tiled: bool = False):
     """Launch the kernel on the current stream.  ``rows_per_wave`` (0/1/2) and
     ``launches`` (0 = automatic, 1 = one kernel when it fits, 2 = two kernels)
     only change the work split, never the result.  ``workspace``: a zero-filled
     uint8 GPU tensor of at least rspx_trie_attn_workspace_bytes bytes (default:
-    a per-stream scratch buffer)."""
+    a per-stream scratch buffer).  ``out_tiled``: ``out`` is a flat bf16 buffer
+    of at least ceil(M / 64) 64 H D elements that receives the [M, H D] result
+    in the tiled activation layout (RSPX_TILED) instead of [H, M, D]."""
     H, M, D = q.shape
     HK, P, D2 = kp.shape
     NN = kn.shape[1]
@@ -47,8 +49,14 @@ def trie_attn(q, kp, vp, kn, vn, msk, sm_scale=None, out=None, rows_per_wave: in
         raise RuntimeError("fused_attn_hyb: msk must be a GPU tensor")
     if msk.dtype not in (torch.bool, torch.uint8):
         msk = msk != 0
-    if out is None:
-        out = torch.empty((H, M, D), dtype=torch.bfloat16, device=dev)
+    if out_tiled:
+        if out is None or out.dtype != torch.bfloat16 or out.numel() < -(-M // 64) * 64 * H * D:
+            raise ValueError("fused_attn_hyb: out_tiled needs a bf16 buffer of ceil(M/64)*64*H*D elements")
+        soh, som = D, _lib.RSPX_TILED
+    else:
+        if out is None:
+            out = torch.empty((H, M, D), dtype=torch.bfloat16, device=dev)
+        soh, som = out.stride(0), out.stride(1)
     L = _lib.lib()
     need = L.rspx_trie_attn_workspace_bytes(H, HK, M, P, D)
     if need < 0:
@@ -65,7 +73,7 @@ def trie_attn(q, kp, vp, kn, vn, msk, sm_scale=None, out=None, rows_per_wave: in
         kn.data_ptr(), kn.stride(0), kn.stride(1),
         vn.data_ptr(), vn.stride(0), vn.stride(1),
         msk.data_ptr(), msk.stride(0), msk.stride(1),
-        out.data_ptr(), out.stride(0), out.stride(1),
+        out.data_ptr(), soh, som,
         H, HK, M, P, NN, D, float(sm_scale),
         ws.data_ptr(), ws.numel(), int(rows_per_wave), *extra,
         _lib.stream_ptr(dev))

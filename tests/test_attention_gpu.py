@@ -453,3 +453,25 @@ def test_wait_that_gives_up_poisons_its_rows(which):
     assert torch.isnan(bad.float()).all()
     good = _run(c, launches=1, workspace=ws)
     assert torch.equal(good, ref)
+
+
+@pytest.mark.parametrize("which", ["cfg2", "n128b70", "one", "d64"])
+def test_tiled_output_is_the_strided_output(which):
+    """out with som = RSPX_TILED (the [M, H D] matrix in the tiled activation layout)
+    holds the strided call's values bit for bit, through one and two launches; rows
+    past M of the last 64-row block are not written."""
+    from _tiled import from_tiled
+    c = {"cfg2": gen.cfg2, "one": lambda: gen.path_case(gen.cfg2(), 10),
+         "d64": lambda: gen.attn_case(7, 16, 2, 64, 3086, 3, 9, 0, 6, None),
+         "n128b70": lambda: gen.attn_case(10, 32, 8, 128, 3072, 8, 32, 0, 32, 128, kv_scale=128 ** -0.5,
+                                          base=70)}[which]()
+    H, M, D = c.q.shape
+    print(f"[tiled out] {which} H={H} M={M} D={D}", flush=True)
+    ref = _run(c)                                           # [H, M, D]
+    want = ref.permute(1, 0, 2).reshape(M, H * D)
+    n = -(-M // 64) * 64 * H * D
+    for launches in (0, 1, 2):
+        buf = torch.full((n,), float("nan"), dtype=torch.bfloat16, device="cuda")
+        _run(c, out=buf, out_tiled=True, launches=launches)
+        assert torch.equal(from_tiled(buf, M, H * D), want)
+        assert torch.isnan(buf.float()).sum().item() == (-(-M // 64) * 64 - M) * H * D
