@@ -195,11 +195,13 @@ def counter_probe(args) -> int:
     """Child run for rocprofv3 --pmc (MFMA counters): per dispatch, in this order, three
     attention calls at 8B heads with a 3072-token prompt KV and tries of 16, 64 and 128
     nodes, then the 64-row linear layers of one 8B decoder layer (q/k/v [6144, 4096],
-    o [4096, 4096], gate/up [24576, 4096], down [4096, 12288]) once each."""
+    o [4096, 4096], gate/up [24576, 4096], down [4096, 12288]) once each, with x and the
+    weights in the tiled layouts the decoder step uses."""
     import torch
 
     from respect_amd import _lib
     from respect_amd.kernels.attention import make_launcher
+    from respect_amd.kernels.gemm import tile_weight
     from respect_amd.workloads import AttnWorkload, merged_trie
     for n, seqs, length, lo, hi in ((16, 2, 10, 4, 4), (64, 4, 24, 0, 16), (128, 5, 32, 8, 8)):
         wl = AttnWorkload(P=3072, tree=merged_trie(7, seqs, length, lo, hi, n), sets=1, seed=n)
@@ -210,12 +212,14 @@ def counter_probe(args) -> int:
     L = _lib.lib()
     dev = torch.device("cuda")
     s = _lib.stream_ptr(dev)
-    x = torch.randn(64, 12288, device=dev).to(torch.bfloat16)
+    x = torch.randn(64 * 12288, device=dev).to(torch.bfloat16)   # tiled [64, K] for K <= 12288
+    T = _lib.RSPX_TILED
     for N, K in ((6144, 4096), (4096, 4096), (24576, 4096), (4096, 12288)):
-        w = (0.02 * torch.randn(N, K, device=dev)).to(torch.bfloat16)
+        w = tile_weight((0.02 * torch.randn(N, K, device=dev)).to(torch.bfloat16))
         y = torch.empty(64, N, device=dev, dtype=torch.bfloat16)
         ws = torch.zeros(max(16, L.rspx_linear_workspace_bytes(64, N, K)), dtype=torch.uint8, device=dev)
-        _lib.check("rspx_linear", L.rspx_linear(x.data_ptr(), 12288, w.data_ptr(), K, y.data_ptr(), N, 64, N, K, 0,
+        torch.cuda.synchronize()
+        _lib.check("rspx_linear", L.rspx_linear(x.data_ptr(), T, w.data_ptr(), T, y.data_ptr(), N, 64, N, K, 0,
                                                 ws.data_ptr(), ws.numel(), s))
         torch.cuda.synchronize()
         _log(f"counter probe: linear 64 x [{N}, {K}]")
