@@ -89,10 +89,10 @@ class Layer:
         self.tqkv = tile_weight(w(cfg.qkv_rows, H))  # [q | k | v] rows
         self.q_norm = norm_w(D)
         self.k_norm = norm_w(D)
-        self.to = tile_weight(w(H, cfg.heads * D))
+        self.tout = tile_weight(w(H, cfg.heads * D))
         self.post_norm = norm_w(H)
         wgu = w(2 * F, H)                            # [gate | up] rows
-        self.td = tile_weight(w(H, F))
+        self.tdown = tile_weight(w(H, F))
         # With one K chunk the gate/up product carries SwiGLU in its epilogue
         # (rspx_linear_silu), which wants the rows interleaved: 2i gate i, 2i + 1 up i.
         self.gu_fused = _lib.lib().rspx_linear_splits(2 * F, H) == 1
@@ -104,11 +104,11 @@ class Layer:
 
     @property
     def wo(self) -> torch.Tensor:
-        return self.to.dense()
+        return self.tout.dense()
 
     @property
     def wd(self) -> torch.Tensor:
-        return self.td.dense()
+        return self.tdown.dense()
 
     @property
     def wgu(self) -> torch.Tensor:
@@ -241,7 +241,7 @@ class Decoder:
                 cv.data_ptr(), cv.stride(0), cv.stride(1), qo.data_ptr(), T, HQ, HK, D, cfg.eps, s))
             trie_attn(qo.permute(1, 0, 2), ck[:, :P], cv[:, :P], ck[:, P:P + NN], cv[:, P:P + NN], msk,
                       self.sm_scale, out=att, workspace=ws_attn, out_tiled=True)
-            hp, S = self._partials(att.data_ptr(), TILED, T, lay.to)
+            hp, S = self._partials(att.data_ptr(), TILED, T, lay.tout)
             _lib.check("rspx_add_rmsnorm_partials", L.rspx_add_rmsnorm_partials(
                 x.data_ptr(), Hd, hp, S, lay.post_norm.data_ptr(), x.data_ptr(), Hd, y.data_ptr(), TILED,
                 T, Hd, cfg.eps, s))
@@ -256,7 +256,7 @@ class Decoder:
                 _lib.check("rspx_silu_mul", L.rspx_silu_mul(gu.data_ptr(), gu.stride(0), gu.data_ptr() + 2 * F,
                                                             gu.stride(0), mlp.data_ptr(), F, T, F, s))
                 msx = F
-            hp, S = self._partials(mlp.data_ptr(), msx, T, lay.td)
+            hp, S = self._partials(mlp.data_ptr(), msx, T, lay.tdown)
             nxt = self.layers[li + 1].in_norm if li + 1 < len(self.layers) else self.final_norm
             _lib.check("rspx_add_rmsnorm_partials", L.rspx_add_rmsnorm_partials(
                 x.data_ptr(), Hd, hp, S, nxt.data_ptr(), x.data_ptr(), Hd, y.data_ptr(), TILED,
