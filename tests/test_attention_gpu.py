@@ -475,3 +475,26 @@ def test_tiled_output_is_the_strided_output(which):
         _run(c, out=buf, out_tiled=True, launches=launches)
         assert torch.equal(from_tiled(buf, M, H * D), want)
         assert torch.isnan(buf.float()).sum().item() == (-(-M // 64) * 64 - M) * H * D
+
+
+def test_tiled_output_rejects_a_head_stride_other_than_d():
+    """som = RSPX_TILED names the [M, H D] layout, whose head stride is D: any other soh is
+    RSPX_EINVAL and nothing is launched."""
+    from respect_amd import _lib
+    c = gen.cfg1()
+    H, M, D = c.q.shape
+    HK, P, _ = c.kp.shape
+    NN = c.kn.shape[1]
+    L = _lib.lib()
+    q, kp, vp, kn, vn = (_dev(a) for a in (c.q, c.kp, c.vp, c.kn, c.vn))
+    msk = _dev(c.msk, None)
+    out = torch.full((-(-M // 64) * 64 * H * D,), 7.0, dtype=torch.bfloat16, device="cuda")
+    ws = torch.zeros(L.rspx_trie_attn_workspace_bytes(H, HK, M, P, D), dtype=torch.uint8, device="cuda")
+    args = (q.data_ptr(), q.stride(0), q.stride(1), kp.data_ptr(), kp.stride(0), kp.stride(1),
+            vp.data_ptr(), vp.stride(0), vp.stride(1), kn.data_ptr(), kn.stride(0), kn.stride(1),
+            vn.data_ptr(), vn.stride(0), vn.stride(1), msk.data_ptr(), msk.stride(0), msk.stride(1), out.data_ptr())
+    tail = (H, HK, M, P, NN, D, c.sm_scale, ws.data_ptr(), ws.numel(), 0, _lib.stream_ptr(q.device))
+    assert L.rspx_trie_attn(*args, 2 * D, _lib.RSPX_TILED, *tail) == -1   # RSPX_EINVAL
+    torch.cuda.synchronize()
+    assert torch.all(out == 7.0)
+    assert L.rspx_trie_attn(*args, D, _lib.RSPX_TILED, *tail) == 0
