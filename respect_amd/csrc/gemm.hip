@@ -16,9 +16,10 @@
 // chunk count S comes from 64-column tiles whatever W is, so W never changes
 // a bit of the result).  W -- the large operand, read exactly once -- goes
 // straight from HBM into the MFMA A operand registers (lane (n16, g4) loads
-// W[col n16][k + 8 g4, +8): 16 contiguous bytes), double-buffered in rounds
-// of 8 k-blocks.  X (at most 64 rows) is shared by the 4 waves: each round of
-// it is copied into LDS with direct-to-LDS loads laid out as MFMA B fragments
+// W[col n16][k + 8 g4, +8): 16 contiguous bytes), in rounds of 8 k-blocks
+// requested 3 rounds ahead.  X (at most 64 rows) is shared by the block's
+// waves: each round of it is copied into LDS with direct-to-LDS loads laid
+// out as MFMA B fragments
 // (one conflict-free ds_read_b128 per 16-row tile and k-block).  The output
 // tile D[n][m] comes back as 4 consecutive columns per lane.
 //
