@@ -19,9 +19,9 @@
 // W[col n16][k + 8 g4, +8): 16 contiguous bytes), in rounds of 8 k-blocks
 // requested 3 rounds ahead.  X (at most 64 rows) is shared by the block's
 // waves: each round of it is copied into LDS with direct-to-LDS loads laid
-// out as MFMA B fragments
-// (one conflict-free ds_read_b128 per 16-row tile and k-block).  The output
-// tile D[n][m] comes back as 4 consecutive columns per lane.
+// out as MFMA B fragments (one conflict-free ds_read_b128 per 16-row tile and
+// k-block).  The output tile D[n][m] comes back as 4 consecutive columns per
+// lane.
 //
 // x may also come in the tiled layout (row stride RSPX_TILED, tiled_offset in
 // common.h): a 64-row block's k-block is then four 1 KB operand tiles, and
