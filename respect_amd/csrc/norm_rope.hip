@@ -157,26 +157,27 @@ __global__ __launch_bounds__(256) void rmsnorm_small_kernel(RowIn in, const uint
   rms_row_wave<TPR, VPL, MODE, SC>(in, row, w, y, sy, sub, n, eps);
 }
 
-// Long rows: one 256-thread workgroup per row, VPL 8-element vectors per
+// Long rows: one TH-thread workgroup per row, VPL 8-element vectors per
 // thread.  Wave sums are combined in wave order through LDS.
-template <int VPL, int MODE, int SC>
-__global__ __launch_bounds__(256) void rmsnorm_row_kernel(RowIn in, const uint16_t* w, uint16_t* y, int64_t sy, int n,
-                                                          float eps) {
-  __shared__ float part[4];
+template <int VPL, int MODE, int SC, int TH = 256>
+__global__ __launch_bounds__(TH) void rmsnorm_row_kernel(RowIn in, const uint16_t* w, uint16_t* y, int64_t sy, int n,
+                                                         float eps) {
+  constexpr int NW = TH / 64;
+  __shared__ float part[NW];
   const int row = blockIdx.x;
   const int t = threadIdx.x, lane = __lane_id(), wv = t >> 6;
   // The weights are requested first (see rms_row_wave).
   u32x4 wraw[VPL];
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
-    const int c = (v * 256 + t) * 8;
+    const int c = (v * TH + t) * 8;
     wraw[v] = c < n ? *reinterpret_cast<const u32x4*>(w + c) : u32x4{0u, 0u, 0u, 0u};
   }
   float xv[VPL][8];
   float ss = 0.f;
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
-    const int c = (v * 256 + t) * 8;
+    const int c = (v * TH + t) * 8;
     if (c < n) {
       load_row_vec<MODE, SC>(in, row, c, xv[v]);
     } else {
@@ -189,11 +190,13 @@ __global__ __launch_bounds__(256) void rmsnorm_row_kernel(RowIn in, const uint16
   ss = lane_group_sum<64>(ss);
   if (lane == 0) part[wv] = ss;
   __syncthreads();
-  const float tot = ((part[0] + part[1]) + part[2]) + part[3];
+  float tot = part[0];
+#pragma unroll
+  for (int k = 1; k < NW; ++k) tot = tot + part[k];
   const float r = rsqrt_rn(tot / (float)n + eps);
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
-    const int c = (v * 256 + t) * 8;
+    const int c = (v * TH + t) * 8;
     if (c < n) {
       float wvv[8], o[8];
       unpack8(wraw[v], wvv);
@@ -417,7 +420,7 @@ static void launch_rmsnorm(const RowIn& in, const uint16_t* W, uint16_t* Y, int6
   } else if (vec <= 256) {
     hipLaunchKernelGGL((rmsnorm_row_kernel<1, MODE, SC>), dim3(rows), dim3(256), 0, s, in, W, Y, sy, n, eps);
   } else if (vec <= 512) {
-    hipLaunchKernelGGL((rmsnorm_row_kernel<2, MODE, SC>), dim3(rows), dim3(256), 0, s, in, W, Y, sy, n, eps);
+    hipLaunchKernelGGL((rmsnorm_row_kernel<1, MODE, SC, 512>), dim3(rows), dim3(512), 0, s, in, W, Y, sy, n, eps);
   } else if (vec <= 1024) {
     hipLaunchKernelGGL((rmsnorm_row_kernel<4, MODE, SC>), dim3(rows), dim3(256), 0, s, in, W, Y, sy, n, eps);
   } else {
