@@ -1732,6 +1732,8 @@ static int trie_attn_impl(const void* q, int64_t sqh, int64_t sqm, const void* k
   if (NN > 0 && (span(HK, sknh, NN, sknn, D) >= lim || span(HK, svnh, NN, svnn, D) >= lim ||
                  span(M, smm, NN, smn, 1) >= lim))
     return RSPX_EUNSUPPORTED;
+  // The group partials too ([HK][R][NG][D] fp32, addressed with 32-bit byte offsets).
+  if ((int64_t)(pl.total - pl.off_gp_acc) >= 2 * lim) return RSPX_EUNSUPPORTED;
 
   TrieAttnArgs a;
   a.q = static_cast<const uint16_t*>(q);   a.sqh = (int)sqh;   a.sqm = (int)sqm;

@@ -58,6 +58,7 @@ def test_attn_argument_errors(lib):
     assert _attn(lib, stride=100) == -4           # stride not a multiple of 8
     assert _attn(lib, M=0) == 0                   # nothing to do, no launch
     assert _attn(lib, NN=4104) == -1              # node segment beyond NMAX = 4096
+    assert _attn(lib, M=17000, P=3072, ws=1 << 40) == -2   # group partials past 2^31 bytes
     assert lib.rspx_trie_attn_workspace_bytes(32, 8, 64, 3072, 128) > 65536
     assert lib.rspx_trie_attn_workspace_bytes(32, 8, 64, 3072, 96) < 0
 
