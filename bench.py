@@ -614,7 +614,8 @@ def bench_committed(args) -> dict:
 
 
 def bench_floor(args) -> dict:
-    """What the 8B-shape attention launch costs before any arithmetic (rspx_floor_launch):
+    """What the 8B-shape attention launch costs before any arithmetic (bench_floor.so, a
+    bench-only library built from bench_floor.hip):
     its grid (256 x 512 threads, 147 KB LDS) empty; streaming each workgroup's K/V share
     with every load in flight (196 KB per workgroup, each byte read by 4 row blocks, as the
     attention reads it; and 49 KB unique shares); and the attention's own 2-round
@@ -624,7 +625,13 @@ def bench_floor(args) -> dict:
     import torch
 
     from respect_amd import _lib
-    L = _lib.lib()
+    so = Path(__file__).resolve().with_name("bench_floor.so")
+    if not so.exists():
+        raise RuntimeError("bench_floor.so is not built (__graft_entry__.build() builds it)")
+    fl = ctypes.CDLL(str(so))
+    fl.rspx_bench_floor_launch.restype = ctypes.c_int
+    fl.rspx_bench_floor_launch.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                           ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     dev = torch.device("cuda")
     g = torch.Generator(device=dev)
     g.manual_seed(4)
@@ -635,8 +642,9 @@ def bench_floor(args) -> dict:
     res = {}
     for which, name in ((0, "empty_grid_us"), (1, "stream_196KB_per_wg_us"), (2, "stream_49KB_unique_us"),
                         (3, "ring_schedule_us")):
-        ls = [_launcher(L.rspx_floor_launch, which, ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
-                        ctypes.c_void_p(out.data_ptr()), s) for k, v in sets]
+        ls = [_launcher(fl.rspx_bench_floor_launch, which, ctypes.c_void_p(k.data_ptr()),
+                        ctypes.c_void_p(v.data_ptr()), 8, 3072, 128, ctypes.c_void_p(out.data_ptr()), s)
+              for k, v in sets]
         res[name] = round(time_launches(ls, args.steps, args.warmup) * 1e3, 2)
     res["workload"] = ("the attention's 8B-shape grid over K/V [8, 3072, 128] bf16: empty, streaming, "
                        "and its own load schedule without arithmetic")

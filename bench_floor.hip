@@ -1,6 +1,7 @@
-// Measurement kernels for the trie-attention roofline (no counterpart in the
-// reference): what a launch of the attention's 8B-shape grid costs before any
-// arithmetic.  256 workgroups of 512 threads holding 147 KB of LDS each (one
+// Bench-only measurement kernels for the trie-attention roofline (no
+// counterpart in the reference; built into bench_floor.so next to bench.py,
+// not into the product library): what a launch of the attention's 8B-shape
+// grid costs before any arithmetic.  256 workgroups of 512 threads holding 147 KB of LDS each (one
 // per CU, as fused_kernel<128, 2>), over K and V of 8 kv heads x 3072 keys x
 // head_dim 128 bf16.  Workgroup b takes kv head b % 8, row block (b / 8) % 4
 // and key group b / 32 (keys [384 q, 384 q + 384)), as the attention does.
@@ -15,10 +16,12 @@
 // Every load is a raw-buffer load whose descriptor covers exactly one head of
 // K (or V), so nothing outside the tensors is read; results feed a
 // never-taken store so that no load is dropped.
-#include "common.h"
-#include "respect_amd.h"
+#include <hip/hip_runtime.h>
 
-namespace rspx {
+#include <cstdint>
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 namespace floor_probe {
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -85,21 +88,28 @@ __global__ __launch_bounds__(512) void ring_kernel(const uint16_t* K, const uint
 }
 
 }  // namespace floor_probe
-}  // namespace rspx
 
-using namespace rspx::floor_probe;
+using namespace floor_probe;
 
-extern "C" int rspx_floor_launch(int which, const void* K, const void* V, void* out, void* stream) {
-  static bool attr = false;
-  if (!attr) {
+// which: 0 empty grid, 1 stream, 2 stream with unique shares, 3 ring (above).
+// K and V are [HK][P][D] bf16, contiguous; only HK 8, P 3072, D 128 (the shape
+// the kernels' descriptors are built for) is accepted, so no load can leave
+// the tensors.  Returns 0, or -1 for a bad argument or shape, -5 for a HIP
+// error.  out: >= 256 x 512 ints (never written in practice).
+extern "C" int rspx_bench_floor_launch(int which, const void* K, const void* V, int HK, int P, int D, void* out,
+                                       void* stream) {
+  if (which < 0 || which > 3) return -1;
+  if (which > 0 && (!K || !V || HK != 8 || P != kKeys || D != 128)) return -1;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return -5;
+  static bool attr[64];
+  if (!attr[dev]) {
     const void* fns[] = {(const void*)empty_kernel, (const void*)stream_kernel<false>, (const void*)stream_kernel<true>,
                          (const void*)ring_kernel};
     for (const void* f : fns)
-      if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kLds) != hipSuccess) return RSPX_ELAUNCH;
-    attr = true;
+      if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kLds) != hipSuccess) return -5;
+    attr[dev] = true;
   }
-  if (which < 0 || which > 3) return RSPX_EINVAL;
-  if (which > 0 && (!K || !V)) return RSPX_EINVAL;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint16_t* k = static_cast<const uint16_t*>(K);
   const uint16_t* v = static_cast<const uint16_t*>(V);
@@ -111,5 +121,5 @@ extern "C" int rspx_floor_launch(int which, const void* K, const void* V, void* 
     case 2: hipLaunchKernelGGL(stream_kernel<true>, grid, blk, kLds, s, k, v, o); break;
     default: hipLaunchKernelGGL(ring_kernel, grid, blk, kLds, s, k, v, o); break;
   }
-  return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
+  return hipGetLastError() == hipSuccess ? 0 : -5;
 }

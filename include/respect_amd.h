@@ -139,12 +139,19 @@ int rspx_trie_attn_launches(const void* q, int64_t sqh, int64_t sqm, const void*
                             float sm_scale, void* workspace, int64_t workspace_bytes, int rows_per_wave, int launches,
                             void* stream);
 
-/* 1 if a one-launch call on this workspace ever ran out of its bounded wait,
- * 0 if not, < 0 on error.  Synchronises the stream.  A workgroup whose wait
- * runs out stores NaN in every element of the output rows it merges, so such
- * a call's output carries the failure without this query.
+/* 1 if a one-launch call on this workspace ran out of its bounded wait since
+ * the flag was last cleared, 0 if not, < 0 on error; a set flag is cleared
+ * (each failure is reported once).  workspace NULL: the static scratch of
+ * rspx_trie_attn_noalloc on the current device.  Synchronises the stream, so
+ * it cannot be called under graph capture.  A workgroup whose wait runs out
+ * (after 4 ms of the device's real-time counter) stores NaN in every element
+ * of the output rows it merges, so such a call's output carries the failure
+ * without this query.  The flag is the workspace's first int
+ * (RSPX_ATTN_STATUS_WORD): a caller may copy it to the host with a copy it
+ * already makes instead of calling this function, and zero it itself.
  */
-int rspx_trie_attn_status(const void* workspace, int H, int HK, int M, int P, int D, void* stream);
+#define RSPX_ATTN_STATUS_WORD 0
+int rspx_trie_attn_status(void* workspace, int H, int HK, int M, int P, int D, void* stream);
 
 /* rspx_trie_attn without a workspace argument: no counterpart in the
  * reference; for callers that cannot allocate device memory (code under HIP
@@ -155,7 +162,10 @@ int rspx_trie_attn_status(const void* workspace, int H, int HK, int M, int P, in
  * RSPX_EWORKSPACE (the 8B shape holds up to 251 query rows at 3072 prompt
  * keys).  Every call on one GPU shares that GPU's array: calls that overlap
  * on one GPU (two streams, two host threads) race and give invalid results.
- * Same results, bit for bit, as rspx_trie_attn.
+ * The array is zero when the library is loaded (static storage), so no call
+ * needs a fill first, on any stream; its timeout flag is read and cleared by
+ * rspx_trie_attn_status(NULL, ...).  Same results, bit for bit, as
+ * rspx_trie_attn.
  */
 int rspx_trie_attn_noalloc(const void* q, int64_t sqh, int64_t sqm, const void* kp, int64_t skph, int64_t skpn,
                            const void* vp, int64_t svph, int64_t svpn, const void* kn, int64_t sknh, int64_t sknn,
@@ -178,21 +188,12 @@ int rspx_blocked_attn(const void* q, int64_t sqh, int64_t sqm, const void* kp, i
                       void* out, int64_t soh, int64_t som, int H, int HK, int M, int P, int NN, int D, int BN,
                       float sm_scale, void* stream);
 
-/* Measurement kernels, no counterpart in the reference: the floor of the
- * 8B-shape attention launch (256 workgroups x 512 threads, 147 KB LDS each)
- * over K, V [8][3072][128] bf16 (out: >= 256 x 512 ints, never written in
- * practice).  which: 0 empty grid; 1 every workgroup streams its 196 KB share
- * of K/V (each byte read by 4 row blocks) with all loads in flight; 2 the same
- * with 49 KB unique shares; 3 the attention's own 2-round direct-to-LDS load
- * schedule without its arithmetic.
- */
-int rspx_floor_launch(int which, const void* K, const void* V, void* out, void* stream);
-
 /* Test hook, no counterpart in the reference: sets how many times a one-launch
  * workgroup polls its row block's counter before its wait gives up (a
- * negative value restores the default, 2^22 polls); returns the previous
- * value.  Lets a test drive the give-up path while every kernel still exits
- * normally.  Process-wide, not thread-safe; read at each launch.
+ * negative value restores the default: no poll bound, the 4 ms deadline
+ * alone ends a wait); returns the previous value.  Lets a test drive the
+ * give-up path (0 polls: every wait gives up at once) while every kernel still
+ * exits normally.  Process-wide, not thread-safe; read at each launch.
  */
 int rspx_trie_attn_set_spin_limit(int polls);
 

@@ -46,7 +46,6 @@ SIGNATURES: dict[str, tuple] = {
         _i32, _i32, _i32, _i32, _i32, _i32, _f32, _c_p, _i64, _i32, _i32, _c_p]),
     "rspx_trie_attn_status": (_i32, [_c_p, _i32, _i32, _i32, _i32, _i32, _c_p]),
     "rspx_trie_attn_set_spin_limit": (_i32, [_i32]),
-    "rspx_floor_launch": (_i32, [_i32, _c_p, _c_p, _c_p, _c_p]),
     "rspx_blocked_attn": (_i32, [
         _c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _i64, _i64,
         _c_p, _i64, _i64, _c_p, _i64, _i64,
@@ -125,6 +124,12 @@ def stream_ptr(device: torch.device) -> int:
 
 
 _WORKSPACES: dict = {}
+
+
+def current_workspace(device: torch.device, tag: str = "attn") -> torch.Tensor | None:
+    """The current stream's scratch of ``tag`` if one was made, else None."""
+    stream = torch.cuda.current_stream(device)
+    return _WORKSPACES.get((device.index, stream.cuda_stream, tag))
 
 
 def workspace(device: torch.device, nbytes: int, tag: str = "attn") -> torch.Tensor:

@@ -83,6 +83,23 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
     return LIB
 
 
+def build_bench_floor(verbose: bool = False) -> Path:
+    """Compile ``bench_floor.hip`` (repository root; bench-only launch-floor probes,
+    not part of the product ABI) into ``bench_floor.so`` beside it."""
+    src = ROOT / "bench_floor.hip"
+    out = ROOT / "bench_floor.so"
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIPCC_FLAGS, "-shared", "-o", str(tmp), str(src)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("hipcc failed on bench_floor.hip:\n" + r.stdout + r.stderr)
+    os.replace(tmp, out)
+    return out
+
+
 if __name__ == "__main__":
     path = build(verbose="-v" in sys.argv)
     print(path)
+    print(build_bench_floor(verbose="-v" in sys.argv))

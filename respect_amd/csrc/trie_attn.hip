@@ -96,7 +96,9 @@ struct TrieAttnArgs {
   float* gp_acc;      // [HK][R][NG][D]
   int* sync;          // fused launch: a timeout flag, then [HK][NRB][2] counters
   int spin;           // fused launch: polls of a block's counter before the wait gives up
+  int deadline;       // fused launch: s_memrealtime ticks a wait may last before it gives up
 };
+static_assert(sizeof(TrieAttnArgs) == 184, "kernel argument struct stays at 184 bytes");
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -1424,6 +1426,11 @@ __device__ __forceinline__ void nan_rows(const TrieAttnArgs& A, int g, int p0, i
 // read.  The last workgroup of a block to finish resets the block's counters
 // to zero, whether or not a wait gave up.
 //
+// The wait is bounded in time: kWaitMs milliseconds of the device's
+// constant-rate real-time counter (s_memrealtime, hipDeviceAttributeWallClockRate
+// kHz), far beyond a call's normal length (tens of microseconds), short enough
+// that a broken co-residency surfaces as a failed call instead of a stall.
+//
 // Visibility without cache-wide fences: every word that crosses workgroups
 // (group partials, counters) is written by an agent-scope atomic store or
 // read-modify-write and read by a load with the same coherence bit (sc1) as an
@@ -1434,10 +1441,26 @@ __device__ __forceinline__ void nan_rows(const TrieAttnArgs& A, int g, int p0, i
 // wait has returned.  A release/acquire pair at agent scope (buffer_wbl2 and
 // buffer_inv of the whole L2) would order the same accesses at several
 // microseconds per workgroup.
-constexpr int kSpinLimit = 1 << 22;
+constexpr int kSpinLimit = 0x7fffffff;   // no poll bound of its own: the deadline ends a wait
+constexpr int kWaitMs = 4;
 // Polls before a fused launch's wait gives up (rspx_trie_attn_set_spin_limit
 // lowers it so tests can exercise the give-up path with every kernel exiting).
 static int g_spin_limit = kSpinLimit;
+
+// kWaitMs in s_memrealtime ticks of the current device (100 MHz if the rate
+// cannot be queried).
+static int wait_deadline_ticks() {
+  static int ticks[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kWaitMs * 100000;
+  if (ticks[dev] == 0) {
+    int khz = 0;
+    if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0) khz = 100000;
+    const int64_t t = (int64_t)khz * kWaitMs;
+    ticks[dev] = (int)(t < 0x7fffffff ? t : 0x7fffffff);
+  }
+  return ticks[dev];
+}
 constexpr int kSyncWords = 4096;   // timeout flag + [HK][NRB][2] counters
 
 // Rows [r0, rend) merged by workgroup (g, rb, q) of a fused launch: its share
@@ -1469,10 +1492,14 @@ __device__ __forceinline__ void block_tail(const TrieAttnArgs& A, char* lds, int
   if (r0 < rend) {
     const lds_float* np = node_rows<D>(A, g, r0, rend0, (lds_char*)lds, w, pre, pf);
     if (w == 0) {
+      // Bounded in time (A.deadline ticks of the constant-rate real-time
+      // counter) and in polls (A.spin, lowered only by a test hook).
       int v = 0;
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
       for (int it = 0; it < A.spin; ++it) {
         v = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (v >= A.NG) break;
+        if (__builtin_amdgcn_s_memrealtime() - t0 > (uint64_t)A.deadline) break;
         __builtin_amdgcn_s_sleep(2);
       }
       if (lane == 0) {
@@ -1751,6 +1778,7 @@ static int trie_attn_impl(const void* q, int64_t sqh, int64_t sqm, const void* k
   a.gp_acc = reinterpret_cast<float*>(ws + pl.off_gp_acc);
   a.sync = reinterpret_cast<int*>(ws + pl.off_sync);
   a.spin = g_spin_limit;
+  a.deadline = wait_deadline_ticks();
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (D) {
@@ -1776,33 +1804,29 @@ extern "C" int rspx_trie_attn(const void* q, int64_t sqh, int64_t sqm, const voi
 // ------------------------------------------------------------------ allocation-free variant
 // A workspace that lives in the code object: one per GPU the library runs on,
 // held until the process ends.  Its first kSyncWords ints are the one-launch
-// synchronisation words (zero between calls: every call leaves them at zero);
-// the group partials follow, as in a caller's workspace.  In host code the
-// array's name is only a stand-in: the device address comes from
-// hipGetSymbolAddress, once per device, and is what kernels are given.
+// synchronisation words; the group partials follow, as in a caller's
+// workspace.  The array has static storage with no initialiser, so the code
+// object's loader hands it over zero-filled on every device before any call
+// (no fill kernel, nothing to order against the first call's stream); every
+// call leaves the counters at zero again and rspx_trie_attn_status(NULL, ...)
+// clears the timeout flag it reports.  In host code the array's name is only a
+// stand-in: the device address comes from hipGetSymbolAddress, once per
+// device, and is what kernels are given.
 constexpr size_t kStaticScratchBytes = size_t(32) << 20;
 static __device__ __align__(256) char scratch[kStaticScratchBytes];
-
-__global__ void zero_words_kernel(int* p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0;
-}
 
 static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[64];
 
-// Device address of this device's scratch; the first call on a device looks it
-// up and queues a fill kernel that zeroes the synchronisation words.
-static int static_scratch(void** out, hipStream_t s) {
+// Device address of the current device's scratch (looked up on the first call
+// on that device; no device work is queued).
+static int static_scratch(void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return RSPX_ELAUNCH;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return RSPX_ELAUNCH;
-    hipLaunchKernelGGL(zero_words_kernel, dim3((kSyncWords + 255) / 256), dim3(256), 0, s, static_cast<int*>(p),
-                       kSyncWords);
-    if (hipGetLastError() != hipSuccess) return RSPX_ELAUNCH;
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];
@@ -1821,7 +1845,7 @@ extern "C" int rspx_trie_attn_noalloc(const void* q, int64_t sqh, int64_t sqm, c
   if (pl.total > kStaticScratchBytes) return RSPX_EWORKSPACE;
   if (M == 0) return RSPX_OK;
   void* ws = nullptr;
-  const int sr = static_scratch(&ws, static_cast<hipStream_t>(stream));
+  const int sr = static_scratch(&ws);
   if (sr != RSPX_OK) return sr;
   return trie_attn_impl(q, sqh, sqm, kp, skph, skpn, vp, svph, svpn, kn, sknh, sknn, vn, svnh, svnn, msk, smm, smn,
                         out, soh, som, H, HK, M, P, NN, D, sm_scale, ws, (int64_t)kStaticScratchBytes, rows_per_wave,
@@ -1847,14 +1871,23 @@ extern "C" int rspx_trie_attn_set_spin_limit(int polls) {
   return prev;
 }
 
-extern "C" int rspx_trie_attn_status(const void* workspace, int H, int HK, int M, int P, int D, void* stream) {
+extern "C" int rspx_trie_attn_status(void* workspace, int H, int HK, int M, int P, int D, void* stream) {
   Plan pl;
-  if (make_plan(H, HK, M, P, 0, D, 1, &pl) != RSPX_OK || !workspace) return RSPX_EINVAL;
+  if (make_plan(H, HK, M, P, 0, D, 1, &pl) != RSPX_OK) return RSPX_EINVAL;
+  void* ws = workspace;
+  if (!ws && static_scratch(&ws) != RSPX_OK) return RSPX_ELAUNCH;
+  int* flag = reinterpret_cast<int*>(static_cast<char*>(ws) + pl.off_sync);
   int v = 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (hipMemcpyAsync(&v, static_cast<const char*>(workspace) + pl.off_sync, sizeof(int), hipMemcpyDeviceToHost, s) !=
-          hipSuccess ||
+  if (hipMemcpyAsync(&v, flag, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess ||
       hipStreamSynchronize(s) != hipSuccess)
     return RSPX_ELAUNCH;
+  if (v != 0) {
+    // Read and clear: the flag reports each failure once.
+    static const int zero = 0;
+    if (hipMemcpyAsync(flag, &zero, sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+      return RSPX_ELAUNCH;
+  }
   return v ? 1 : 0;
 }

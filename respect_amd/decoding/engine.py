@@ -42,7 +42,7 @@ from dataclasses import dataclass
 import torch
 
 from .. import _lib
-from ..kernels.attention import trie_attn
+from ..kernels.attention import raise_if_gave_up, status_word, trie_attn
 from ..kernels.gemm import TiledWeight, tile_weight
 from ..system.fused import rope_tables
 from .acceptance import greedy_token
@@ -137,6 +137,7 @@ class Decoder:
             (torch.randn(cfg.vocab, cfg.hidden, generator=g, device=self.device) * std).to(torch.bfloat16))
         self.sm_scale = cfg.head_dim ** -0.5
         self._ws = {}
+        self.attn_ws_used = None   # attention workspace of the last forward (eager or replayed)
         self._ws_retired = []   # outgrown buffers: a captured graph may still point at them
         self._rope = None       # (cos, sin) [positions, head_dim] bf16 tables
         self._graphs: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
@@ -232,6 +233,7 @@ class Decoder:
         att = torch.empty(rows * HQ * D, dtype=bf, device=dev)   # attention output [T, HQ D], tiled
         mlp = torch.empty(rows * cfg.ffn, dtype=bf, device=dev)  # SwiGLU output [T, F], tiled when fused
         ws_attn = self._workspace("attn", L.rspx_trie_attn_workspace_bytes(HQ, HK, T, P, D))
+        self.attn_ws_used = ws_attn   # its first word flags a wait that gave up (kernels.attention.status_word)
         for li, lay in enumerate(self.layers):
             ck, cv = cache.k[li], cache.v[li]
             qkvp, S = self._partials(y.data_ptr(), TILED, T, lay.tqkv)
@@ -318,6 +320,7 @@ class GraphedForward:
 
     def __init__(self, model: Decoder, cache, P: int, T: int, NN: int):
         dev = model.device
+        self.model = model
         if P + NN > cache.cap - T:
             raise ValueError("KV cache has no room for the graph's scratch slots")
         self.T, self.NN = T, NN
@@ -357,6 +360,10 @@ class GraphedForward:
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             self.logits = body()
+        # The attention workspace the captured calls use, and a pinned host word
+        # for its timeout flag: greedy() copies the flag with the picks.
+        self.attn_ws = model.attn_ws_used
+        self.flag_host = torch.zeros(1, dtype=torch.int32).pin_memory()
 
     def run(self, n: int, base: int, tokens, parents) -> torch.Tensor:
         """Replay for the n-node trie ``tokens`` / ``parents`` (parents precede
@@ -372,12 +379,15 @@ class GraphedForward:
         self.desc.copy_(self.host, non_blocking=True)
         self.copied.record()
         self.graph.replay()
+        self.model.attn_ws_used = self.attn_ws
         return self.logits
 
     def greedy(self, n: int) -> list[int]:
         """The greedy tokens of rows [0, n) of the last replay (rspx_argmax_rows
         over the whole vocabulary, taken inside the graph), on the host."""
         self.picks_host[:n].copy_(self.picks[:n], non_blocking=True)
+        self.flag_host.copy_(status_word(self.attn_ws), non_blocking=True)
         self.picked.record()
         self.picked.synchronize()
+        raise_if_gave_up(int(self.flag_host[0]), self.attn_ws)
         return self.picks_host[:n].tolist()

@@ -9,6 +9,9 @@ node and each node only to its ancestors.  ``forward_tokens_hf`` is the 1-token
 path of respect/decoding/sequential.py:17-27 on the same cache layout, the
 reference every verified row must equal bit for bit.
 
+Both raise AttentionWaitError when an attention call of theirs gave up its
+bounded wait (rows of NaN), before the caller commits anything.
+
 ``model(input_ids=, position_ids=, attention_mask=, past_key_values=,
 use_cache=True)`` must return an object with ``.logits`` (any Hugging Face
 causal LM does); ``cache`` is a ``hf_kv.WindowCache``.
@@ -19,7 +22,9 @@ from typing import Any
 
 import torch
 
+from .. import _lib
 from ..candidates.trie import Trie, trie_ancestry
+from ..kernels.attention import raise_if_gave_up, status_word
 
 
 @torch.no_grad()
@@ -37,7 +42,21 @@ def verify_trie_hf(model: Any, cache: Any, tree: Trie, prompt_len: int, base: in
     allow[0, 0, :, start:start + q] = torch.from_numpy(trie_ancestry(tree)).to(dev)
     cache.set_positions(torch.arange(start, start + q, device=dev))
     out = model(input_ids=ids, position_ids=pos, attention_mask=allow, past_key_values=cache, use_cache=True)
+    _check_attention(dev)
     return out.logits[0]
+
+
+def _check_attention(dev) -> None:
+    """Raise AttentionWaitError (and clear the flag) if a trie-attention call of
+    the forward just run on this stream gave up its bounded wait: its rows are
+    NaN, so the step must not be committed (the caller falls back, as the
+    reference's dispatcher does on a kernel error, dispatch.py:116-122).  One
+    word copied to the host."""
+    if dev.type != "cuda":
+        return
+    ws = _lib.current_workspace(dev)
+    if ws is not None:
+        raise_if_gave_up(int(status_word(ws).item()), ws)
 
 
 @torch.no_grad()
@@ -56,4 +75,5 @@ def forward_tokens_hf(model: Any, cache: Any, token_ids: list[int], slot: int, p
         out = model(input_ids=torch.tensor([[t]], device=dev), position_ids=torch.tensor([[position + j]], device=dev),
                     attention_mask=allow, past_key_values=cache, use_cache=True)
         rows.append(out.logits[0, -1])
+    _check_attention(dev)
     return torch.stack(rows)

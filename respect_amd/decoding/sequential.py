@@ -4,6 +4,7 @@ from __future__ import annotations
 
 import torch
 
+from ..kernels.attention import raise_if_gave_up, status_word
 from .acceptance import greedy_token
 from .verify import node_slots
 
@@ -48,5 +49,8 @@ def sequential(model, cache, token: int, P: int, base: int, eos: int, offset: in
         c += 1
         if token == eos:
             break
-        token = int(greedy_token(logits, offset, size).item())
+        # the attention's timeout flag comes back with the choice (one copy)
+        ws = model.attn_ws_used
+        token, flag = torch.cat([greedy_token(logits, offset, size), status_word(ws).to(torch.int64)]).tolist()
+        raise_if_gave_up(flag, ws)
     return out

@@ -81,6 +81,30 @@ def trie_attn(q, kp, vp, kn, vn, msk, sm_scale=None, out=None, rows_per_wave: in
     return out
 
 
+class AttentionWaitError(RuntimeError):
+    """A one-launch attention call ran out of its bounded wait (its workgroups
+    were not all resident at once): its output rows hold NaN.  Raised by the
+    verification steps before anything is committed, so the caller can fall
+    back (the reference falls back to stock SDPA on any kernel error,
+    respect/kernels/dispatch.py:116-122)."""
+
+
+def status_word(workspace: torch.Tensor) -> torch.Tensor:
+    """The timeout flag of an attention workspace: an int32 [1] view of its
+    first word (RSPX_ATTN_STATUS_WORD), nonzero once a call on it gave up."""
+    return workspace[:4].view(torch.int32)
+
+
+def raise_if_gave_up(flag: int, workspace: torch.Tensor) -> None:
+    """``flag``: the host copy of ``status_word(workspace)`` taken after the
+    calls to check.  Nonzero: clear the word (on the current stream) and raise
+    AttentionWaitError."""
+    if flag:
+        status_word(workspace).zero_()
+        raise AttentionWaitError("trie attention: a one-launch wait gave up (workgroups not co-resident); "
+                                 "the call's output rows are NaN and nothing was committed")
+
+
 def fused_attn_hyb(q, kp, vp, kn, vn, msk, sm_scale=None,
                    BM=64, BN=128, BNB=16, num_warps=4, num_stages=1):
     """q (H, M, D), kp/vp (HK, NP, D), kn/vn (HK, NN, D), msk (M, NN) bool -> (H, M, D)."""

@@ -449,10 +449,12 @@ def test_wait_that_gives_up_poisons_its_rows(which):
     finally:
         L.rspx_trie_attn_set_spin_limit(prev)
     assert _status(c, ws) == 1
+    assert _status(c, ws) == 0          # the query clears what it reports
     # a limit of 0 polls gives up in every workgroup: every row is NaN in every element
     assert torch.isnan(bad.float()).all()
     good = _run(c, launches=1, workspace=ws)
     assert torch.equal(good, ref)
+    assert _status(c, ws) == 0
 
 
 @pytest.mark.parametrize("which", ["cfg2", "n128b70", "one", "d64"])

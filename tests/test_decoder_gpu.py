@@ -255,3 +255,45 @@ def test_capacity_is_enforced(model):
         forward_token(model, cache, 1, P, cache.cap - P)
     with pytest.raises(ValueError):
         model.prefill(torch.zeros(cache.cap + 1, dtype=torch.int64, device="cuda"), cache)
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_attention_wait_that_gives_up_fails_the_step(model, graph):
+    """An attention wait that gives up (0 polls through the test hook, so every kernel
+    still exits normally) makes the verification step raise AttentionWaitError at the
+    device-to-host copy it already makes, before the walk: no token is returned and the
+    cache is not compacted.  The flag is cleared, and the next step on the same cache
+    gives the clean step's tokens and KV bit for bit."""
+    from respect_amd import _lib
+    from respect_amd.decoding.acceptance import greedy_token
+    from respect_amd.decoding.respect import respect_step
+    from respect_amd.kernels.attention import AttentionWaitError, status_word
+    L = _lib.lib()
+    ref_cache, last = _filled_cache(model)
+    t0 = int(greedy_token(last).item())
+    rng = np.random.default_rng(3)
+    tree = _trie([t0] + [int(t) for t in rng.integers(0, 4096, 30)], rng)
+    want = respect_step(model, ref_cache, tree, t0, P, 0, eos=-1, graph=graph)
+    model.release_graphs()
+    cache, _ = _filled_cache(model)
+    compacted = []
+    real_compact = cache.compact
+    cache.compact = lambda *a: compacted.append(a)
+    prev = L.rspx_trie_attn_set_spin_limit(0)
+    print(f"[give-up step] graph={graph} nodes={len(tree.nodes)}", flush=True)
+    try:
+        with pytest.raises(AttentionWaitError):
+            respect_step(model, cache, tree, t0, P, 0, eos=-1, graph=graph)
+    finally:
+        L.rspx_trie_attn_set_spin_limit(prev)
+        cache.compact = real_compact
+    assert compacted == []
+    assert int(status_word(model.attn_ws_used).item()) == 0
+    model.release_graphs()          # a graph captured under the lowered limit keeps it
+    got = respect_step(model, cache, tree, t0, P, 0, eos=-1, graph=graph)
+    assert got == want
+    for li in range(model.cfg.layers):
+        s1 = P + len(want[0])
+        assert torch.equal(cache.k[li][:, :s1], ref_cache.k[li][:, :s1])
+        assert torch.equal(cache.v[li][:, :s1], ref_cache.v[li][:, :s1])
+    model.release_graphs()

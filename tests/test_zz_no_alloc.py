@@ -1,7 +1,8 @@
 """rspx_trie_attn_noalloc (the entry point that allocates nothing, its scratch a static
 device array) against rspx_trie_attn with a caller workspace, through the C ABI: bitwise
 equal on two calls in a row, the second smaller than the first, and sizes beyond the
-static scratch refused with RSPX_EWORKSPACE before any launch."""
+static scratch refused with RSPX_EWORKSPACE before any launch; its timeout flag read and
+cleared without a workspace pointer."""
 import numpy as np
 import pytest
 import torch
@@ -53,6 +54,37 @@ def test_noalloc_equals_workspace_entry_point():
                                         0, s) == 0
         torch.cuda.synchronize()
         assert torch.equal(got2, ref), name
+
+
+def test_noalloc_wait_that_gives_up_is_reported_and_cleared():
+    """The static scratch's timeout flag: read and cleared by rspx_trie_attn_status(NULL, ...)
+    (no workspace pointer); a call whose waits give up (0 polls, forced from the host so every
+    kernel exits normally) is reported once, and the next call on the same scratch is clean."""
+    from respect_amd import _lib
+    L = _lib.lib()
+    s = _lib.stream_ptr(torch.device("cuda"))
+    c = gen.cfg1(seed=5)
+    q, kp, vp, kn, vn, msk = _tensors(c)
+    H, HK, M, P, NN, D = _shape(q, kp, kn)
+    print(f"[noalloc give-up] H={H} HK={HK} M={M} P={P} NN={NN} D={D}", flush=True)
+    assert L.rspx_trie_attn_status(None, H, HK, M, P, D, s) == 0
+    ref = torch.empty_like(q)
+    assert L.rspx_trie_attn_noalloc(*_args(q, kp, vp, kn, vn, msk, ref), H, HK, M, P, NN, D, D ** -0.5, 0, s) == 0
+    bad = torch.empty_like(q)
+    prev = L.rspx_trie_attn_set_spin_limit(0)
+    try:
+        assert L.rspx_trie_attn_noalloc(*_args(q, kp, vp, kn, vn, msk, bad), H, HK, M, P, NN, D, D ** -0.5,
+                                        0, s) == 0
+    finally:
+        L.rspx_trie_attn_set_spin_limit(prev)
+    assert L.rspx_trie_attn_status(None, H, HK, M, P, D, s) == 1
+    assert L.rspx_trie_attn_status(None, H, HK, M, P, D, s) == 0
+    assert torch.isnan(bad.float()).all()
+    good = torch.empty_like(q)
+    assert L.rspx_trie_attn_noalloc(*_args(q, kp, vp, kn, vn, msk, good), H, HK, M, P, NN, D, D ** -0.5, 0, s) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(good, ref)
+    assert L.rspx_trie_attn_status(None, H, HK, M, P, D, s) == 0
 
 
 def test_noalloc_refuses_sizes_beyond_its_scratch():
