@@ -62,14 +62,23 @@ def time_launches(launchers, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
-def cpu_threads() -> int:
-    """Host threads for the CPU baseline: the cores this process may run on, at most 16
-    (a GPU box's CPU share per GPU)."""
+CPU_SHARE = 16   # host CPUs a one-GPU box allots to the GPU's job (its OMP_NUM_THREADS)
+
+
+def cpu_counts() -> dict:
+    """The host's logical CPU count, how many this process may run on (affinity) and
+    the thread count the CPU baseline uses: the affinity count, at most the box's
+    CPU share per GPU (CPU_SHARE; the rest of the host belongs to other GPUs' jobs)."""
+    total = os.cpu_count() or 1
     try:
-        n = len(os.sched_getaffinity(0))
+        aff = len(os.sched_getaffinity(0))
     except AttributeError:  # pragma: no cover
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+        aff = total
+    return {"os_cpu_count": total, "affinity_cpus": aff, "threads": max(1, min(CPU_SHARE, aff))}
+
+
+def cpu_threads() -> int:
+    return cpu_counts()["threads"]
 
 
 def cpu_baseline_attn(wl, budget_s: float = 20.0) -> dict:
@@ -117,7 +126,9 @@ def cpu_baseline_attn(wl, budget_s: float = 20.0) -> dict:
             t0 = time.perf_counter()
             A.attn_hyb(qn, kpn, vpn, knn, vnn, msk.numpy(), wl.sm_scale)
             fold.append(time.perf_counter() - t0)
+    cc = cpu_counts()
     return {"value": round(med * 1e6, 1), "unit": "us per call", "cores": threads, "kind": "port",
+            "os_cpu_count": cc["os_cpu_count"], "affinity_cpus": cc["affinity_cpus"],
             "sample": f"{len(times)} full calls of the 8B-shape 64-node attention on input set 0: fp32 masked "
                       f"SDPA in PyTorch on {threads} host threads (median)",
             "literal_fold": {"value": round(statistics.median(fold) * 1e6, 1), "unit": "us per call", "cores": 1,
