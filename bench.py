@@ -676,6 +676,66 @@ def bench_copy(args) -> dict:
             "GBps": round(nbytes / t / 1e9, 1), "hbm_frac_of_peak": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+PHASES = ("round 0 landed", "round 0 computed", "round 1 landed", "round 1 computed", "round 2 landed",
+          "round 2 computed", "quarter (m, l) exchanged", "scaled quarters written", "quarter sums stored",
+          "node data issued", "partial stored and counted", "node partials", "counter wait", "merge",
+          "counters released")
+
+
+def phase_trace(args) -> int:
+    """The one-launch attention's phase timeline at the headline shape, from the trace build
+    (librespect_amd_trace.so, ``python -m respect_amd.build --phase-trace``): every wave
+    records s_memrealtime (100 MHz) at 16 marks; after back-to-back calls over rotating
+    input sets, the last call's marks are read back.  Per workgroup a phase ends when its
+    last wave passes the mark; printed: the median over workgroups of each phase's length
+    and of each mark's time after the earliest start."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from respect_amd import _lib
+    trace_so = _lib.LIB_PATH.with_name("librespect_amd_trace.so")
+    if not trace_so.exists():
+        print("librespect_amd_trace.so is not built: python -m respect_amd.build --phase-trace", file=sys.stderr)
+        return 2
+    _lib.LIB_PATH = trace_so
+    L = _lib.lib()
+    L.rspx_trie_attn_phase_trace.restype = ctypes.c_int
+    L.rspx_trie_attn_phase_trace.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+    from respect_amd.kernels.attention import make_launcher
+    from respect_amd.workloads import AttnWorkload
+    wl = AttnWorkload(sets=args.sets, seed=0)
+    launchers = [make_launcher(*st, wl.msk, wl.sm_scale)[0] for st in wl.sets]
+    for i in range(40):
+        launchers[i % len(launchers)]()
+    torch.cuda.synchronize()
+    WGS, WAVES, MARKS = 1024, 8, 16
+    buf = np.zeros(WGS * WAVES * MARKS, dtype=np.uint64)
+    _lib.check("rspx_trie_attn_phase_trace", L.rspx_trie_attn_phase_trace(buf.ctypes.data, buf.size))
+    nwg = 256
+    t = buf.reshape(WGS, WAVES, MARKS)[:nwg].astype(np.int64)
+    t0 = t[:, :, 0].min()
+    ends = t.max(axis=1) - t0                     # [wg, mark]: last wave past the mark
+    starts = t[:, :, 0].min(axis=1) - t0
+    span = (ends[:, 15].max() - starts.min()) * 10 / 1000
+    rows = []
+    prev = starts
+    for k in range(1, MARKS):
+        d = (ends[:, k] - prev) * 10 / 1000       # 100 MHz ticks -> us
+        rows.append({"phase": PHASES[k - 1], "median_us": round(float(np.median(d)), 2),
+                     "max_us": round(float(d.max()), 2), "ends_at_us": round(float(np.median(ends[:, k])) / 100, 2)})
+        prev = ends[:, k]
+    out = {"workload": "8B-shape attention, 64-node trie, KV 3072: the last of 40 back-to-back calls",
+           "workgroups": nwg, "start_spread_us": round(float(starts.max() - starts.min()) / 100, 2),
+           "first_start_to_last_end_us": round(float(span), 2),
+           "wg_length_median_us": round(float(np.median(ends[:, 15] - starts)) / 100, 2), "phases": rows}
+    print(json.dumps(out), flush=True)
+    for r in rows:
+        print(f"  {r['phase']:<28} {r['median_us']:6.2f} us  (max {r['max_us']:6.2f}, ends at {r['ends_at_us']:6.2f})")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -690,6 +750,8 @@ def main() -> int:
     ap.add_argument("--no-decoder", action="store_true", help="skip the 36-layer verification-step line")
     ap.add_argument("--decoder-steps", type=int, default=4, help="timed verification steps")
     ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--phase-trace", action="store_true",
+                    help="phase timeline of the headline call from the trace build (librespect_amd_trace.so)")
     ap.add_argument("--counter-probe", action="store_true",
                     help="a few attention and linear-layer dispatches for rocprofv3 --pmc (MFMA counters)")
     args = ap.parse_args()
@@ -697,6 +759,8 @@ def main() -> int:
         return traffic_probe(args)
     if args.counter_probe:
         return counter_probe(args)
+    if args.phase_trace:
+        return phase_trace(args)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: the verification kernels run on a single MI355X "

@@ -50,9 +50,17 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def build(verbose: bool = False, jobs: int = 8) -> Path:
-    """Compile every kernel source and link ``librespect_amd.so`` (always rebuilds)."""
+TRACE_LIB = PKG / "librespect_amd_trace.so"
+
+
+def build(verbose: bool = False, jobs: int = 8, trace: bool = False) -> Path:
+    """Compile every kernel source and link ``librespect_amd.so`` (always rebuilds).
+    ``trace``: the measurement variant ``librespect_amd_trace.so`` instead, built with
+    -DRSPX_PHASE_TRACE (the one-launch attention records per-wave phase timestamps,
+    read back by rspx_trie_attn_phase_trace; ``bench.py --phase-trace``)."""
     srcs = sources()
+    lib_out = TRACE_LIB if trace else LIB
+    flags = [*HIPCC_FLAGS, "-DRSPX_PHASE_TRACE"] if trace else HIPCC_FLAGS
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     cc = hipcc()
@@ -60,7 +68,7 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
         objs, procs = [], []
         for src in srcs:
             obj = Path(td) / (src.stem + ".o")
-            cmd = [cc, *HIPCC_FLAGS, "-I", str(INCLUDE), "-I", str(CSRC), "-c", str(src), "-o", str(obj)]
+            cmd = [cc, *flags, "-I", str(INCLUDE), "-I", str(CSRC), "-c", str(src), "-o", str(obj)]
             if verbose:
                 print(" ".join(cmd), flush=True)
             procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
@@ -74,13 +82,13 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
                 raise RuntimeError(f"hipcc failed on {src.name}:\n" + "\n".join(msgs))
             if verbose and msgs:
                 print("\n".join(msgs))
-        tmp = LIB.with_suffix(".so.tmp")
+        tmp = lib_out.with_suffix(".so.tmp")
         cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
             raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
-        os.replace(tmp, LIB)
-    return LIB
+        os.replace(tmp, lib_out)
+    return lib_out
 
 
 def build_bench_floor(verbose: bool = False) -> Path:
@@ -100,6 +108,8 @@ def build_bench_floor(verbose: bool = False) -> Path:
 
 
 if __name__ == "__main__":
-    path = build(verbose="-v" in sys.argv)
-    print(path)
-    print(build_bench_floor(verbose="-v" in sys.argv))
+    if "--phase-trace" in sys.argv:
+        print(build(verbose="-v" in sys.argv, trace=True))
+    else:
+        print(build(verbose="-v" in sys.argv))
+        print(build_bench_floor(verbose="-v" in sys.argv))

@@ -100,6 +100,31 @@ struct TrieAttnArgs {
 };
 static_assert(sizeof(TrieAttnArgs) == 184, "kernel argument struct stays at 184 bytes");
 
+// Phase timestamps (built only with -DRSPX_PHASE_TRACE, into a separate
+// library; the product library has none of this): wave w of workgroup b
+// records the device's real-time counter (s_memrealtime, 100 MHz) at mark k
+// of the one-launch kernel into g_phase[(b 8 + w) kPhaseMarks + k], read back
+// with rspx_trie_attn_phase_trace.  Marks: 0 start; 1 + 2 r / 2 + 2 r round
+// r (r < 3) landed / computed; 7 quarter (m, l) exchanged; 8 scaled quarters
+// written; 9 quarter sums and (m, l) stores done; 10 node data issued; 11
+// group partial stored and counted; 12 node partials done; 13 wait over; 14
+// merged; 15 counters released.
+constexpr int kPhaseMarks = 16;
+constexpr int kPhaseWgs = 1024;
+#ifdef RSPX_PHASE_TRACE
+__device__ uint64_t g_phase[kPhaseWgs * kWavesA * kPhaseMarks];
+#define RSPX_MARK(k)                                                                                   \
+  do {                                                                                                 \
+    if (__lane_id() == 0 && blockIdx.x < kPhaseWgs)                                                    \
+      g_phase[(blockIdx.x * kWavesA + (threadIdx.x >> 6)) * kPhaseMarks + (k)] =                       \
+          __builtin_amdgcn_s_memrealtime();                                                            \
+  } while (0)
+#else
+#define RSPX_MARK(k) \
+  do {               \
+  } while (0)
+#endif
+
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) char lds_char;
@@ -392,6 +417,7 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
     // Own chunks of round r (and the Q chunks, issued first) have landed.
     wait_rounds<G::OWN, G::RING>(min(nr - 1 - r, G::RING - 1));
     lds_barrier();   // every wave's chunks of round r are in LDS
+    if (r < 3) RSPX_MARK(1 + 2 * r);
     if (r == 0 && has_rows) {
 #pragma unroll
       for (int t = 0; t < kRT; ++t)
@@ -497,6 +523,7 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
         acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[t], acc[t][j], 0, 0, 0);
     }
     }
+    if (r < 3) RSPX_MARK(2 + 2 * r);
     // Round r is consumed by every wave: its ring slot takes round r + RING.
     if (r + G::RING < nr) {
       lds_barrier();
@@ -527,6 +554,7 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
       *(lds_f32x2*)(qml + (((4 * h + k) * kRT + t) * 16 + n16) * 2) = f32x2{mref[t], lrow[t]};
   }
   lds_barrier();
+  RSPX_MARK(7);
   float Mr[kRT], Lr[kRT];
 #pragma unroll
   for (int t = 0; t < kRT; ++t) {
@@ -551,6 +579,7 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
       *(lds_f32x4*)(dst + 4 * ((4 * j + g4) ^ (row & 7))) = acc[t][j] * own;
   }
   lds_barrier();
+  RSPX_MARK(8);
   // Group partial: rows RPI x + lane / (D / 4), columns [4 c4, +4): 1 KB per
   // store instruction; ATOMIC: with the coherence of an agent-scope atomic store.
   // With fewer pieces than waves (D = 32, one row tile) waves past the last
@@ -593,7 +622,9 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
   // Every wave's ring reads are complete: `before_stores` may issue
   // direct-to-LDS loads into the ring.
   lds_barrier();
+  RSPX_MARK(9);
   before_stores();
+  RSPX_MARK(10);
   const __amdgpu_buffer_rsrc_t racc = buffer_rsrc(A.gp_acc, 0x7fffffff);
 #pragma unroll
   for (int jj = 0; jj < NSW; ++jj) {
@@ -1491,6 +1522,7 @@ __device__ __forceinline__ void block_tail(const TrieAttnArgs& A, char* lds, int
   int* gave_up = reinterpret_cast<int*>(lds + node_area_bytes<D>());  // one LDS word past the node areas
   if (r0 < rend) {
     const lds_float* np = node_rows<D>(A, g, r0, rend0, (lds_char*)lds, w, pre, pf);
+    RSPX_MARK(12);
     if (w == 0) {
       // Bounded in time (A.deadline ticks of the constant-rate real-time
       // counter) and in polls (A.spin, lowered only by a test hook).
@@ -1509,9 +1541,11 @@ __device__ __forceinline__ void block_tail(const TrieAttnArgs& A, char* lds, int
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     }
     lds_barrier();
+    RSPX_MARK(13);
     const bool bad = __builtin_amdgcn_readfirstlane(*gave_up);
     if (bad) nan_rows<D>(A, g, r0, rend0, w);
     else merge_rounds<D, true>(A, g, r0, rend0, np, w);
+    RSPX_MARK(14);
     // Further batches (short prompts: few key groups, many rows per workgroup).
     for (int b0 = rend0; b0 < rend; b0 += kNodeRows) {
       const int be = min(rend, b0 + kNodeRows);
@@ -1530,6 +1564,7 @@ __device__ __forceinline__ void block_tail(const TrieAttnArgs& A, char* lds, int
       __hip_atomic_store(cnt + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+  RSPX_MARK(15);
 }
 
 // The group partial is complete in memory (each wave waited for its own
@@ -1538,6 +1573,7 @@ __device__ __forceinline__ void count_partial(const TrieAttnArgs& A, int g, int 
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
   lds_barrier();
+  RSPX_MARK(11);
   if (threadIdx.x == 0)
     __hip_atomic_fetch_add(A.sync + 1 + 2 * (g * A.NRB + rb), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1549,6 +1585,7 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   constexpr int LB = PromptLds<D, kRT>::BYTES > NB ? PromptLds<D, kRT>::BYTES : NB;
   static_assert(NB <= PromptLds<D, kRT>::RINGBYTES, "node LDS and the wait flag inside the ring");
   __shared__ __attribute__((aligned(16))) char lds[LB];
+  RSPX_MARK(0);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = blockIdx.x % A.HK;
   const int rest = blockIdx.x / A.HK;
@@ -1891,3 +1928,14 @@ extern "C" int rspx_trie_attn_status(void* workspace, int H, int HK, int M, int 
   }
   return v ? 1 : 0;
 }
+
+#ifdef RSPX_PHASE_TRACE
+// Trace builds only (not in the product library): copies the phase marks of
+// the last one-launch call, kPhaseWgs x 8 waves x kPhaseMarks uint64, to host.
+extern "C" int rspx_trie_attn_phase_trace(uint64_t* host, int64_t n) {
+  const size_t bytes = sizeof(uint64_t) * (size_t)kPhaseWgs * kWavesA * kPhaseMarks;
+  if (!host || n < (int64_t)(bytes / sizeof(uint64_t))) return RSPX_EINVAL;
+  if (hipDeviceSynchronize() != hipSuccess) return RSPX_ELAUNCH;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_phase), bytes) == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
+}
+#endif
