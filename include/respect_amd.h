@@ -14,6 +14,7 @@
  *   rspx_rope           respect/system/fused.py:67       rope(x, cos, sin)
  *   rspx_qk_norm_rope   respect/kernels/rmsnorm.py:25 followed by the RoPE of
  *                       HF apply_rotary_pos_emb (q_norm/k_norm + RoPE of one decoder layer)
+ *   rspx_rmsnorm_qk_norm_rope  rspx_rmsnorm and rspx_qk_norm_rope in one launch (no counterpart)
  *   rspx_silu_mul       respect/system/fused.py:116      silu_mul(g, u)
  *   rspx_linear         respect/kernels/gemm.py:30       linear(x, w, ..., out_dtype)
  *   rspx_add_rmsnorm    residual add (HF decoder layer) followed by rmsnorm, rmsnorm.py:25
@@ -201,9 +202,12 @@ int rspx_trie_attn_set_spin_limit(int polls);
  * y[r] = bf16(w * bf16(x[r] * rsqrt(mean(x[r]^2) + eps))), fp32 statistics
  * (replaces respect/kernels/rmsnorm.py:25 rmsnorm(x, w, eps)).
  * x, y: [rows, n] with row strides sx, sy (elements; sy may be RSPX_TILED,
- * then n % 32 == 0); w: [n].  n % 8 == 0,
- * n <= 16384.  The sum of squares of a row is taken in an order fixed by n,
- * so a row's output does not depend on `rows`.
+ * then n % 32 == 0); w: [n].  Any n > 0 (the reference's rmsnorm masks any
+ * N, rmsnorm.py:25-32): n % 8 == 0 and n <= 16384 take vectorised kernels
+ * (pointers and strides 16-byte aligned, RSPX_EALIGN otherwise); every other
+ * n a one-workgroup-per-row kernel with 2-byte element loads (2-byte
+ * alignment; row-major y only).  The sum of squares of a row is taken in an
+ * order fixed by n, so a row's output does not depend on `rows`.
  */
 int rspx_rmsnorm(const void* x, int64_t sx, const void* w, void* y, int64_t sy, int rows, int n, float eps,
                  void* stream);
@@ -226,17 +230,35 @@ int rspx_rope(const void* x, int64_t sxb, int64_t sxh, int64_t sxl, const void* 
  * respect/kernels/rmsnorm.py:25 on q/k heads followed by HF
  * apply_rotary_pos_emb).  q: [T, HQ, D] (strides sqt, sqh), k: [T, HK, D]
  * (skt, skh), wq/wk: [D], cos/sin: [T, D] (row stride scs), qo: [T, HQ, D],
- * ko: [T, HK, D] contiguous.  D == 128.  Bitwise equal to rspx_rmsnorm
- * followed by rspx_rope.
+ * ko: [T, HK, D] contiguous.  D % 16 == 0, D <= 512 (the head dims
+ * rspx_rope takes; RSPX_EUNSUPPORTED otherwise).  Bitwise equal to
+ * rspx_rmsnorm followed by rspx_rope at the same D.
  */
 int rspx_qk_norm_rope(const void* q, int64_t sqt, int64_t sqh, const void* k, int64_t skt, int64_t skh,
                       const void* wq, const void* wk, const void* cos, const void* sin, int64_t scs, void* qo,
                       void* ko, int T, int HQ, int HK, int D, float eps, void* stream);
 
+/* rspx_rmsnorm (x, w, y over rows x n, eps) and rspx_qk_norm_rope (q .. D,
+ * qk_eps) in one launch, for a caller whose two inputs are both ready: the
+ * RMSNorm rows and the q/k rows run in disjoint workgroups of one grid, each
+ * on the code of its own kernel, so every output is bitwise what the two
+ * calls give.  The size rules of both, with n % 8 == 0 and n <= 16384
+ * (RSPX_EUNSUPPORTED otherwise).  No counterpart in the reference, whose
+ * RMSNorm (rmsnorm.py:25) and RoPE (fused.py:67) are separate launches: it
+ * saves one launch where both stages are due together, as in the
+ * RMSNorm [64, 4096] + q/k RoPE workload of the element-wise benchmark.
+ */
+int rspx_rmsnorm_qk_norm_rope(const void* x, int64_t sx, const void* w, void* y, int64_t sy, int rows, int n,
+                              float eps, const void* q, int64_t sqt, int64_t sqh, const void* k, int64_t skt,
+                              int64_t skh, const void* wq, const void* wk, const void* cos, const void* sin,
+                              int64_t scs, void* qo, void* ko, int T, int HQ, int HK, int D, float qk_eps,
+                              void* stream);
+
 /* ---------------------------------------------------------------- SwiGLU
  * y = bf16(bf16(g / (1 + exp(-g))) * u)  (replaces respect/system/fused.py:116
  * silu_mul(g, u)).  g, u, y: [rows, cols] with row strides sg, su, sy; views
- * into one packed gate/up tensor are fine.  cols % 8 == 0.
+ * into one packed gate/up tensor are fine.  Any cols; 2-byte alignment (two
+ * elements per thread where cols, the strides and the pointers are even).
  */
 int rspx_silu_mul(const void* g, int64_t sg, const void* u, int64_t su, void* y, int64_t sy, int rows, int cols,
                   void* stream);
@@ -248,14 +270,20 @@ int rspx_silu_mul(const void* g, int64_t sg, const void* u, int64_t su, void* y,
  * caller's, as in the reference).  Row strides sx, sw, so in elements; rows
  * 16-byte aligned; sx may be RSPX_TILED, and so may sw: w is then in the
  * tiled weight layout rspx_linear_tile_weight writes (same results, bit for
- * bit).  N % 16 == 0, K % 256 == 0.
+ * bit).  Any M, N, K (the reference's kernel masks every edge,
+ * gemm.py:19-27): with N % 16 == 0 and K % 256 == 0 the streaming kernel
+ * runs; any other (N, K) runs one bounded-load MFMA chain per output tile,
+ * row-major operands only (RSPX_EUNSUPPORTED for RSPX_TILED), 2-byte
+ * alignment (4-byte for an fp32 out), row strides below 2^24 elements.
  *
  * Reduction order: K is cut into rspx_linear_splits(N, K) equal chunks (a
- * function of N and K only); each chunk is a fixed chain of bf16 MFMAs in
- * increasing k; chunk results are added in chunk order and rounded once.  A
- * row's output bits therefore do not depend on M.  With more than one chunk
- * the fp32 chunk partials go through `workspace`
- * (rspx_linear_workspace_bytes(M, N, K) bytes, 16-byte aligned).
+ * function of N and K only; 1 outside N % 16 == 0, K % 256 == 0); each chunk
+ * is a fixed chain of bf16 MFMAs over 32-wide k-blocks in increasing k (k
+ * past K reads as zero); chunk results are added in chunk order and rounded
+ * once.  A row's output bits therefore do not depend on M.  With more than
+ * one chunk the fp32 chunk partials go through `workspace`
+ * (rspx_linear_workspace_bytes(M, N, K) bytes, 16-byte aligned; 0 with one
+ * chunk).
  */
 int rspx_linear_splits(int N, int K);
 int64_t rspx_linear_workspace_bytes(int M, int N, int K);
@@ -280,6 +308,8 @@ int rspx_linear_silu(const void* x, int64_t sx, const void* w, int64_t sw, void*
  * rspx_linear_splits(N, K), also when S == 1) for a consumer that adds them
  * in chunk order and rounds -- rspx_add_rmsnorm_partials,
  * rspx_qkv_rope_cache_partials -- so the sum never takes a launch of its own.
+ * N % 16 == 0 and K % 256 == 0 (RSPX_EUNSUPPORTED otherwise), as for
+ * rspx_linear_silu.
  */
 int rspx_linear_partials(const void* x, int64_t sx, const void* w, int64_t sw, float* part, int M, int N, int K,
                          void* stream);
@@ -310,7 +340,8 @@ int rspx_add_rmsnorm(const void* r, int64_t sr, const void* h, int64_t sh, const
 /* The same with h given as the fp32 chunk partials hp[S][rows][n] of a
  * linear layer (rspx_linear_partials; 1 <= S <= 8, the most
  * rspx_linear_splits gives): h = bf16 of their chunk-order sum,
- * bit for bit the h rspx_linear would have produced.
+ * bit for bit the h rspx_linear would have produced.  n % 8 == 0 and
+ * n <= 16384 (RSPX_EUNSUPPORTED otherwise).
  */
 int rspx_add_rmsnorm_partials(const void* r, int64_t sr, const float* hp, int S, const void* w, void* xo, int64_t sxo,
                               void* y, int64_t sy, int rows, int n, float eps, void* stream);
@@ -320,7 +351,8 @@ int rspx_add_rmsnorm_partials(const void* r, int64_t sr, const float* hp, int S,
  * sqkv).  q and k get RMSNorm over head_dim (wq / wk) and RoPE (cos/sin rows
  * per token, stride scs) with the arithmetic of rspx_qk_norm_rope; q goes to
  * qo [T, HQ, D] (contiguous); k and v are written into the KV cache of the
- * layer: cache_k[h * skh + slots[t] * skn + d] (likewise v).  D == 128.
+ * layer: cache_k[h * skh + slots[t] * skn + d] (likewise v).  D % 16 == 0,
+ * D <= 512.
  * cap: slots per head of the cache.  A token whose slot lies outside
  * [0, cap) writes no K/V and gets a NaN q row (the reference's index_copy_
  * would raise a device-side assert; here the error reaches every output the

@@ -62,6 +62,9 @@ SIGNATURES: dict[str, tuple] = {
     "rspx_rope": (_i32, [_c_p, _i64, _i64, _i64, _c_p, _c_p, _i64, _i64, _c_p, _i32, _i32, _i32, _i32, _c_p]),
     "rspx_qk_norm_rope": (_i32, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _c_p,
                                  _i32, _i32, _i32, _i32, _f32, _c_p]),
+    "rspx_rmsnorm_qk_norm_rope": (_i32, [_c_p, _i64, _c_p, _c_p, _i64, _i32, _i32, _f32,
+                                         _c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _c_p,
+                                         _i32, _i32, _i32, _i32, _f32, _c_p]),
     "rspx_silu_mul": (_i32, [_c_p, _i64, _c_p, _i64, _c_p, _i64, _i32, _i32, _c_p]),
     "rspx_linear_splits": (_i32, [_i32, _i32]),
     "rspx_linear_workspace_bytes": (_i64, [_i32, _i32, _i32]),

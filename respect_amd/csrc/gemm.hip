@@ -418,6 +418,90 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* part, int S, i
   }
 }
 
+// Any shape outside gemm_kernel's (N % 16 != 0 or K % 256 != 0): one chain
+// of v_mfma_f32_16x16x32_bf16 over the 32-wide k-blocks of K in increasing k,
+// rounded once -- an order fixed by K alone, so a row's bits never depend on
+// M.  Workgroup = 4 waves on adjacent 16-column groups of a 64-column tile,
+// times one 64-row tile (MT row tiles of 16).  Operands go from memory
+// straight into the MFMA registers through bounded buffer loads: rows past M,
+// columns past N and k past K get an out-of-range offset and read as zero, so
+// they add exact zeros to the chain.  V16 (every row 16-byte aligned, K % 8
+// == 0): a lane's 8 consecutive k come in one 16-byte load, else in eight
+// 2-byte loads; both give the same operand values.
+struct AnyArgs {
+  const uint16_t* x; int64_t sx;  // [M, K]
+  const uint16_t* w; int64_t sw;  // [N, K]
+  void* out; int64_t so;          // [M, N], bf16 or fp32
+  int M, N, K, out_fp32;
+};
+
+// The MFMA operand of one lane: row `row` (element offset roff from the
+// descriptor's base; ok = the row exists), k .. k + 7.
+template <bool V16>
+__device__ __forceinline__ u32x4 any_frag(__amdgpu_buffer_rsrc_t r, int roff, bool ok, int k, int K) {
+  if constexpr (V16) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, ok && k < K ? (roff + k) * 2 : kOOB, 0, 0));
+  } else {
+    uint32_t h[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      h[j] = __builtin_amdgcn_raw_buffer_load_b16(r, ok && k + j < K ? (roff + k + j) * 2 : kOOB, 0, 0);
+    return u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+  }
+}
+
+template <int MT, bool V16>
+__global__ __launch_bounds__(256) void gemm_any_kernel(AnyArgs A) {
+  const int lane = __lane_id(), wv = threadIdx.x >> 6;
+  const int n16 = lane & 15, g4 = lane >> 4;
+  const int n0 = blockIdx.x * 64 + wv * 16, m0 = blockIdx.y * kRows;
+  if (n0 >= A.N) return;  // whole wave; no barriers below
+  const int nw = min(16, A.N - n0), mw = min(kRows, A.M - m0);
+  // Descriptors start at the wave's first column and the tile's first row,
+  // so every offset fits 31 bits (the host checks 64 rows of x and 16 of w).
+  const __amdgpu_buffer_rsrc_t rw = rsrc(A.w + (int64_t)n0 * A.sw, ((int64_t)(nw - 1) * A.sw + A.K) * 2);
+  const __amdgpu_buffer_rsrc_t rx = rsrc(A.x + (int64_t)m0 * A.sx, ((int64_t)(mw - 1) * A.sx + A.K) * 2);
+  const bool wok = n16 < nw;
+  const int woff = n16 * (int)A.sw;
+  int xoff[MT];
+  bool xok[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    xok[t] = 16 * t + n16 < mw;
+    xoff[t] = (16 * t + n16) * (int)A.sx;
+  }
+  f32x4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int nkb = (A.K + 31) >> 5;
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int k = 32 * kb + 8 * g4;
+    const u32x4 wf = any_frag<V16>(rw, woff, wok, k, A.K);
+    u32x4 xf[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) xf[t] = any_frag<V16>(rx, xoff[t], xok[t], k, A.K);
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wf), __builtin_bit_cast(bf16x8, xf[t]),
+                                                       acc[t], 0, 0, 0);
+  }
+  // acc[t][e] = D[column 4 g4 + e][row 16 t + n16] of the wave's tile.
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int m = m0 + 16 * t + n16;
+    if (m >= A.M) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int n = n0 + 4 * g4 + e;
+      if (n >= A.N) continue;
+      if (A.out_fp32)
+        static_cast<float*>(A.out)[(int64_t)m * A.so + n] = acc[t][e];
+      else
+        static_cast<uint16_t*>(A.out)[(int64_t)m * A.so + n] = f32_to_bf16_rne(acc[t][e]);
+    }
+  }
+}
+
 }  // namespace gemm
 
 // Chunk count of the K reduction: a function of (N, K) only.  More chunks
@@ -471,14 +555,18 @@ extern "C" int rspx_linear_tile_weight(const void* w, int64_t sw, int N, int K, 
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }
 
+// Shapes gemm_kernel takes; every other (N, K) runs gemm_any_kernel (one
+// K chain).  The choice depends on (N, K) only.
+static bool linear_fast_shape(int N, int K) { return N % 16 == 0 && K % gemm::kRoundK == 0; }
+
 extern "C" int rspx_linear_splits(int N, int K) {
-  if (N <= 0 || K <= 0 || K % gemm::kRoundK != 0) return -1;
-  return linear_splits(N, K);
+  if (N <= 0 || K <= 0) return -1;
+  return linear_fast_shape(N, K) ? linear_splits(N, K) : 1;
 }
 
 extern "C" int64_t rspx_linear_workspace_bytes(int M, int N, int K) {
-  if (M < 0 || N <= 0 || K <= 0 || K % gemm::kRoundK != 0) return -1;
-  const int S = linear_splits(N, K);
+  if (M < 0 || N <= 0 || K <= 0) return -1;
+  const int S = rspx_linear_splits(N, K);
   return S > 1 ? (int64_t)S * M * N * (int64_t)sizeof(float) : 0;
 }
 
@@ -572,8 +660,42 @@ static int linear_check(const void* x, int64_t sx, const void* w, int64_t sw, in
 }
 }  // namespace rspx
 
+// Any (N, K): row-major x and w with rows of at least K elements (2-byte
+// aligned, any stride below 2^24 elements), out [M, N] with row stride so.
+static int linear_any(const void* x, int64_t sx, const void* w, int64_t sw, void* out, int64_t so, int M, int N,
+                      int K, int out_fp32, hipStream_t s) {
+  if (M < 0 || N <= 0 || K <= 0) return RSPX_EINVAL;
+  if (M == 0) return RSPX_OK;
+  if (!x || !w || !out) return RSPX_EINVAL;
+  if (sx == kTiled || sw == kTiled) return RSPX_EUNSUPPORTED;  // the tiled layouts need N % 16, K % 32
+  if (sx < K || sw < K || so < N) return RSPX_EINVAL;
+  auto al = [](const void* p, unsigned a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
+  if (!al(x, 2) || !al(w, 2) || !al(out, out_fp32 ? 4 : 2)) return RSPX_EALIGN;
+  // 31-bit byte offsets inside one 64-row tile of x and one 16-row slice of w.
+  if (((int64_t)gemm::kRows * sx + K) * 2 >= (1ll << 31) - 64 || ((int64_t)16 * sw + K) * 2 >= (1ll << 31) - 64)
+    return RSPX_EUNSUPPORTED;
+  const int64_t gx = (N + 63) / 64, gy = (M + gemm::kRows - 1) / gemm::kRows;
+  if (gy > 65535) return RSPX_EUNSUPPORTED;
+  gemm::AnyArgs a{static_cast<const uint16_t*>(x), sx, static_cast<const uint16_t*>(w), sw, out, so, M, N, K,
+                  out_fp32 ? 1 : 0};
+  const bool v16 = K % 8 == 0 && sx % 8 == 0 && sw % 8 == 0 && al(x, 16) && al(w, 16);
+  const int mt = M >= gemm::kRows ? 4 : (M + 15) / 16;
+  const dim3 g((unsigned)gx, (unsigned)gy), b(256);
+#define RSPX_ANY_MT(V)                                                                   \
+  if (mt == 4) hipLaunchKernelGGL((gemm::gemm_any_kernel<4, V>), g, b, 0, s, a);         \
+  else if (mt == 3) hipLaunchKernelGGL((gemm::gemm_any_kernel<3, V>), g, b, 0, s, a);    \
+  else if (mt == 2) hipLaunchKernelGGL((gemm::gemm_any_kernel<2, V>), g, b, 0, s, a);    \
+  else hipLaunchKernelGGL((gemm::gemm_any_kernel<1, V>), g, b, 0, s, a);
+  if (v16) { RSPX_ANY_MT(true) }
+  else { RSPX_ANY_MT(false) }
+#undef RSPX_ANY_MT
+  return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
+}
+
 extern "C" int rspx_linear(const void* x, int64_t sx, const void* w, int64_t sw, void* out, int64_t so, int M, int N,
                            int K, int out_fp32, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (N > 0 && K > 0 && !linear_fast_shape(N, K))
+    return linear_any(x, sx, w, sw, out, so, M, N, K, out_fp32, static_cast<hipStream_t>(stream));
   int rc = linear_check(x, sx, w, sw, M, N, K);
   if (rc != RSPX_OK || M == 0) return rc;
   if (!out) return RSPX_EINVAL;

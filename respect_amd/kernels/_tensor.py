@@ -14,7 +14,9 @@ def _aligned(t: torch.Tensor, inner_contig: bool = True) -> bool:
 
 def as_kernel_input(t: torch.Tensor, name: str, dtype=torch.bfloat16) -> torch.Tensor:
     """Check device/dtype; return ``t`` itself when its layout suits the kernels
-    (contiguous last dim, 16-byte aligned rows), else a contiguous copy."""
+    (contiguous last dim, 16-byte aligned rows), else a contiguous copy that
+    starts 16-byte aligned (its rows are aligned too when the last dim is a
+    multiple of 8; the kernels take other lengths unaligned)."""
     if not t.is_cuda:
         raise RuntimeError(f"{name}: respect_amd kernels need a GPU tensor (got {t.device})")
     if t.dtype != dtype:
@@ -22,6 +24,6 @@ def as_kernel_input(t: torch.Tensor, name: str, dtype=torch.bfloat16) -> torch.T
     if _aligned(t):
         return t
     t = t.contiguous()
-    if not _aligned(t):
+    if t.data_ptr() % 16 != 0:
         t = t.clone()
     return t

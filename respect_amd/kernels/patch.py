@@ -14,10 +14,9 @@ then runs in an order that does not depend on how many rows a call carries.
 The language model is found as ``model.vlm.model[.language_model]`` (the
 reference's Alpamayo wrapper) or, for a plain Hugging Face causal LM, as
 ``model.model[.language_model]`` with ``lm_head`` beside it.  Before anything
-is swapped, every target is checked against what the kernels build (bf16
-weights, in_features % 256 == 0, out_features % 16 == 0; bf16 RMSNorms with
-``variance_epsilon``); the first misfit raises ``ValueError`` naming it and
-the model is left untouched.
+is swapped, every target is checked against what the kernels build (2-D bf16
+weights of any shape; bf16 RMSNorms with ``variance_epsilon``); the first
+misfit raises ``ValueError`` naming it and the model is left untouched.
 """
 from __future__ import annotations
 
@@ -111,8 +110,7 @@ def _language_model(model: Any) -> tuple[Any, Any]:
 
 def _fits_linear(mod: nn.Module) -> bool:
     w = getattr(mod, "weight", None)
-    return (w is not None and w.dim() == 2 and w.dtype == torch.bfloat16 and w.shape[1] % 256 == 0
-            and w.shape[0] % 16 == 0)
+    return w is not None and w.dim() == 2 and w.dtype == torch.bfloat16
 
 
 def _fits_norm(mod: nn.Module) -> bool:
@@ -140,8 +138,7 @@ def _plan(model: Any) -> list[tuple[str, nn.Module, str, Any]]:
         if not _fits_linear(mod):
             w = getattr(mod, "weight", None)
             shape = None if w is None else (tuple(w.shape), w.dtype)
-            raise ValueError(f"install: {name} {shape} is not a shape the row-invariant linear builds "
-                             "(bf16, in_features % 256 == 0, out_features % 16 == 0)")
+            raise ValueError(f"install: {name} {shape} is not a 2-D bf16 weight the row-invariant linear builds")
         todo.append((name, parent, attr, (lambda m: FixedLinear(m, "lm")) if kind == "lm" else FixedLinear))
 
     for i, layer in enumerate(lm.layers):

@@ -3,7 +3,8 @@
 Same call as respect/kernels/rmsnorm.py:25 (``rmsnorm(x, w, eps)``): the last
 dimension is normalised, rounding where PyTorch rounds (fp32 statistics, bf16
 after the scaling, bf16 after the weight).  The HIP kernel reduces a row in an
-order fixed by the row length alone (respect_amd/csrc/norm_rope.hip).
+order fixed by the row length alone (respect_amd/csrc/norm_rope.hip), for any
+row length.
 """
 from __future__ import annotations
 
@@ -17,6 +18,8 @@ def rmsnorm(x, w, eps):
     """x [..., N] bf16, w [N] bf16 -> bf16 tensor shaped like x."""
     shape = x.shape
     N = shape[-1]
+    if w.numel() != N:
+        raise ValueError(f"rmsnorm: w has {w.numel()} elements for rows of {N}")
     xs = as_kernel_input(x.reshape(-1, N), "x")
     w = as_kernel_input(w.reshape(N), "w")
     M = xs.shape[0]

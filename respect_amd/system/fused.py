@@ -88,6 +88,38 @@ def qk_norm_rope(q, k, wq, wk, eps, cos, sin):
     return qo, ko
 
 
+def rmsnorm_qk_norm_rope(x, w, eps, q, k, wq, wk, qk_eps, cos, sin):
+    """``rmsnorm(x, w, eps)`` and ``qk_norm_rope(q, k, wq, wk, qk_eps, cos, sin)`` in one
+    launch -> (y, q_out, k_out), bitwise the two calls' results.  x [..., N] with N % 8 == 0
+    and N <= 16384; the rest as qk_norm_rope.  No counterpart in the reference (two
+    launches there): for a caller with both inputs ready."""
+    N = x.shape[-1]
+    if w.numel() != N:
+        raise ValueError(f"rmsnorm_qk_norm_rope: w has {w.numel()} elements for rows of {N}")
+    xs = as_kernel_input(x.reshape(-1, N), "x")
+    w = as_kernel_input(w.reshape(N), "w")
+    T, HQ, D = q.shape
+    HK = k.shape[1]
+    q = as_kernel_input(q, "q")
+    k = as_kernel_input(k, "k")
+    wq = as_kernel_input(wq.contiguous(), "wq")
+    wk = as_kernel_input(wk.contiguous(), "wk")
+    cos = as_kernel_input(cos.reshape(T, D), "cos")
+    sin = as_kernel_input(sin.reshape(T, D), "sin")
+    if cos.stride(0) != sin.stride(0):
+        cos, sin = cos.contiguous(), sin.contiguous()
+    y = torch.empty((xs.shape[0], N), dtype=torch.bfloat16, device=x.device)
+    qo = torch.empty((T, HQ, D), dtype=torch.bfloat16, device=q.device)
+    ko = torch.empty((T, HK, D), dtype=torch.bfloat16, device=q.device)
+    rc = _lib.lib().rspx_rmsnorm_qk_norm_rope(
+        xs.data_ptr(), xs.stride(0), w.data_ptr(), y.data_ptr(), y.stride(0), xs.shape[0], N, float(eps),
+        q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1), wq.data_ptr(), wk.data_ptr(),
+        cos.data_ptr(), sin.data_ptr(), cos.stride(0), qo.data_ptr(), ko.data_ptr(), T, HQ, HK, D, float(qk_eps),
+        _lib.stream_ptr(x.device))
+    _lib.check("rspx_rmsnorm_qk_norm_rope", rc)
+    return y.reshape(x.shape), qo, ko
+
+
 def rope_tables(positions, head_dim: int = 128, theta: float = 1.0e6, device=None):
     """cos/sin rows [T, head_dim] (bf16) for integer positions, computed like HF's
     Qwen3VLTextRotaryEmbedding: fp32 inv_freq, fp32 angles, bf16 cos/sin."""

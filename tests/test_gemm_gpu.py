@@ -83,11 +83,72 @@ def test_linear_strided_and_errors():
     assert torch.equal(linear(big[:, 512:1536], wd), linear(xd, wd))
     # the chunk count depends on (N, K) only
     assert lib().rspx_linear_splits(4096, 4096) == lib().rspx_linear_splits(4096, 4096) > 0
-    with pytest.raises(RspxError):
-        linear(torch.zeros(4, 100, device="cuda", dtype=torch.bfloat16),
-               torch.zeros(16, 100, device="cuda", dtype=torch.bfloat16))
+    from respect_amd.kernels.gemm import tile_weight
+    with pytest.raises(RspxError):   # the tiled weight layout needs N % 16 == 0 and K % 32 == 0
+        tile_weight(torch.zeros(20, 100, device="cuda", dtype=torch.bfloat16))
     with pytest.raises(TypeError):
         linear(xd.float(), wd)
+
+
+@pytest.mark.parametrize("M,N,K", [(7, 1000, 1000), (1, 1000, 1000), (64, 1000, 4096), (5, 4096, 1000),
+                                   (3, 17, 33), (130, 250, 777), (2, 24, 4104), (70, 4100, 520)])
+def test_linear_any_shape(M, N, K):
+    """Shapes outside N % 16 == 0 and K % 256 == 0 (the reference's linear masks any M, N, K,
+    respect/kernels/gemm.py:19-27): the parity bar above in bf16, the accumulation bound in
+    fp32, rows bitwise independent of M, and the same bits from unaligned, strided operands
+    (two-byte loads) as from aligned ones."""
+    from respect_amd import _lib
+    from respect_amd.kernels.gemm import linear
+    print(f"[linear any] M={M} N={N} K={K}", flush=True)
+    L = _lib.lib()
+    assert L.rspx_linear_splits(N, K) == 1 and L.rspx_linear_workspace_bytes(M, N, K) == 0
+    x, w = _xw(M * 11 + N + K, M, N, K)
+    xd, wd = _dev(x), _dev(w)
+    out = linear(xd, wd)
+    o = out.float().cpu().numpy()
+    ex = G.linear_exact(x, w)
+    ref = bf16.round_bf16(ex.astype(np.float32))
+    bound = G.linear_error_bound(x, w)
+    allowed = bound + bf16.ulp(np.abs(ex) + bound)
+    print(f"  max ulp {bf16.ulp_diff(o, ref).max():.2f} equal {(o == ref).mean():.5f}", flush=True)
+    assert np.all(np.abs(o - ex) <= allowed)
+    assert (o == ref).mean() >= 0.99
+    f32 = linear(xd, wd, out_dtype=torch.float32)
+    assert np.all(np.abs(f32.cpu().numpy().astype(np.float64) - ex) <= bound + 1e-30)
+    # rows alone and in a longer call
+    for m in sorted({0, M // 2, M - 1}):
+        assert torch.equal(linear(xd[m:m + 1], wd), out[m:m + 1])
+    big = torch.cat([xd, xd.flip(0), xd[:1]])
+    assert torch.equal(linear(big, wd)[:M], out)
+    # operands one element past a 16-byte boundary, rows K + 3 apart, output rows N + 1 apart
+    s = _lib.stream_ptr(xd.device)
+    xb = torch.zeros(M, K + 3, device="cuda", dtype=torch.bfloat16)
+    wb = torch.zeros(N, K + 3, device="cuda", dtype=torch.bfloat16)
+    xb[:, 1:K + 1] = xd
+    wb[:, 1:K + 1] = wd
+    ob = torch.full((M, N + 1), float("nan"), device="cuda", dtype=torch.bfloat16)
+    _lib.check("rspx_linear", L.rspx_linear(xb.data_ptr() + 2, K + 3, wb.data_ptr() + 2, K + 3, ob.data_ptr(), N + 1,
+                                            M, N, K, 0, None, 0, s))
+    torch.cuda.synchronize()
+    assert torch.equal(ob[:, :N], out)
+    assert torch.isnan(ob[:, N].float()).all()     # nothing written past column N
+
+
+def test_linear_any_shape_errors():
+    from respect_amd import _lib
+    L = _lib.lib()
+    s = _lib.stream_ptr(torch.device("cuda"))
+    x = torch.zeros(4, 100, device="cuda", dtype=torch.bfloat16)
+    w = torch.zeros(24, 100, device="cuda", dtype=torch.bfloat16)
+    o = torch.zeros(4, 24, device="cuda", dtype=torch.bfloat16)
+    assert L.rspx_linear(x.data_ptr(), 100, w.data_ptr(), 100, o.data_ptr(), 24, 4, 24, 100, 0, None, 0, s) == 0
+    assert L.rspx_linear(x.data_ptr(), 99, w.data_ptr(), 100, o.data_ptr(), 24, 4, 24, 100, 0, None, 0, s) == -1
+    assert L.rspx_linear(x.data_ptr() + 1, 100, w.data_ptr(), 100, o.data_ptr(), 24, 4, 24, 100, 0, None, 0, s) == -4
+    assert L.rspx_linear(x.data_ptr(), _lib.RSPX_TILED, w.data_ptr(), 100, o.data_ptr(), 24, 4, 24, 100, 0, None, 0,
+                         s) == -2
+    # rspx_linear_silu and rspx_linear_partials keep the N % 16, K % 256 shapes
+    assert L.rspx_linear_partials(x.data_ptr(), 100, w.data_ptr(), 100, o.data_ptr(), 4, 24, 100, s) == -2
+    torch.cuda.synchronize()
 
 
 def test_partials_consumers_equal_linear_then_op():

@@ -32,12 +32,15 @@ def test_install_wraps_every_linear_and_norm_and_uninstall_restores():
     assert ALL_ATTENTION_FUNCTIONS["sdpa"] is dispatch.ORIG
 
 
-def test_install_refuses_unsupported_shapes():
+def test_install_refuses_unsupported_weights():
     from respect_amd.kernels import patch
-    m = tiny_model(hidden=192, ffn=512, heads=3, kv_heads=1)   # in_features 192: not a multiple of 256
+    m = tiny_model(hidden=192, ffn=512, heads=3, kv_heads=1)   # ragged shapes are built (any N, K)
+    m.model.layers[0].self_attn.q_proj.float()                  # an fp32 weight is not
+    before = {n: type(mod) for n, mod in m.named_modules()}
     with pytest.raises(ValueError, match="layers.0.self_attn.q_proj"):
         patch.install(m, 8)
     assert not patch.is_installed()
+    assert {n: type(mod) for n, mod in m.named_modules()} == before
 
 
 def test_dispatch_falls_back_without_prompt_length():

@@ -23,14 +23,18 @@ def _path(tree, i):
     return p[::-1]
 
 
-def test_trie_verification_equals_one_token_path_bitwise():
+@pytest.mark.parametrize("shape", [{}, dict(hidden=200, ffn=520, vocab=1000)],
+                         ids=["aligned", "ragged"])
+def test_trie_verification_equals_one_token_path_bitwise(shape):
+    """shape "ragged": hidden 200, FFN 520 and vocabulary 1000, so every linear layer and
+    RMSNorm runs the any-shape kernels."""
     from transformers.cache_utils import DynamicCache
     from respect_amd.candidates.trie import build_trie
     from respect_amd.decoding.hf_kv import FixedKVBuffer, compact
     from respect_amd.decoding.hf_verify import forward_tokens_hf, verify_trie_hf
     from respect_amd.kernels import dispatch, patch
 
-    m = tiny_model(device="cuda")
+    m = tiny_model(device="cuda", **shape)
     cfg_vocab = m.lm_head.weight.shape[0]
     g = torch.Generator().manual_seed(1)
     P, CAP, base = 40, 64, 3
