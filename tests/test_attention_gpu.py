@@ -391,15 +391,17 @@ def test_one_and_two_launches_equal(which):
 def test_one_and_two_pass_node_segments_equal(shape):
     """The same trie and committed slots in a node segment of 128 and 192 slots (two and
     three chunks of K and V resident), of 256 slots (the extra slots masked out; V resident,
-    scores from K fragments loaded into registers) and of 384 slots (streamed: a score pass,
-    then K and V gathered by rank) give the same bits, through one and two launches."""
+    scores from K fragments loaded into registers), of 384 slots (streamed: a score pass
+    whose scores stay in LDS, then V gathered by rank) and of 1024 / 512 slots (streamed past
+    the kept-score limit: the scores recomputed from K gathered by rank) give the same
+    bits, through one and two launches."""
     args = {"8b": (11, 32, 8, 128, 3072, 4, 24, 0, 16, 64), "d64": (7, 16, 2, 64, 3086, 3, 9, 0, 6, None)}[shape]
     kw = {"kv_scale": 128 ** -0.5} if shape == "8b" else {}
     base = 40 if shape == "8b" else 90
     short = gen.attn_case(*args, base=base, **kw)
     assert 64 < short.kn.shape[1] <= 128
     ref = _run(short, launches=2)
-    for step in (192, 256, 384):
+    for step in (192, 256, 384, 1024 if shape == "8b" else 512):
         long = gen.attn_case(*args, base=base, nn_step=step, **kw)
         assert long.kn.shape[1] == step and np.array_equal(long.msk[:, :short.kn.shape[1]], short.msk)
         for launches in (1, 2):
