@@ -11,7 +11,9 @@
 // On MI355X the packed gate/up [64, 2 x 12288] call takes 3.02 us at two
 // elements per thread, 3.09 at four and 3.42 at eight (rotating inputs beyond
 // the MALL): a launch this small is bound by memory latency, and more waves
-// in flight hide more of it.  g and u may be strided views (e.g. the two
+// in flight hide more of it.  Non-temporal stores (not kept in L2) shorten the
+// write-back at the kernel's end: 3.02 -> 2.80 us (non-temporal loads 2.86,
+// both 2.84).  g and u may be strided views (e.g. the two
 // halves of a packed [rows, 2F] gate/up).
 
 #include "common.h"
@@ -31,10 +33,11 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* g, int64_
   if constexpr (PAIR) {
     const uint32_t gw = *reinterpret_cast<const uint32_t*>(g + row * sg + c);
     const uint32_t uw = *reinterpret_cast<const uint32_t*>(u + row * su + c);
-    *reinterpret_cast<uint32_t*>(y + row * sy + c) =
-        pack_bf16x2(swiglu1(bf16_lo(gw), bf16_lo(uw)), swiglu1(bf16_hi(gw), bf16_hi(uw)));
+    __builtin_nontemporal_store(pack_bf16x2(swiglu1(bf16_lo(gw), bf16_lo(uw)), swiglu1(bf16_hi(gw), bf16_hi(uw))),
+                                reinterpret_cast<uint32_t*>(y + row * sy + c));
   } else {
-    y[row * sy + c] = f32_to_bf16_rne(swiglu1(bf16_to_f32(g[row * sg + c]), bf16_to_f32(u[row * su + c])));
+    __builtin_nontemporal_store(
+        f32_to_bf16_rne(swiglu1(bf16_to_f32(g[row * sg + c]), bf16_to_f32(u[row * su + c]))), y + row * sy + c);
   }
 }
 
