@@ -93,9 +93,9 @@ const char* rspx_version(void);
  *
  * workspace: device memory of at least rspx_trie_attn_workspace_bytes(...)
  * bytes, 16-byte aligned and zero-filled before its first use; every call
- * leaves its synchronisation words (the first 16 KiB, at the same place for
- * every shape) at zero again, so calls of any shapes may share one workspace
- * in turn.  It holds those words (per-row-block counters of the one-launch
+ * moves each per-row-block counter it uses (in the first 16 KiB, at the same
+ * place for every shape) by exactly 8, so they stay multiples of 8 between
+ * calls and calls of any shapes may share one workspace in turn.  It holds those words (per-row-block counters of the one-launch
  * path) and the per-group partial results.  A workspace must not be used by
  * two calls that can run at the same time.
  * NN <= 4096 (the node-slot limit of the reference dispatcher, NMAX).

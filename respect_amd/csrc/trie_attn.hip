@@ -1454,8 +1454,8 @@ __device__ __forceinline__ void nan_rows(const TrieAttnArgs& A, int g, int p0, i
 // (A.spin polls), and a workgroup whose wait gives up stores NaN in every
 // element of the rows it would merge -- the failure reaches the caller's
 // output without a host synchronisation -- and raises a flag the host can
-// read.  The last workgroup of a block to finish resets the block's counters
-// to zero, whether or not a wait gave up.
+// read.  Counters are never reset: every call moves each block's counter by
+// exactly kCountUnit, whether or not a wait gave up (see kCountUnit).
 //
 // The wait is bounded in time: kWaitMs milliseconds of the device's
 // constant-rate real-time counter (s_memrealtime, hipDeviceAttributeWallClockRate
@@ -1492,7 +1492,16 @@ static int wait_deadline_ticks() {
   }
   return ticks[dev];
 }
-constexpr int kSyncWords = 4096;   // timeout flag + [HK][NRB][2] counters
+constexpr int kSyncWords = 4096;   // timeout flag + [HK][NRB][2] counters (the second word of each pair unused)
+// Every one-launch call adds exactly kCountUnit to the counter of each row
+// block it computes: the block's NG workgroups add kCountUnit / NG each, the
+// first kCountUnit % NG of them one more (NG <= kGroupTarget = kCountUnit).
+// So between calls every counter is a multiple of kCountUnit, and a workgroup
+// of call k that reads its block's counter before adding its own share sees a
+// value in [kCountUnit k, kCountUnit (k + 1)): no call ever resets a counter,
+// and calls of any shapes may share the words in turn.
+constexpr uint32_t kCountUnit = kGroupTarget;
+static_assert((kCountUnit & (kCountUnit - 1)) == 0, "2^32 is a multiple of the unit: wrap-around keeps the invariant");
 
 // Rows [r0, rend) merged by workgroup (g, rb, q) of a fused launch: its share
 // of the row block, a multiple of 4 rows.
@@ -1507,15 +1516,17 @@ __device__ __forceinline__ void merge_share(const TrieAttnArgs& A, int rb, int q
 // After workgroup (g, rb, q) has counted its group partial of row block rb:
 // the node partials of its merge rows in batches of at most kNodeRows (the
 // first batch while the block's other workgroups finish, then the bounded
-// wait), the merge, and the block's counters back to zero once every
-// workgroup of the block is past its wait.  pre / pf: node_rows' first batch.
+// wait), then the merge.  pre / pf: node_rows' first batch.  old: what
+// count_partial's add returned (thread 0): the counter before this
+// workgroup's share, so the block is complete once the counter has moved
+// kCountUnit past the multiple of kCountUnit below it.
 template <int D, int kRT>
 __device__ __forceinline__ void block_tail(const TrieAttnArgs& A, char* lds, int g, int rb, int q,
-                                           const NodePre<D>& pre, bool pf) {
+                                           const NodePre<D>& pre, bool pf, int old) {
   using LY = NodeLds<D>;
   const int lane = __lane_id();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  int* cnt = A.sync + 1 + 2 * (g * A.NRB + rb);
+  const int* cnt = A.sync + 1 + 2 * (g * A.NRB + rb);
   int r0, rend;
   merge_share<kRT>(A, rb, q, r0, rend);
   const int rend0 = min(rend, r0 + kNodeRows);
@@ -1526,17 +1537,19 @@ __device__ __forceinline__ void block_tail(const TrieAttnArgs& A, char* lds, int
     if (w == 0) {
       // Bounded in time (A.deadline ticks of the constant-rate real-time
       // counter) and in polls (A.spin, lowered only by a test hook).
-      int v = 0;
+      const uint32_t base = (uint32_t)__builtin_amdgcn_readfirstlane(old) & ~(kCountUnit - 1);
+      uint32_t v = base;
       const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
       for (int it = 0; it < A.spin; ++it) {
-        v = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (v >= A.NG) break;
+        v = (uint32_t)__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (v - base >= kCountUnit) break;
         if (__builtin_amdgcn_s_memrealtime() - t0 > (uint64_t)A.deadline) break;
         __builtin_amdgcn_s_sleep(2);
       }
+      const bool short_ = v - base < kCountUnit;
       if (lane == 0) {
-        *gave_up = v < A.NG;
-        if (v < A.NG) __hip_atomic_store(A.sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *gave_up = short_;
+        if (short_) __hip_atomic_store(A.sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     }
@@ -1555,27 +1568,24 @@ __device__ __forceinline__ void block_tail(const TrieAttnArgs& A, char* lds, int
       else merge_rounds<D, true>(A, g, b0, be, npb, w);
     }
   }
-  // Counters back to zero once every workgroup of the block is past its wait.
-  lds_barrier();
-  if (threadIdx.x == 0) {
-    const int d = __hip_atomic_fetch_add(cnt + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (d == A.NG - 1) {
-      __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(cnt + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
   RSPX_MARK(15);
 }
 
 // The group partial is complete in memory (each wave waited for its own
-// stores): count it in the row block's counter.
-__device__ __forceinline__ void count_partial(const TrieAttnArgs& A, int g, int rb) {
+// stores): add workgroup q's share of kCountUnit to the row block's counter.
+// Returns, in thread 0, the counter before the add.
+__device__ __forceinline__ int count_partial(const TrieAttnArgs& A, int g, int rb, int q) {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
   lds_barrier();
   RSPX_MARK(11);
-  if (threadIdx.x == 0)
-    __hip_atomic_fetch_add(A.sync + 1 + 2 * (g * A.NRB + rb), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  int old = 0;
+  if (threadIdx.x == 0) {
+    const int share = (int)kCountUnit / A.NG + (q < (int)kCountUnit % A.NG ? 1 : 0);
+    old = __hip_atomic_fetch_add(A.sync + 1 + 2 * (g * A.NRB + rb), share, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return old;
 }
 
 template <int D, int kRT>
@@ -1602,8 +1612,8 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   prompt_block<D, kRT, true>(A, lds, g, rb, q, [&] {
     if (pf) node_prefetch<D>(A, g, r0, rend0, (lds_char*)lds, w, pre);
   });
-  count_partial(A, g, rb);
-  block_tail<D, kRT>(A, lds, g, rb, q, pre, pf);
+  const int old = count_partial(A, g, rb, q);
+  block_tail<D, kRT>(A, lds, g, rb, q, pre, pf, old);
 }
 
 // The same work as fused_kernel for grids twice as large as the device holds
@@ -1625,13 +1635,17 @@ __global__ __launch_bounds__(512) void fused2_kernel(TrieAttnArgs A) {
   const int rbw = rest % NRBW;
   const int q = rest / NRBW;
   const int nb = rbw + NRBW < A.NRB ? 2 : 1;
-  for (int b = 0; b < nb; ++b) {
-    const int rb = rbw + NRBW * b;
-    prompt_block<D, kRT, true>(A, lds, g, rb, q, [] {});
-    count_partial(A, g, rb);
+  int old[2] = {0, 0};
+  for (int b = 0; b < 2; ++b) {
+    if (b < nb) {
+      const int rb = rbw + NRBW * b;
+      prompt_block<D, kRT, true>(A, lds, g, rb, q, [] {});
+      old[b] = count_partial(A, g, rb, q);
+    }
   }
   NodePre<D> none;
-  for (int b = 0; b < nb; ++b) block_tail<D, kRT>(A, lds, g, rbw + NRBW * b, q, none, false);
+  for (int b = 0; b < 2; ++b)
+    if (b < nb) block_tail<D, kRT>(A, lds, g, rbw + NRBW * b, q, none, false, old[b]);
 }
 
 // ------------------------------------------------------------------ host side

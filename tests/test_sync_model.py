@@ -3,22 +3,26 @@
 fused2_kernel), run on the CPU under many random schedules.
 
 Each workgroup (g, rb, q) of a row block of NG workgroups:
-  1. stores its group partial, then counts it: cnt[rb] += 1;
-  2. polls cnt[rb] until it reaches NG or a deadline passes (then it "gives
-     up": its rows become NaN and the status word is set);
-  3. merges, reading the NG partials of its block;
-  4. adds 1 to done[rb]; the workgroup that brings done[rb] to NG resets
-     cnt[rb] and done[rb] to zero.
-fused2_kernel runs steps 1 for both of its row blocks before any step 2.
+  1. stores its group partial, then adds its share to the block's counter --
+     kCountUnit / NG, plus one for the first kCountUnit % NG workgroups, so a
+     call moves every counter it uses by exactly kCountUnit -- keeping the
+     value before its add (`old`);
+  2. polls the counter until it is kCountUnit past base = old rounded down
+     to a multiple of kCountUnit, or a deadline passes (then it "gives up":
+     its rows become NaN and the status word is set);
+  3. merges, reading the NG partials of its block.
+Counters are never reset.  fused2_kernel runs step 1 for both of its row
+blocks before any step 2.
 
 The scheduler holds at most `slots` workgroups resident (dispatch in
 workgroup order, a slot freed when a workgroup ends) and interleaves the
-resident ones at random.  Checked in every schedule:
+resident ones at random.  Calls run one after another, with different NG and
+row-block counts sharing the counters.  Checked in every schedule:
   - safety: a workgroup that merges without giving up saw all NG partials of
     its block complete (no merge reads a partial before its count);
-  - no counter is reset while a workgroup of its block can still read it;
-  - the counters are zero when the grid ends (the next call starts clean),
-    whether or not a wait gave up;
+  - every counter a call uses moves by exactly kCountUnit, whether or not a
+    wait gave up, so the next call (of any shape) starts from multiples of
+    kCountUnit;
   - liveness: with the whole grid resident no wait gives up; with fewer slots
     than workgroups the deadline ends every wait, so the grid still drains.
 """
@@ -26,11 +30,19 @@ import random
 
 import pytest
 
+UNIT = 8   # kCountUnit = kGroupTarget
 
-def run(NRB, NG, slots, two=False, deadline=200, seed=0):
+
+def share(q, NG):
+    return UNIT // NG + (1 if q < UNIT % NG else 0)
+
+
+def run(cnt, NRB, NG, slots, two=False, deadline=200, seed=0):
+    """One call on the shared counters `cnt` (one per row block)."""
+    assert 1 <= NG <= UNIT
     rng = random.Random(seed)
-    cnt = [0] * NRB
-    done = [0] * NRB
+    start = list(cnt)
+    assert all(c % UNIT == 0 for c in start)
     stored = [set() for _ in range(NRB)]
     NRBW = (NRB + 1) // 2
     wgs = []
@@ -41,30 +53,27 @@ def run(NRB, NG, slots, two=False, deadline=200, seed=0):
     events = {"gave_up": 0, "merged": 0}
 
     def program(wg):
+        olds = []
         for rb in wg["blocks"]:                      # prompt groups, then counts
             yield
             stored[rb].add(wg["q"])                  # partial complete (vmcnt 0, barrier)
-            cnt[rb] += 1                             # count_partial
-        for rb in wg["blocks"]:                      # block_tail
-            polls, v = 0, 0
+            olds.append(cnt[rb])                     # count_partial: fetch-add, old value
+            cnt[rb] += share(wg["q"], NG)
+        for rb, old in zip(wg["blocks"], olds):      # block_tail
+            base = old - old % UNIT
+            polls = 0
             while True:
                 v = cnt[rb]
-                if v >= NG or polls >= deadline:
+                if v - base >= UNIT or polls >= deadline:
                     break
                 polls += 1
                 yield
-            if v >= NG:
+            if v - base >= UNIT:
                 assert len(stored[rb]) == NG         # every partial of the block is complete
                 events["merged"] += 1
             else:
                 events["gave_up"] += 1
             yield
-            assert cnt[rb] >= v                      # no reset while this workgroup reads
-            done[rb] += 1
-            if done[rb] == NG:
-                cnt[rb] = 0
-                done[rb] = 0
-                stored[rb].clear()
 
     pending = list(wgs)
     resident = []
@@ -76,44 +85,76 @@ def run(NRB, NG, slots, two=False, deadline=200, seed=0):
             next(resident[p])
         except StopIteration:
             resident.pop(p)
-    assert cnt == [0] * NRB and done == [0] * NRB
+    assert [c - s for c, s in zip(cnt, start)] == [UNIT] * NRB
     return events
 
 
-@pytest.mark.parametrize("NRB,NG,two", [(1, 32, False), (2, 16, False), (4, 8, False), (4, 8, True),
-                                        (3, 8, True)])
+def n_wgs(NRB, NG, two):
+    return NG * (((NRB + 1) // 2) if two else NRB)
+
+
+@pytest.mark.parametrize("NRB,NG,two", [(1, 8, False), (2, 8, False), (4, 8, False), (4, 8, True), (3, 6, True),
+                                        (4, 3, False), (2, 5, False), (1, 1, False), (2, 7, True)])
 def test_resident_grid_never_gives_up(NRB, NG, two):
-    """8B-shape grids (256 workgroups = 8 kv heads x 32; one kv head modelled) all resident."""
-    n = NG * (((NRB + 1) // 2) if two else NRB)
-    for seed in range(40):
-        ev = run(NRB, NG, slots=n, two=two, seed=seed)
+    """Grids of every NG (the 8B shape: 4 row blocks x 8 groups per kv head) all resident."""
+    for seed in range(30):
+        cnt = [0] * NRB
+        for call in range(3):
+            ev = run(cnt, NRB, NG, slots=n_wgs(NRB, NG, two), two=two, seed=seed * 7 + call)
+            assert ev["gave_up"] == 0 and ev["merged"] == NRB * NG
+
+
+def test_calls_of_different_shapes_share_the_counters():
+    """A sequence of calls with different NG, row-block counts and one or two blocks per
+    workgroup on one set of counters (a shared workspace): every call merges cleanly."""
+    rng = random.Random(5)
+    cnt = [0] * 8
+    for call in range(60):
+        NRB = rng.randint(1, 8)
+        NG = rng.randint(1, UNIT)
+        two = rng.random() < 0.3
+        sub = cnt[:NRB]
+        ev = run(sub, NRB, NG, slots=n_wgs(NRB, NG, two), two=two, seed=call)
+        cnt[:NRB] = sub
         assert ev["gave_up"] == 0 and ev["merged"] == NRB * NG
+    assert all(c % UNIT == 0 for c in cnt)
 
 
-@pytest.mark.parametrize("NRB,NG,two", [(2, 16, False), (4, 8, True)])
+@pytest.mark.parametrize("NRB,NG,two", [(2, 8, False), (4, 8, True), (3, 5, False)])
 def test_partial_residency_drains_by_the_deadline(NRB, NG, two):
     """Fewer slots than workgroups (another process holding CUs): waits give up at the
-    deadline, every workgroup still ends, and the counters are zero afterwards."""
-    n = NG * (((NRB + 1) // 2) if two else NRB)
+    deadline, every workgroup still ends, each counter still moves by exactly one unit,
+    and the next call, fully resident, merges cleanly."""
     gave = 0
-    for seed in range(40):
-        ev = run(NRB, NG, slots=n // 2, two=two, seed=seed)
+    for seed in range(30):
+        cnt = [0] * NRB
+        ev = run(cnt, NRB, NG, slots=max(1, n_wgs(NRB, NG, two) // 2), two=two, seed=seed)
         assert ev["gave_up"] + ev["merged"] == NRB * NG
         gave += ev["gave_up"]
+        ev = run(cnt, NRB, NG, slots=n_wgs(NRB, NG, two), two=two, seed=seed + 100)
+        assert ev["gave_up"] == 0
     assert gave > 0
 
 
-def test_model_catches_a_count_before_the_store():
-    """A planted mistake in the model (counting before the partial is complete) is caught."""
-    def bad_run():
+def test_model_catches_planted_mistakes():
+    """Planted mistakes in the model fail it: a count before the store, and shares that
+    do not add up to the unit (the next call's base would be off)."""
+    def count_before_store():
         cnt, stored = [0], set()
-        order = [("count", 0), ("count", 1), ("merge", 0), ("store", 0), ("store", 1)]
-        for op, q in order:
+        for op, q in [("count", 0), ("count", 1), ("merge", 0), ("store", 0), ("store", 1)]:
             if op == "count":
-                cnt[0] += 1
+                cnt[0] += UNIT // 2
             elif op == "store":
                 stored.add(q)
-            elif cnt[0] >= 2:
+            elif cnt[0] >= UNIT:
                 assert len(stored) == 2
     with pytest.raises(AssertionError):
-        bad_run()
+        count_before_store()
+    global share
+    good = share
+    try:
+        share = lambda q, NG: UNIT // NG      # drops the remainder: NG = 3 adds 6, not 8
+        with pytest.raises(AssertionError):
+            run([0], 1, 3, slots=3)
+    finally:
+        share = good
