@@ -108,7 +108,7 @@ static_assert(sizeof(TrieAttnArgs) == 184, "kernel argument struct stays at 184 
 // r (r < 3) landed / computed; 7 quarter (m, l) exchanged; 8 scaled quarters
 // written; 9 quarter sums and (m, l) stores done; 10 node data issued; 11
 // group partial stored and counted; 12 node partials done; 13 wait over; 14
-// merged; 15 counters released.
+// merged; 15 end.
 constexpr int kPhaseMarks = 16;
 constexpr int kPhaseWgs = 1024;
 #ifdef RSPX_PHASE_TRACE
@@ -755,12 +755,25 @@ constexpr int kNodeRounds = kNodeRows / kWavesA;  // rows per wave in one node_r
 // wave's first task and the mask bytes of the wave's rows.
 template <int D> struct NodePre {
   bf16x8 qf[D / 32];
-  // Mask words of chunks 0, 1, 2 (byte i: the mask byte of round i), named
-  // scalars read with constant indices only: a run-time choice between them
-  // can fold into one indexed load, which puts the whole struct in scratch.
-  uint32_t mb0 = 0, mb1 = 0, mb2 = 0;
+  // Raw mask bytes of chunk c and round i (m<c><i>), loaded without branches
+  // from clamped addresses; node_rows zeroes the ones out of range and packs
+  // them.  Nothing here is combined at issue time, so issuing them makes no
+  // wave wait for its loads (a use right after the loads would wait for every
+  // load in flight, the node K/V included, before the group partial is
+  // stored).  Named scalars read with constant indices only: a run-time choice
+  // between them can fold into one indexed load, which puts the whole struct
+  // in scratch.
+  uint32_t m00 = 0, m01 = 0, m10 = 0, m11 = 0, m20 = 0, m21 = 0;
 };
-static_assert(kNodeRounds <= 4, "mask bytes of every round in one 32-bit word");
+static_assert(kNodeRounds == 2, "NodePre holds the mask bytes of two rounds");
+// node_masks of chunk c from node_prefetch's raw bytes (r0: round 0, r1: round 1).
+// The empty asm pins the packing here: hoisted up to the loads, it made the
+// wave wait for them before the group partial's stores.
+__device__ __forceinline__ uint32_t pre_masks(const TrieAttnArgs& A, int nrd, int c, uint32_t r0, uint32_t r1) {
+  asm volatile("" : "+v"(r0), "+v"(r1));
+  const bool in = c * kChunk + __lane_id() < A.NN;
+  return (in && nrd > 0 ? r0 : 0u) | ((in && nrd > 1 ? r1 : 0u) << 8);
+}
 
 // Chunk c0 of kv head g's node K (score fragments) and, if `withv`, V rows
 // (16-byte units swizzled by row) into LDS buffer b: 1 KB pieces x = w, w + nw,
@@ -1149,9 +1162,9 @@ __device__ __forceinline__ const lds_float* node_rows(const TrieAttnArgs& A, int
     uint32_t mb[LY::RES];
     if (have_pre) {
       static_assert(LY::RES <= 3, "NodePre holds the mask bytes of three chunks");
-      mb[0] = pre.mb0;
-      if constexpr (LY::RES > 1) mb[1] = pre.mb1;
-      if constexpr (LY::RES > 2) mb[2] = pre.mb2;
+      mb[0] = pre_masks(A, nrd, 0, pre.m00, pre.m01);
+      if constexpr (LY::RES > 1) mb[1] = pre_masks(A, nrd, 1, pre.m10, pre.m11);
+      if constexpr (LY::RES > 2) mb[2] = pre_masks(A, nrd, 2, pre.m20, pre.m21);
     } else {
 #pragma unroll
       for (int c = 0; c < LY::RES; ++c) {
@@ -1298,18 +1311,27 @@ __device__ __forceinline__ void node_prefetch(const TrieAttnArgs& A, int g, int 
                                               NodePre<D>& pre) {
   constexpr int nw = kWavesA;
   const int nrd = (rend - p0 - w + nw - 1) / nw;
-  // One call per chunk with a constant index into pre.mb (a rolled loop
-  // would index it at run time and put `pre` in scratch memory).
-  auto chunk = [&](int b) -> uint32_t {
-    if (b >= NodeLds<D>::RES || b * kChunk >= A.NN) return 0;
-    node_issue<D>(A, g, b * kChunk, kv, b, w, nw, true);
-    return node_masks(A, p0, nrd, w, b * kChunk);
+  for (int b = 0; b < NodeLds<D>::RES && b * kChunk < A.NN; ++b) node_issue<D>(A, g, b * kChunk, kv, b, w, nw, true);
+  // Mask byte of round i, chunk c: row p0 + w + 8 i (p0 past the wave's rows),
+  // slot c kChunk + lane clamped into [0, NN); node_rows zeroes what is out of range.
+  auto raw = [&](int c, int i) -> uint32_t {
+    const int t = min(c * kChunk + __lane_id(), A.NN - 1);
+    const int r = i < nrd ? p0 + w + kWavesA * i : p0;
+    return A.msk[(r >> A.GQS) * A.smm + t * A.smn];
   };
-  pre.mb0 = chunk(0);
-  pre.mb1 = chunk(1);
-  pre.mb2 = chunk(2);
+  pre.m00 = raw(0, 0);
+  pre.m01 = raw(0, 1);
+  if constexpr (NodeLds<D>::RES > 1) {
+    pre.m10 = raw(1, 0);
+    pre.m11 = raw(1, 1);
+  }
+  if constexpr (NodeLds<D>::RES > 2) {
+    pre.m20 = raw(2, 0);
+    pre.m21 = raw(2, 1);
+  }
   node_q<D>(A, g, p0, rend, pre.qf);
 }
+
 
 // Columns per lane when one wave merges one row (D = 32: half the wave).
 template <int D> constexpr int merge_cols() { return D >= 64 ? D / 64 : 1; }
@@ -1516,10 +1538,10 @@ __device__ __forceinline__ void merge_share(const TrieAttnArgs& A, int rb, int q
 // After workgroup (g, rb, q) has counted its group partial of row block rb:
 // the node partials of its merge rows in batches of at most kNodeRows (the
 // first batch while the block's other workgroups finish, then the bounded
-// wait), then the merge.  pre / pf: node_rows' first batch.  old: what
-// count_partial's add returned (thread 0): the counter before this
-// workgroup's share, so the block is complete once the counter has moved
-// kCountUnit past the multiple of kCountUnit below it.
+// wait), then the merge.  pre / pf: node_rows' first batch.  old: the
+// counter before this workgroup's share (counter_before), so the block is
+// complete once the counter has moved kCountUnit past the multiple of
+// kCountUnit below it.
 template <int D, int kRT>
 __device__ __forceinline__ void block_tail(const TrieAttnArgs& A, char* lds, int g, int rb, int q,
                                            const NodePre<D>& pre, bool pf, int old) {
@@ -1573,19 +1595,24 @@ __device__ __forceinline__ void block_tail(const TrieAttnArgs& A, char* lds, int
 
 // The group partial is complete in memory (each wave waited for its own
 // stores): add workgroup q's share of kCountUnit to the row block's counter.
-// Returns, in thread 0, the counter before the add.
-__device__ __forceinline__ int count_partial(const TrieAttnArgs& A, int g, int rb, int q) {
+__device__ __forceinline__ void count_partial(const TrieAttnArgs& A, int g, int rb, int q) {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
   lds_barrier();
   RSPX_MARK(11);
-  int old = 0;
   if (threadIdx.x == 0) {
     const int share = (int)kCountUnit / A.NG + (q < (int)kCountUnit % A.NG ? 1 : 0);
-    old = __hip_atomic_fetch_add(A.sync + 1 + 2 * (g * A.NRB + rb), share, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(A.sync + 1 + 2 * (g * A.NRB + rb), share, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  return old;
+}
+
+// The row block's counter as this workgroup finds it before adding its own
+// share (read at the kernel's start): in [kCountUnit k, kCountUnit (k + 1))
+// during call k.  Every lane loads it, with no branch around the load, so the
+// value is waited for only where block_tail uses it (a value merged from a
+// branch is copied, and the copy waits for the load).
+__device__ __forceinline__ int counter_before(const TrieAttnArgs& A, int g, int rb) {
+  return __hip_atomic_load(A.sync + 1 + 2 * (g * A.NRB + rb), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int D, int kRT>
@@ -1604,6 +1631,7 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   int r0, rend;
   merge_share<kRT>(A, rb, q, r0, rend);
   const int rend0 = min(rend, r0 + kNodeRows);               // the first batch of node rows
+  const int old = counter_before(A, g, rb);
 
   // A resident node segment (K/V, score fragment, mask bytes of the first
   // batch) is loaded while the group partial is being stored.
@@ -1612,7 +1640,7 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   prompt_block<D, kRT, true>(A, lds, g, rb, q, [&] {
     if (pf) node_prefetch<D>(A, g, r0, rend0, (lds_char*)lds, w, pre);
   });
-  const int old = count_partial(A, g, rb, q);
+  count_partial(A, g, rb, q);
   block_tail<D, kRT>(A, lds, g, rb, q, pre, pf, old);
 }
 
@@ -1635,12 +1663,12 @@ __global__ __launch_bounds__(512) void fused2_kernel(TrieAttnArgs A) {
   const int rbw = rest % NRBW;
   const int q = rest / NRBW;
   const int nb = rbw + NRBW < A.NRB ? 2 : 1;
-  int old[2] = {0, 0};
+  const int old[2] = {counter_before(A, g, rbw), counter_before(A, g, nb > 1 ? rbw + NRBW : rbw)};
   for (int b = 0; b < 2; ++b) {
     if (b < nb) {
       const int rb = rbw + NRBW * b;
       prompt_block<D, kRT, true>(A, lds, g, rb, q, [] {});
-      old[b] = count_partial(A, g, rb, q);
+      count_partial(A, g, rb, q);
     }
   }
   NodePre<D> none;

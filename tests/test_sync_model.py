@@ -3,10 +3,10 @@
 fused2_kernel), run on the CPU under many random schedules.
 
 Each workgroup (g, rb, q) of a row block of NG workgroups:
+  0. reads the block's counter at its start (`old`, before its own add);
   1. stores its group partial, then adds its share to the block's counter --
      kCountUnit / NG, plus one for the first kCountUnit % NG workgroups, so a
-     call moves every counter it uses by exactly kCountUnit -- keeping the
-     value before its add (`old`);
+     call moves every counter it uses by exactly kCountUnit;
   2. polls the counter until it is kCountUnit past base = old rounded down
      to a multiple of kCountUnit, or a deadline passes (then it "gives up":
      its rows become NaN and the status word is set);
@@ -53,12 +53,11 @@ def run(cnt, NRB, NG, slots, two=False, deadline=200, seed=0):
     events = {"gave_up": 0, "merged": 0}
 
     def program(wg):
-        olds = []
+        olds = [cnt[rb] for rb in wg["blocks"]]      # counter_before, at the kernel's start
         for rb in wg["blocks"]:                      # prompt groups, then counts
             yield
             stored[rb].add(wg["q"])                  # partial complete (vmcnt 0, barrier)
-            olds.append(cnt[rb])                     # count_partial: fetch-add, old value
-            cnt[rb] += share(wg["q"], NG)
+            cnt[rb] += share(wg["q"], NG)            # count_partial
         for rb, old in zip(wg["blocks"], olds):      # block_tail
             base = old - old % UNIT
             polls = 0
