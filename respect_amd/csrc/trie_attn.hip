@@ -132,17 +132,20 @@ typedef __attribute__((address_space(3))) char lds_char;
 // state (m, l, acc) <- state (+) incoming.  An incoming partial with m = -inf
 // is empty and left out (it would be an exact no-op).  From the empty state
 // (-inf, 0, 0) the first combine reproduces the incoming partial exactly.
+// Selects instead of a branch: the values are the same, and a branch here
+// let the compiler sink the incoming partial's loads into it, after the
+// other loads' wait.
 template <int N>
 __device__ __forceinline__ void combine(float& m, float& l, float* acc, float m2, float l2,
                                         const float* acc2) {
-  if (m2 == kNegInf) return;
+  const bool skip = m2 == kNegInf;
   const float mn = fmaxf(m, m2);
   const float a = fexp2(m - mn);
   const float b = fexp2(m2 - mn);
-  l = __builtin_fmaf(l2, b, l * a);
+  l = skip ? l : __builtin_fmaf(l2, b, l * a);
 #pragma unroll
-  for (int i = 0; i < N; ++i) acc[i] = __builtin_fmaf(acc2[i], b, acc[i] * a);
-  m = mn;
+  for (int i = 0; i < N; ++i) acc[i] = skip ? acc[i] : __builtin_fmaf(acc2[i], b, acc[i] * a);
+  m = skip ? m : mn;
 }
 
 // Sum / max over the four 16-lane rows of a wave, the same operand order in
@@ -1353,13 +1356,18 @@ __device__ __forceinline__ void merge_row(const TrieAttnArgs& A, int g, int r, f
   // Byte offsets of the partials fit 31 bits (checked by the host for COH).
   const __amdgpu_buffer_rsrc_t rml = buffer_rsrc(A.gp_ml, 0x7fffffff);
   const __amdgpu_buffer_rsrc_t racc = buffer_rsrc(A.gp_acc, 0x7fffffff);
+  // Every group slot loads, with no branch around a load (groups past NG
+  // re-read group NG - 1 and are not combined): a load under a branch makes
+  // the compiler wait for the loads before it at the branch's join, which
+  // split these loads into several memory round trips.
 #pragma unroll
   for (int qq = 0; qq < kGroupTarget; ++qq) {
-    if (qq < NG) {
-      const size_t ao = (gbase + qq) * D + DL * ln;
+    {
+      const int qc = qq < NG ? qq : NG - 1;
+      const size_t ao = (gbase + qc) * D + DL * ln;
       if constexpr (COH) {
         // sc1 (cache policy 16): the coherence of an agent-scope atomic load.
-        const f32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(rml, (int)((gbase + qq) * 8), 0, 16);
+        const f32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(rml, (int)((gbase + qc) * 8), 0, 16);
         gm[qq] = ml.x;
         gl[qq] = ml.y;
         if constexpr (DL == 4) {
@@ -1374,7 +1382,7 @@ __device__ __forceinline__ void merge_row(const TrieAttnArgs& A, int g, int r, f
           ga[qq][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(racc, (int)(ao * 4), 0, 16));
         }
       } else {
-        const float2 ml = *reinterpret_cast<const float2*>(A.gp_ml + (gbase + qq) * 2);
+        const float2 ml = *reinterpret_cast<const float2*>(A.gp_ml + (gbase + qc) * 2);
         gm[qq] = ml.x;
         gl[qq] = ml.y;
 #pragma unroll
@@ -1387,7 +1395,7 @@ __device__ __forceinline__ void merge_row(const TrieAttnArgs& A, int g, int r, f
   for (int k = 0; k < DL; ++k) facc[k] = 0.f;
 #pragma unroll
   for (int qq = 0; qq < kGroupTarget; ++qq)
-    if (qq < NG) combine<DL>(fm, fl, facc, gm[qq], gl[qq], ga[qq]);
+    combine<DL>(fm, fl, facc, qq < NG ? gm[qq] : kNegInf, gl[qq], ga[qq]);   // past NG: left out
   combine<DL>(fm, fl, facc, m, l, acc);
   if (!on) return;
   uint16_t* o = A.out + out_offset<D>(A.soh, A.som, A.HK << A.GQS, R.hd, R.mq, DL * lane);
