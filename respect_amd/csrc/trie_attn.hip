@@ -268,6 +268,19 @@ __device__ __forceinline__ s16x4 lds_read_tr(const lds_char* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
 }
 
+// lds_read_tr pair without the compiler's fence: the intrinsic's memory
+// operand carries no alias information, so the compiler puts s_waitcnt
+// vmcnt(0) in front of it -- a wait for every vector-memory operation in
+// flight, the group partial's counter add included.  For LDS data that is
+// known to be in place (its loads waited for), read the two halves in asm and
+// wait for them (lgkmcnt) inside the asm that hands them out.
+__device__ __forceinline__ void lds_read_tr2_nofence(const lds_char* p0, const lds_char* p1, s16x4& lo, s16x4& hi) {
+  asm volatile("ds_read_b64_tr_b16 %0, %2\n\tds_read_b64_tr_b16 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+               : "=&v"(lo), "=&v"(hi)
+               : "v"(p0), "v"(p1)
+               : "memory");
+}
+
 __device__ __forceinline__ void lds_barrier() {
   // Every wave's LDS reads issued so far are complete, then a raw s_barrier:
   // __syncthreads() would also wait for every direct-to-LDS load in flight.
@@ -1016,8 +1029,14 @@ __device__ __forceinline__ void node_task(const TrieAttnArgs& A, int g, int p0, 
 #pragma unroll
     for (int jj = 0; jj < NJ; ++jj) {
       const int b = 2 * (NJ * sl + jj) + (c4 >> 1);
-      const s16x4 lo = lds_read_tr(vrow0 + 16 * (b ^ vsw0) + 8 * (c4 & 1));
-      const s16x4 hi = lds_read_tr(vrow1 + 16 * (b ^ vsw1) + 8 * (c4 & 1));
+      s16x4 lo, hi;
+      if constexpr (RES) {
+        // V rows resident since before the caller's wait: no fence needed.
+        lds_read_tr2_nofence(vrow0 + 16 * (b ^ vsw0) + 8 * (c4 & 1), vrow1 + 16 * (b ^ vsw1) + 8 * (c4 & 1), lo, hi);
+      } else {
+        lo = lds_read_tr(vrow0 + 16 * (b ^ vsw0) + 8 * (c4 & 1));
+        hi = lds_read_tr(vrow1 + 16 * (b ^ vsw1) + 8 * (c4 & 1));
+      }
       const bf16x8 vop = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, hop, acc[jj], 0, 0, 0);
       acc[jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, lop, acc[jj], 0, 0, 0);
@@ -1608,7 +1627,9 @@ __device__ __forceinline__ void count_partial(const TrieAttnArgs& A, int g, int 
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
   lds_barrier();
   RSPX_MARK(11);
-  if (threadIdx.x == 0) {
+  // The add from the last wave: waves 0-3 score the node slots next, and a
+  // wave with the add in flight would wait for it at its first vmcnt wait.
+  if (threadIdx.x == 64 * (kWavesA - 1)) {
     const int share = (int)kCountUnit / A.NG + (q < (int)kCountUnit % A.NG ? 1 : 0);
     __hip_atomic_fetch_add(A.sync + 1 + 2 * (g * A.NRB + rb), share, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
