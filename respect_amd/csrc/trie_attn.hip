@@ -424,15 +424,19 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
   const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kpg + ks0 * A.skpn, 2 * ((P - ks0 - 1) * A.skpn + D));
   const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(vpg + ks0 * A.svpn, 2 * ((P - ks0 - 1) * A.svpn + D));
   const int kstep = 2 * kStep * A.skpn, vstep = 2 * kStep * A.svpn;
-  const int pro = min(nr, G::RING);
-  for (int rr = 0; rr < pro; ++rr)
-    issue_round<D>(rk, rv, kstep, vstep, kQuarters * rr, voff, ring + (rr % G::RING) * G::ROUND, w);
+  // Round 0 alone first: requested together with the next rounds, it shared
+  // the memory path with them and landed later; rounds 1 .. RING - 1 are
+  // requested once round 0 is in, and land while it is computed.
+  issue_round<D>(rk, rv, kstep, vstep, 0, voff, ring, w);
 
   bf16x8 qop[kRT][DQ];
   for (int r = 0; r < nr; ++r) {
     // Own chunks of round r (and the Q chunks, issued first) have landed.
-    wait_rounds<G::OWN, G::RING>(min(nr - 1 - r, G::RING - 1));
+    wait_rounds<G::OWN, G::RING>(r == 0 ? 0 : min(nr - 1 - r, G::RING - 1));
     lds_barrier();   // every wave's chunks of round r are in LDS
+    if (r == 0)
+      for (int rr = 1; rr < min(nr, G::RING); ++rr)
+        issue_round<D>(rk, rv, kstep, vstep, kQuarters * rr, voff, ring + rr * G::ROUND, w);
     if (r < 3) RSPX_MARK(1 + 2 * r);
     if (r == 0 && has_rows) {
 #pragma unroll
