@@ -795,31 +795,44 @@ __device__ __forceinline__ uint32_t pre_masks(const TrieAttnArgs& A, int nrd, in
   return (in && nrd > 0 ? r0 : 0u) | ((in && nrd > 1 ? r1 : 0u) << 8);
 }
 
-// Chunk c0 of kv head g's node K (score fragments) and, if `withv`, V rows
-// (16-byte units swizzled by row) into LDS buffer b: 1 KB pieces x = w, w + nw,
-// ...  Slots past NN read zeros.
+// Chunk c0 of kv head g's node K (score fragments) and V rows (16-byte units
+// swizzled by row) into LDS buffer b: 1 KB pieces x = w + 8 j of the chunk's
+// D / 8 K pieces, then its D / 8 V pieces.  Slots past NN read zeros.  Piece
+// x + 8 lies a fixed distance further on than piece x, in memory and in LDS
+// (8 is a multiple of the D / 32 K pieces per 16 slots, and V rows move by a
+// multiple of the swizzle's 8-row period), so each wave computes its first K
+// and V offsets once and steps them: straight-line issue, no per-piece
+// divisions.
 template <int D>
-__device__ __forceinline__ void node_issue(const TrieAttnArgs& A, int g, int c0, lds_char* kv, int b, int w,
-                                           int nw, bool withv) {
+__device__ __forceinline__ void node_issue(const TrieAttnArgs& A, int g, int c0, lds_char* kv, int b, int w) {
   using LY = NodeLds<D>;
   constexpr int DQ = D / 32, RB = 2 * D;
-  constexpr int KX = LY::CB / 1024;
+  constexpr int KX = LY::CB / 1024;        // K pieces (and V pieces) of a chunk
+  constexpr int NJ = 2 * KX / kWavesA;     // pieces per wave
+  static_assert(8 % DQ == 0 && 1024 % RB == 0 && (KX % kWavesA == 0 || 2 * KX == kWavesA), "piece stepping");
   const int lane = __lane_id();
   const int left = A.NN - c0 - 1;
   const __amdgpu_buffer_rsrc_t rk =
       buffer_rsrc(A.kn + (g * A.sknh + c0 * A.sknn), 2 * (left * A.sknn + D));
   const __amdgpu_buffer_rsrc_t rv =
       buffer_rsrc(A.vn + (g * A.svnh + c0 * A.svnn), 2 * (left * A.svnn + D));
-  const int nx = withv ? 2 * KX : KX;
-  for (int x = w; x < nx; x += nw) {
-    if (x < KX) {
-      const int slot = 16 * (x / DQ) + (lane & 15);
-      bdma16(rk, 2 * (slot * A.sknn + 32 * (x % DQ) + 8 * (lane >> 4)), LY::kbuf(kv, b) + x * 1024);
-    } else {
-      const int byte = (x - KX) * 1024 + 16 * lane;
-      const int row = byte / RB, u = (byte % RB) / 16;
-      bdma16(rv, 2 * row * A.svnn + 16 * (u ^ vswz<D>(row)), LY::vbuf(kv, b) + (x - KX) * 1024);
+  // First K piece of the wave: w (at D = 32, one piece per wave: K for w < 4).
+  const int koff = 2 * ((16 * (w / DQ) + (lane & 15)) * A.sknn + 32 * (w % DQ) + 8 * (lane >> 4));
+  const int kstep = 2 * 16 * (8 / DQ) * A.sknn;
+  // First V piece: w, or w - KX at D = 32.
+  const int y0 = KX % kWavesA == 0 ? w : w - KX;
+  const int row = y0 * (1024 / RB) + 16 * lane / RB;
+  const int voff = 2 * row * A.svnn + 16 * (((16 * lane) % RB) / 16 ^ vswz<D>(row));
+  const int vstep = 2 * kWavesA * (1024 / RB) * A.svnn;
+  if constexpr (KX % kWavesA == 0) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      if (j < KX / kWavesA) bdma16(rk, koff + j * kstep, LY::kbuf(kv, b) + (w + kWavesA * j) * 1024);
+      else bdma16(rv, voff + (j - KX / kWavesA) * vstep, LY::vbuf(kv, b) + (w + kWavesA * (j - KX / kWavesA)) * 1024);
     }
+  } else {
+    const bool isk = w < KX;
+    bdma16(isk ? rk : rv, isk ? koff : voff, isk ? LY::kbuf(kv, b) + w * 1024 : LY::vbuf(kv, b) + y0 * 1024);
   }
 }
 
@@ -1196,7 +1209,7 @@ __device__ __forceinline__ const lds_float* node_rows(const TrieAttnArgs& A, int
       for (int c = 0; c < LY::RES; ++c) {
         mb[c] = 0;
         if (c < nch) {
-          node_issue<D>(A, g, kChunk * c, kv, c, w, nw, true);
+          node_issue<D>(A, g, kChunk * c, kv, c, w);
           mb[c] = node_masks(A, p0, nrd, w, kChunk * c);
         }
       }
@@ -1337,11 +1350,11 @@ __device__ __forceinline__ void node_prefetch(const TrieAttnArgs& A, int g, int 
                                               NodePre<D>& pre) {
   constexpr int nw = kWavesA;
   const int nrd = (rend - p0 - w + nw - 1) / nw;
-  for (int b = 0; b < NodeLds<D>::RES && b * kChunk < A.NN; ++b) node_issue<D>(A, g, b * kChunk, kv, b, w, nw, true);
+  for (int b = 0; b < NodeLds<D>::RES && b * kChunk < A.NN; ++b) node_issue<D>(A, g, b * kChunk, kv, b, w);
   // Mask byte of round i, chunk c: row p0 + w + 8 i (p0 past the wave's rows),
   // slot c kChunk + lane clamped into [0, NN); node_rows zeroes what is out of range.
   auto raw = [&](int c, int i) -> uint32_t {
-    const int t = min(c * kChunk + __lane_id(), A.NN - 1);
+    const int t = min(c * kChunk + (int)__lane_id(), A.NN - 1);
     const int r = i < nrd ? p0 + w + kWavesA * i : p0;
     return A.msk[(r >> A.GQS) * A.smm + t * A.smn];
   };
