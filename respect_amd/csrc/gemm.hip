@@ -400,14 +400,16 @@ __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
   }
 }
 
-// out[m][n] = round(((p0 + p1) + p2) + ...), 4 columns per thread.
+// out[m][n] = round(((p0 + p1) + p2) + ...), 4 columns per thread.  Grid:
+// x = 256-thread blocks along a row, y = rows from row0 (at most 65535 per
+// launch), so no thread divides to find its row.
 template <int SC>
 __global__ __launch_bounds__(256) void reduce_kernel(const float* part, int S, int M, int N, void* out, int64_t so,
-                                                     int out_fp32) {
-  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
-  if (i >= (int64_t)M * N) return;
-  const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
-  const f32x4 v = sum_parts4<SC>(part + i, S, (int64_t)M * N);
+                                                     int out_fp32, int row0) {
+  const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (n >= N) return;
+  const int m = row0 + blockIdx.y;
+  const f32x4 v = sum_parts4<SC>(part + (int64_t)m * N + n, S, (int64_t)M * N);
   if (out_fp32) {
     *reinterpret_cast<f32x4*>(static_cast<float*>(out) + (int64_t)m * so + n) = v;
   } else {
@@ -636,10 +638,13 @@ static int linear_launch(const void* x, int64_t sx, const void* w, int64_t sw, v
 #undef RSPX_GEMM_MT
 #undef RSPX_GEMM_NR
   if (S > 1 && !to_part) {
-    const int64_t quads = (int64_t)M * N / 4;
-    RSPX_WITH_SPLITS(S, SC,
-                     hipLaunchKernelGGL((gemm::reduce_kernel<SC>), dim3((unsigned)((quads + 255) / 256)), dim3(256), 0,
-                                        s, part, S, M, N, out, so, a.out_fp32));
+    const unsigned bx = (unsigned)((N / 4 + 255) / 256);
+    for (int row0 = 0; row0 < M; row0 += 65535) {
+      const dim3 rg(bx, (unsigned)min(M - row0, 65535));
+      RSPX_WITH_SPLITS(S, SC,
+                       hipLaunchKernelGGL((gemm::reduce_kernel<SC>), rg, dim3(256), 0, s, part, S, M, N, out, so,
+                                          a.out_fp32, row0));
+    }
   }
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }

@@ -16,7 +16,9 @@
 // (and its row's var), so rows never influence each other.
 //
 // 8 bf16 per thread: 16-byte loads, 16-byte bf16 stores, 2 x 16-byte fp32
-// stores.  Rows may be strided; the innermost dimension is contiguous.
+// stores.  Rows may be strided; the innermost dimension is contiguous.  Grid:
+// x = blocks of 8-element units along a row, y = rows from row0 (at most
+// 65535 per launch), so no thread divides to find its row.
 
 #include "common.h"
 #include "respect_amd.h"
@@ -28,12 +30,12 @@ __device__ __forceinline__ float rsqrt_rn(float v) { return 1.0f / __builtin_sqr
 }  // namespace
 static inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-__global__ __launch_bounds__(256) void square_kernel(const uint16_t* x, int64_t sx, float* q, int64_t sq, int rows,
-                                                     int vcols) {
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (gid >= (int64_t)rows * vcols) return;
-  const int row = (int)(gid / vcols);
-  const int c = (int)(gid - (int64_t)row * vcols) * 8;
+__global__ __launch_bounds__(256) void square_kernel(const uint16_t* x, int64_t sx, float* q, int64_t sq, int vcols,
+                                                     int row0) {
+  const int v = blockIdx.x * 256 + threadIdx.x;
+  if (v >= vcols) return;
+  const int row = row0 + blockIdx.y;
+  const int c = v * 8;
   const u32x4 xw = *reinterpret_cast<const u32x4*>(x + row * sx + c);
   f32x4 a, b;
 #pragma unroll
@@ -50,12 +52,12 @@ __global__ __launch_bounds__(256) void square_kernel(const uint16_t* x, int64_t 
 }
 
 __global__ __launch_bounds__(256) void add_sq_kernel(const uint16_t* r, int64_t sr, const uint16_t* h, int64_t sh,
-                                                     uint16_t* x, int64_t sx, float* q, int64_t sq, int rows,
-                                                     int vcols) {
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (gid >= (int64_t)rows * vcols) return;
-  const int row = (int)(gid / vcols);
-  const int c = (int)(gid - (int64_t)row * vcols) * 8;
+                                                     uint16_t* x, int64_t sx, float* q, int64_t sq, int vcols,
+                                                     int row0) {
+  const int v = blockIdx.x * 256 + threadIdx.x;
+  if (v >= vcols) return;
+  const int row = row0 + blockIdx.y;
+  const int c = v * 8;
   const u32x4 rw = *reinterpret_cast<const u32x4*>(r + row * sr + c);
   const u32x4 hw = *reinterpret_cast<const u32x4*>(h + row * sh + c);
   u32x4 xo;
@@ -78,12 +80,12 @@ __global__ __launch_bounds__(256) void add_sq_kernel(const uint16_t* r, int64_t 
 }
 
 __global__ __launch_bounds__(256) void norm_apply_kernel(const uint16_t* x, int64_t sx, const float* var,
-                                                         const uint16_t* w, uint16_t* y, int64_t sy, int rows,
-                                                         int vcols, float eps) {
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (gid >= (int64_t)rows * vcols) return;
-  const int row = (int)(gid / vcols);
-  const int c = (int)(gid - (int64_t)row * vcols) * 8;
+                                                         const uint16_t* w, uint16_t* y, int64_t sy, int vcols,
+                                                         float eps, int row0) {
+  const int v = blockIdx.x * 256 + threadIdx.x;
+  if (v >= vcols) return;
+  const int row = row0 + blockIdx.y;
+  const int c = v * 8;
   const float rr = rsqrt_rn(var[row] + eps);
   const u32x4 xw = *reinterpret_cast<const u32x4*>(x + row * sx + c);
   const u32x4 ww = *reinterpret_cast<const u32x4*>(w + c);
@@ -102,13 +104,13 @@ __global__ __launch_bounds__(256) void norm_apply_kernel(const uint16_t* x, int6
 // contiguous 8-element run.
 __global__ __launch_bounds__(256) void rope_vision_kernel(const uint16_t* x, int64_t sxl, int64_t sxh,
                                                           const float* cs, const float* sn, int64_t scl, uint16_t* y,
-                                                          int L, int NH, int D) {
+                                                          int NH, int D, int l0) {
   const int vD = D / 8;
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (gid >= (int64_t)L * NH * vD) return;
-  const int v = (int)(gid % vD);
-  const int64_t lh = gid / vD;
-  const int h = (int)(lh % NH), l = (int)(lh / NH);
+  const int u = blockIdx.x * 256 + threadIdx.x;   // unit of token l's NH x vD units
+  if (u >= NH * vD) return;
+  const int l = blockIdx.y + l0;
+  const int h = u / vD, v = u - h * vD;
+  const int64_t lh = (int64_t)l * NH + h;
   const int d = 8 * v, half = D / 2;
   const uint16_t* row = x + l * sxl + h * sxh;
   const bool lo = d < half;
@@ -132,10 +134,14 @@ __global__ __launch_bounds__(256) void rope_vision_kernel(const uint16_t* x, int
   *reinterpret_cast<u32x4*>(y + lh * D + d) = out;
 }
 
+// One launch per 65535 rows: grid (ceil(units / 256), rows), the kernel's
+// row0 argument last.
 template <class K, class... Args>
-static int launch_rows(K kernel, int64_t threads, void* stream, Args... args) {
-  hipLaunchKernelGGL(kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), args...);
+static int launch_rows(K kernel, int rows, int units, void* stream, Args... args) {
+  const unsigned bx = (unsigned)((units + 255) / 256);
+  for (int row0 = 0; row0 < rows; row0 += 65535)
+    hipLaunchKernelGGL(kernel, dim3(bx, (unsigned)min(rows - row0, 65535)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), args..., row0);
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }
 
@@ -149,8 +155,7 @@ extern "C" int rspx_square(const void* x, int64_t sx, float* q, int64_t sq, int 
   if ((int64_t)rows * n == 0) return RSPX_OK;
   if (!x || !q || sx < n || sq < n) return RSPX_EINVAL;
   if (!al16(x) || !al16(q) || sx % 8 || sq % 4) return RSPX_EALIGN;
-  return launch_rows(square_kernel, (int64_t)rows * (n / 8), stream, static_cast<const uint16_t*>(x), sx, q, sq, rows,
-                     n / 8);
+  return launch_rows(square_kernel, rows, n / 8, stream, static_cast<const uint16_t*>(x), sx, q, sq, n / 8);
 }
 
 extern "C" int rspx_add_sq(const void* r, int64_t sr, const void* h, int64_t sh, void* x, int64_t sx, float* q,
@@ -160,8 +165,8 @@ extern "C" int rspx_add_sq(const void* r, int64_t sr, const void* h, int64_t sh,
   if ((int64_t)rows * n == 0) return RSPX_OK;
   if (!r || !h || !x || !q || sr < n || sh < n || sx < n || sq < n) return RSPX_EINVAL;
   if (!al16(r) || !al16(h) || !al16(x) || !al16(q) || sr % 8 || sh % 8 || sx % 8 || sq % 4) return RSPX_EALIGN;
-  return launch_rows(add_sq_kernel, (int64_t)rows * (n / 8), stream, static_cast<const uint16_t*>(r), sr,
-                     static_cast<const uint16_t*>(h), sh, static_cast<uint16_t*>(x), sx, q, sq, rows, n / 8);
+  return launch_rows(add_sq_kernel, rows, n / 8, stream, static_cast<const uint16_t*>(r), sr,
+                     static_cast<const uint16_t*>(h), sh, static_cast<uint16_t*>(x), sx, q, sq, n / 8);
 }
 
 extern "C" int rspx_norm_apply(const void* x, int64_t sx, const float* var, const void* w, void* y, int64_t sy,
@@ -171,8 +176,8 @@ extern "C" int rspx_norm_apply(const void* x, int64_t sx, const float* var, cons
   if ((int64_t)rows * n == 0) return RSPX_OK;
   if (!x || !var || !w || !y || sx < n || sy < n) return RSPX_EINVAL;
   if (!al16(x) || !al16(w) || !al16(y) || sx % 8 || sy % 8) return RSPX_EALIGN;
-  return launch_rows(norm_apply_kernel, (int64_t)rows * (n / 8), stream, static_cast<const uint16_t*>(x), sx, var,
-                     static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy, rows, n / 8, eps);
+  return launch_rows(norm_apply_kernel, rows, n / 8, stream, static_cast<const uint16_t*>(x), sx, var,
+                     static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), sy, n / 8, eps);
 }
 
 extern "C" int rspx_rope_vision(const void* x, int64_t sxl, int64_t sxh, const float* cos, const float* sin,
@@ -182,6 +187,7 @@ extern "C" int rspx_rope_vision(const void* x, int64_t sxl, int64_t sxh, const f
   if ((int64_t)L * NH == 0) return RSPX_OK;
   if (!x || !cos || !sin || !y || scl < D) return RSPX_EINVAL;
   if (!al16(x) || !al16(cos) || !al16(sin) || !al16(y) || sxl % 8 || sxh % 8 || scl % 4) return RSPX_EALIGN;
-  return launch_rows(rope_vision_kernel, (int64_t)L * NH * (D / 8), stream, static_cast<const uint16_t*>(x), sxl,
-                     sxh, cos, sin, scl, static_cast<uint16_t*>(y), L, NH, D);
+  if ((int64_t)NH * (D / 8) > 0x7fffffff - 255) return RSPX_EUNSUPPORTED;
+  return launch_rows(rope_vision_kernel, L, NH * (D / 8), stream, static_cast<const uint16_t*>(x), sxl, sxh, cos,
+                     sin, scl, static_cast<uint16_t*>(y), NH, D);
 }

@@ -8,14 +8,16 @@
 //
 // Two bf16 per thread (4-byte loads of g and u, one 4-byte store), or one
 // where cols is odd or an operand is not 4-byte aligned (the same values).
-// On MI355X the packed gate/up [64, 2 x 12288] call takes 3.02 us at two
-// elements per thread, 3.09 at four and 3.42 at eight (rotating inputs beyond
-// the MALL): a launch this small is bound by memory latency, and more waves
-// in flight hide more of it.  Non-temporal stores (not kept in L2) shorten the
-// write-back at the kernel's end: 3.02 -> 2.80 us (non-temporal loads 2.86,
-// both 2.84).  g and u may be strided views (e.g. the two
-// halves of a packed [rows, 2F] gate/up).
-
+// Grid: x = 512-thread blocks along a row, y = rows (one launch per 65535
+// rows), so a thread finds its row and column without a division.  On MI355X the
+// packed gate/up [64, 2 x 12288] call (rotating inputs beyond the MALL)
+// takes 2.48 us; the same kernel indexed by one flat thread number, whose
+// row comes from a 64-bit division, took 2.79 us (the division's ~60
+// instructions stand before the loads of a call that is one memory round
+// trip).  256-thread blocks: 2.54 us; 128: 2.64 us; four elements per
+// thread: 3.02 us.  Non-temporal stores (not kept in L2) shorten the
+// write-back at the kernel's end (3.02 -> 2.80 us in the flat form).  g and
+// u may be strided views (e.g. the two halves of a packed [rows, 2F] gate/up).
 #include "common.h"
 #include "respect_amd.h"
 
@@ -23,13 +25,17 @@ namespace rspx {
 
 __device__ __forceinline__ float swiglu1(float g, float u) { return round_bf16(silu_f32(g)) * u; }
 
+constexpr int kSwigluThreads = 512;
+constexpr int kMaxGridY = 65535;
+
 template <bool PAIR>
-__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* g, int64_t sg, const uint16_t* u,
-                                                       int64_t su, uint16_t* y, int64_t sy, int rows, int units) {
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (gid >= (int64_t)rows * units) return;
-  const int row = (int)(gid / units);
-  const int c = (int)(gid - (int64_t)row * units) * (PAIR ? 2 : 1);
+__global__ __launch_bounds__(kSwigluThreads) void silu_mul_kernel(const uint16_t* g, int64_t sg, const uint16_t* u,
+                                                                  int64_t su, uint16_t* y, int64_t sy, int row0,
+                                                                  int units) {
+  const int unit = blockIdx.x * kSwigluThreads + threadIdx.x;
+  if (unit >= units) return;
+  const int c = unit * (PAIR ? 2 : 1);
+  const int row = row0 + blockIdx.y;
   if constexpr (PAIR) {
     const uint32_t gw = *reinterpret_cast<const uint32_t*>(g + row * sg + c);
     const uint32_t uw = *reinterpret_cast<const uint32_t*>(u + row * su + c);
@@ -40,7 +46,6 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* g, int64_
         f32_to_bf16_rne(swiglu1(bf16_to_f32(g[row * sg + c]), bf16_to_f32(u[row * su + c]))), y + row * sy + c);
   }
 }
-
 }  // namespace rspx
 
 using namespace rspx;
@@ -54,13 +59,15 @@ extern "C" int rspx_silu_mul(const void* g, int64_t sg, const void* u, int64_t s
   if (!al(g, 2) || !al(u, 2) || !al(y, 2)) return RSPX_EALIGN;
   const bool pair = cols % 2 == 0 && al(g, 4) && al(u, 4) && al(y, 4) && sg % 2 == 0 && su % 2 == 0 && sy % 2 == 0;
   const int units = pair ? cols / 2 : cols;
-  const int64_t blocks = ((int64_t)rows * units + 255) / 256;
-  if (blocks > 0x7fffffff) return RSPX_EUNSUPPORTED;
+  const unsigned bx = (unsigned)((units + kSwigluThreads - 1) / kSwigluThreads);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const uint16_t* G = static_cast<const uint16_t*>(g);
   const uint16_t* U = static_cast<const uint16_t*>(u);
   uint16_t* Y = static_cast<uint16_t*>(y);
-  if (pair) hipLaunchKernelGGL(silu_mul_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, G, sg, U, su, Y, sy, rows, units);
-  else hipLaunchKernelGGL(silu_mul_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, G, sg, U, su, Y, sy, rows, units);
+  for (int row0 = 0; row0 < rows; row0 += kMaxGridY) {   // one launch per 65535 rows
+    const dim3 grid(bx, (unsigned)min(rows - row0, kMaxGridY));
+    if (pair) hipLaunchKernelGGL(silu_mul_kernel<true>, grid, dim3(kSwigluThreads), 0, s, G, sg, U, su, Y, sy, row0, units);
+    else hipLaunchKernelGGL(silu_mul_kernel<false>, grid, dim3(kSwigluThreads), 0, s, G, sg, U, su, Y, sy, row0, units);
+  }
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }
