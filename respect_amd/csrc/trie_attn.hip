@@ -111,12 +111,16 @@ static_assert(sizeof(TrieAttnArgs) == 184, "kernel argument struct stays at 184 
 // merged; 15 end.
 constexpr int kPhaseMarks = 16;
 constexpr int kPhaseWgs = 1024;
+// Dispatch-order index of this workgroup (x fastest, then y, then z).
+__device__ __forceinline__ int wg_linear() {
+  return blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+}
 #ifdef RSPX_PHASE_TRACE
 __device__ uint64_t g_phase[kPhaseWgs * kWavesA * kPhaseMarks];
 #define RSPX_MARK(k)                                                                                   \
   do {                                                                                                 \
-    if (__lane_id() == 0 && blockIdx.x < kPhaseWgs)                                                    \
-      g_phase[(blockIdx.x * kWavesA + (threadIdx.x >> 6)) * kPhaseMarks + (k)] =                       \
+    if (__lane_id() == 0 && wg_linear() < kPhaseWgs)                                                   \
+      g_phase[(wg_linear() * kWavesA + (threadIdx.x >> 6)) * kPhaseMarks + (k)] =                      \
           __builtin_amdgcn_s_memrealtime();                                                            \
   } while (0)
 #else
@@ -660,9 +664,7 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
 template <int D, int kRT>
 __global__ __launch_bounds__(512) void prompt_kernel(TrieAttnArgs A) {
   __shared__ __attribute__((aligned(16))) char lds[PromptLds<D, kRT>::BYTES];
-  const int g = blockIdx.x % A.HK;
-  const int rest = blockIdx.x / A.HK;
-  prompt_block<D, kRT, false>(A, lds, g, rest % A.NRB, rest / A.NRB, [] {});
+  prompt_block<D, kRT, false>(A, lds, blockIdx.x, blockIdx.y, blockIdx.z, [] {});
 }
 
 // ------------------------------------------------------------------ node partials and merge
@@ -1574,7 +1576,15 @@ static_assert((kCountUnit & (kCountUnit - 1)) == 0, "2^32 is a multiple of the u
 template <int kRT>
 __device__ __forceinline__ void merge_share(const TrieAttnArgs& A, int rb, int q, int& r0, int& rend) {
   const int rows_blk = 32 * kRT;
-  const int rpw = 4 * ((rows_blk / 4 + A.NG - 1) / A.NG);
+  // ceil(rows_blk / 4 / NG) for NG = 1 .. kGroupTarget, 5 bits each: no division.
+  constexpr int a = rows_blk / 4;
+  constexpr uint64_t tab = [] {
+    uint64_t t = 0;
+    for (int n = 1; n <= kGroupTarget; ++n) t |= (uint64_t)((a + n - 1) / n) << (5 * n);
+    return t;
+  }();
+  static_assert(a < 32, "5-bit table entries");
+  const int rpw = 4 * (int)((tab >> (5 * A.NG)) & 31);
   r0 = rb * rows_blk + q * rpw;
   rend = min(rb * rows_blk + min(rows_blk, (q + 1) * rpw), A.R);
 }
@@ -1670,10 +1680,12 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   __shared__ __attribute__((aligned(16))) char lds[LB];
   RSPX_MARK(0);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g = blockIdx.x % A.HK;
-  const int rest = blockIdx.x / A.HK;
-  const int rb = rest % A.NRB;
-  const int q = rest / A.NRB;
+  const int g = blockIdx.x, rb = blockIdx.y, q = blockIdx.z;
+  // Every argument the prologue needs, requested in one batch: left to the
+  // compiler, they came in three dependent scalar-load round trips before the
+  // first K/V request.
+  asm volatile("" ::"s"(A.q), "s"(A.kp), "s"(A.vp), "s"(A.sync), "s"(A.sqh), "s"(A.sqm), "s"(A.skph), "s"(A.skpn),
+               "s"(A.svph), "s"(A.svpn), "s"(A.P), "s"(A.NRB), "s"(A.NG), "s"(A.S), "s"(A.R), "s"(A.GQS));
   int r0, rend;
   merge_share<kRT>(A, rb, q, r0, rend);
   const int rend0 = min(rend, r0 + kNodeRows);               // the first batch of node rows
@@ -1703,11 +1715,11 @@ __global__ __launch_bounds__(512) void fused2_kernel(TrieAttnArgs A) {
   constexpr int NB = node_area_bytes<D>() + 16;
   constexpr int LB = PromptLds<D, kRT>::BYTES > NB ? PromptLds<D, kRT>::BYTES : NB;
   __shared__ __attribute__((aligned(16))) char lds[LB];
-  const int g = blockIdx.x % A.HK;
-  const int rest = blockIdx.x / A.HK;
+  const int g = blockIdx.x, rbw = blockIdx.y, q = blockIdx.z;
+  // Every argument the prologue needs, requested in one batch.
+  asm volatile("" ::"s"(A.q), "s"(A.kp), "s"(A.vp), "s"(A.sync), "s"(A.sqh), "s"(A.sqm), "s"(A.skph), "s"(A.skpn),
+               "s"(A.svph), "s"(A.svpn), "s"(A.P), "s"(A.NRB), "s"(A.NG), "s"(A.S), "s"(A.R), "s"(A.GQS));
   const int NRBW = (A.NRB + 1) / 2;
-  const int rbw = rest % NRBW;
-  const int q = rest / NRBW;
   const int nb = rbw + NRBW < A.NRB ? 2 : 1;
   const int old[2] = {counter_before(A, g, rbw), counter_before(A, g, nb > 1 ? rbw + NRBW : rbw)};
   for (int b = 0; b < 2; ++b) {
@@ -1811,16 +1823,16 @@ static void launch_rt(const TrieAttnArgs& a, const Plan& pl, hipStream_t s, int 
                    (size_t)a.HK * pl.R * pl.NG * D * sizeof(float) < (size_t(1) << 31);
   const int cap = one ? fused_capacity<D, RT>() : 0;
   if (one && pl.prompt_wgs <= cap) {
-    hipLaunchKernelGGL((fused_kernel<D, RT>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);
+    hipLaunchKernelGGL((fused_kernel<D, RT>), dim3(a.HK, pl.NRB, pl.NG), dim3(64 * kWavesA), 0, s, a);
     return;
   }
   // Two row blocks per workgroup (fused2_kernel) when that grid fits.
   const int wgs2 = a.HK * ((pl.NRB + 1) / 2) * pl.NG;
   if (one && pl.NRB > 1 && wgs2 <= fused_capacity<D, RT, true>()) {
-    hipLaunchKernelGGL((fused2_kernel<D, RT>), dim3(wgs2), dim3(64 * kWavesA), 0, s, a);
+    hipLaunchKernelGGL((fused2_kernel<D, RT>), dim3(a.HK, (pl.NRB + 1) / 2, pl.NG), dim3(64 * kWavesA), 0, s, a);
     return;
   }
-  if (pl.prompt_wgs > 0) hipLaunchKernelGGL((prompt_kernel<D, RT>), dim3(pl.prompt_wgs), dim3(64 * kWavesA), 0, s, a);
+  if (pl.prompt_wgs > 0) hipLaunchKernelGGL((prompt_kernel<D, RT>), dim3(a.HK, pl.NRB, pl.NG), dim3(64 * kWavesA), 0, s, a);
   hipLaunchKernelGGL((node_merge_kernel<D>), dim3(pl.node_wgs), dim3(64 * kWavesA), 0, s, a);
 }
 
