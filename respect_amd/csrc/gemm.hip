@@ -264,11 +264,11 @@ __global__ __launch_bounds__(64 * W) void gemm_kernel(Args A) {
   constexpr int NC = 8 * MT;
   const int XPW = NC % W == 0 ? NC / W : (NC - w + W - 1) / W;
   const int n16 = lane & 15, g4 = lane >> 4;
-  const int NT = (A.N + kCols - 1) / kCols;
-  const int nt = blockIdx.x % NT;
-  const int rest = blockIdx.x / NT;
-  const int s = rest % A.S;
-  const int mt = rest / A.S;
+  // Grid (column tile, K chunk, 64-row tile): no index divisions.  The
+  // arguments the prologue needs are requested in one batch.
+  const int nt = blockIdx.x, s = blockIdx.y, mt = blockIdx.z;
+  asm volatile("" ::"s"(A.x), "s"(A.w), "s"(A.sx), "s"(A.sw), "s"(A.M), "s"(A.N), "s"(A.K), "s"(A.KC),
+               "s"(A.x_tiled));
   const int col = nt * kCols + 16 * w;        // this wave's first column
   const int row0 = mt * kRows;
   const int k0 = s * A.KC;
@@ -598,8 +598,7 @@ static int linear_launch(const void* x, int64_t sx, const void* w, int64_t sw, v
   const int waves = (N % 96 == 0 && wg8 < 256 && wg6 >= 256 && wg6 <= 512) ? 6
                     : (wg8 >= 192 && (M >= 32 || wg8 < 1024)) ? 8 : 4;
   const int NT = (N + 16 * waves - 1) / (16 * waves);
-  const int64_t grid = (int64_t)NT * S * MTILES;
-  if (grid > 0x7fffffff) return RSPX_EUNSUPPORTED;
+  if (MTILES > 65535) return RSPX_EUNSUPPORTED;
   const int mt = (MTILES > 1 || M >= 64) ? 4 : (M + 15) / 16;  // row tiles per 64-row tile
   // X-resident blocks pay where X is large against each block's W slice and
   // the grid is one wave of 6- or 8-wave blocks (q/k/v [64 x 4096] .
@@ -607,7 +606,7 @@ static int linear_launch(const void* x, int64_t sx, const void* w, int64_t sw, v
   // one row they cost a little.
   const bool xres = waves >= 6 && M >= 32;
   const int nr = a.KC / gemm::kRoundK;
-  const dim3 g((unsigned)grid), b(64 * waves);
+  const dim3 g((unsigned)NT, (unsigned)S, (unsigned)MTILES), b(64 * waves);
 #define RSPX_GEMM_NR(MTV, WV, WTV)                                                                       \
   switch (nr) {                                                                                          \
     case 1: hipLaunchKernelGGL((gemm::gemm_kernel<MTV, 1, WV, false, WTV>), g, b, 0, s, a); break;       \
