@@ -398,18 +398,21 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(const uint16_t* qkv
                                                              const uint16_t* wk, const uint16_t* cosb,
                                                              const uint16_t* sinb, int64_t scs, const int* slots,
                                                              int cap, uint16_t* ck, int64_t skh, int64_t skn, uint16_t* cv,
-                                                             int64_t svh, int64_t svn, uint16_t* qo, int T, int HQ,
+                                                             int64_t svh, int64_t svn, uint16_t* qo, int t0, int HQ,
                                                              int HK, float eps) {
+  // Grid (blocks of 16 head rows, token t0 + y): token t's q heads, then its
+  // k heads, then its v heads; no index division.  The arguments the loads
+  // need are requested in one batch (left to the compiler: three dependent
+  // scalar-load round trips).
+  asm volatile("" ::"s"(qkv), "s"(sqkv), "s"(qp), "s"(S), "s"(sps), "s"(wq), "s"(wk), "s"(cosb), "s"(sinb),
+               "s"(scs), "s"(slots), "s"(t0), "s"(HQ), "s"(HK));
   constexpr int D = 128;
-  const int gid = blockIdx.x * 256 + threadIdx.x;
-  const int rowid = gid >> 4;
-  const int sub = gid & 15;
-  const int nq = T * HQ, nk = T * HK;
-  if (rowid >= nq + 2 * nk) return;
-  int kind, t, hh;
-  if (rowid < nq) { kind = 0; t = rowid / HQ; hh = rowid - t * HQ; }
-  else if (rowid < nq + nk) { kind = 1; t = (rowid - nq) / HK; hh = rowid - nq - t * HK; }
-  else { kind = 2; t = (rowid - nq - nk) / HK; hh = rowid - nq - nk - t * HK; }
+  const int rowid = (blockIdx.x * 256 + threadIdx.x) >> 4;   // head row of the token
+  const int sub = threadIdx.x & 15;
+  if (rowid >= HQ + 2 * HK) return;
+  const int t = t0 + blockIdx.y;
+  const int kind = rowid < HQ ? 0 : rowid < HQ + HK ? 1 : 2;
+  const int hh = kind == 0 ? rowid : kind == 1 ? rowid - HQ : rowid - HQ - HK;
   const int col = (kind == 0 ? hh * D : kind == 1 ? (HQ + hh) * D : (HQ + HK + hh) * D) + sub * 8;
   // Norm weights and rotary rows are requested with the projection values
   // (v rows load them unused): after the reduction they would be one more
@@ -874,16 +877,20 @@ static int qkv_rope_cache_launch(const uint16_t* qkv, int64_t sqkv, const float*
 #undef RSPX_QKVC_ANY
     return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
   }
-  const int64_t threads = (int64_t)T * (HQ + 2 * HK) * 16;
-  if (threads + 255 >= 0x7fffff00) return RSPX_EUNSUPPORTED;   // 32-bit thread indices
-  RSPX_WITH_SPLITS(qp ? S : 1, SC,
-                   hipLaunchKernelGGL((qkv_rope_cache_kernel<SC>), dim3((unsigned)((threads + 255) / 256)), dim3(256),
-                                      0, static_cast<hipStream_t>(stream), qkv, sqkv, qp, S, sps,
-                                      static_cast<const uint16_t*>(wq), static_cast<const uint16_t*>(wk),
-                                      static_cast<const uint16_t*>(cosb), static_cast<const uint16_t*>(sinb), scs,
-                                      slots, cap, static_cast<uint16_t*>(cache_k), skh, skn,
-                                      static_cast<uint16_t*>(cache_v), svh, svn, static_cast<uint16_t*>(qo), T, HQ,
-                                      HK, eps));
+  const int64_t per_token = (int64_t)(HQ + 2 * HK) * 16;
+  if (per_token + 255 >= 0x7fffff00) return RSPX_EUNSUPPORTED;   // 32-bit thread indices
+  const unsigned bx = (unsigned)((per_token + 255) / 256);
+  for (int t0 = 0; t0 < T; t0 += 65535) {   // one launch per 65535 tokens
+    const dim3 grid(bx, (unsigned)min(T - t0, 65535));
+    RSPX_WITH_SPLITS(qp ? S : 1, SC,
+                     hipLaunchKernelGGL((qkv_rope_cache_kernel<SC>), grid, dim3(256), 0,
+                                        static_cast<hipStream_t>(stream), qkv, sqkv, qp, S, sps,
+                                        static_cast<const uint16_t*>(wq), static_cast<const uint16_t*>(wk),
+                                        static_cast<const uint16_t*>(cosb), static_cast<const uint16_t*>(sinb), scs,
+                                        slots, cap, static_cast<uint16_t*>(cache_k), skh, skn,
+                                        static_cast<uint16_t*>(cache_v), svh, svn, static_cast<uint16_t*>(qo), t0, HQ,
+                                        HK, eps));
+  }
   return hipGetLastError() == hipSuccess ? RSPX_OK : RSPX_ELAUNCH;
 }
 
