@@ -100,6 +100,10 @@ struct TrieAttnArgs {
 };
 static_assert(sizeof(TrieAttnArgs) == 184, "kernel argument struct stays at 184 bytes");
 
+__device__ __forceinline__ int wg_index(const TrieAttnArgs& A, int g, int rb, int q) {
+  return g + A.HK * (rb + A.NRB * q);
+}
+
 // Phase timestamps (built only with -DRSPX_PHASE_TRACE, into a separate
 // library; the product library has none of this): wave w of workgroup b
 // records the device's real-time counter (s_memrealtime, 100 MHz) at mark k
@@ -111,16 +115,15 @@ static_assert(sizeof(TrieAttnArgs) == 184, "kernel argument struct stays at 184 
 // merged; 15 end.
 constexpr int kPhaseMarks = 16;
 constexpr int kPhaseWgs = 1024;
-// Dispatch-order index of this workgroup (x fastest, then y, then z).
-__device__ __forceinline__ int wg_linear() {
-  return blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-}
+// Dispatch-order index of workgroup (g, rb, q) of the one-launch grid
+// (kv head fastest, then row block, then group), from values every mark's
+// scope holds: no grid-size loads in the traced kernel.
 #ifdef RSPX_PHASE_TRACE
 __device__ uint64_t g_phase[kPhaseWgs * kWavesA * kPhaseMarks];
 #define RSPX_MARK(k)                                                                                   \
   do {                                                                                                 \
-    if (__lane_id() == 0 && wg_linear() < kPhaseWgs)                                                   \
-      g_phase[(wg_linear() * kWavesA + (threadIdx.x >> 6)) * kPhaseMarks + (k)] =                      \
+    if (__lane_id() == 0 && wg_index(A, g, rb, q) < kPhaseWgs)                                         \
+      g_phase[(wg_index(A, g, rb, q) * kWavesA + (threadIdx.x >> 6)) * kPhaseMarks + (k)] =            \
           __builtin_amdgcn_s_memrealtime();                                                            \
   } while (0)
 #else
@@ -1678,9 +1681,9 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   constexpr int LB = PromptLds<D, kRT>::BYTES > NB ? PromptLds<D, kRT>::BYTES : NB;
   static_assert(NB <= PromptLds<D, kRT>::RINGBYTES, "node LDS and the wait flag inside the ring");
   __shared__ __attribute__((aligned(16))) char lds[LB];
-  RSPX_MARK(0);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = blockIdx.x, rb = blockIdx.y, q = blockIdx.z;
+  RSPX_MARK(0);
   // Every argument the prologue needs, requested in one batch: left to the
   // compiler, they came in three dependent scalar-load round trips before the
   // first K/V request.
