@@ -1783,6 +1783,7 @@ static int make_plan(int H, int HK, int M, int P, int NN, int D, int rows_per_wa
   if (D == 256 && rt != 1) return RSPX_EUNSUPPORTED;
   pl->RT = rt;
   pl->NRB = (pl->R + 32 * rt - 1) / (32 * rt);
+  if (pl->NRB > 65535) return RSPX_EUNSUPPORTED;   // the grid's y dimension (row blocks)
   pl->prompt_wgs = HK * pl->NRB * pl->NG;
   pl->node_wgs = HK * ((pl->R + 7) / 8);
   const size_t parts = (size_t)HK * pl->R * pl->NG;
