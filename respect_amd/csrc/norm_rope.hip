@@ -382,6 +382,9 @@ __device__ __forceinline__ void qk_norm_rope_row(const QKArgs& a, int gid) {
 }
 
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QKArgs a) {
+  asm volatile("" ::"s"(a.q), "s"(a.k), "s"(a.sqt), "s"(a.sqh), "s"(a.skt), "s"(a.skh), "s"(a.wq), "s"(a.wk),
+               "s"(a.cosb), "s"(a.sinb), "s"(a.scs), "s"(a.qo), "s"(a.ko), "s"(a.T), "s"(a.HQ), "s"(a.HK),
+               "s"(a.eps));   // one argument batch
   qk_norm_rope_row<false>(a, blockIdx.x * 256 + threadIdx.x);
 }
 
@@ -597,6 +600,12 @@ template <int NK, int QK, int TH>
 __global__ __launch_bounds__(TH) void rmsnorm_qk_norm_rope_kernel(RowIn in, const uint16_t* w, uint16_t* y,
                                                                   int64_t sy, int rows, int n, float eps, int nb,
                                                                   QKArgs a) {
+  // The arguments either kind of workgroup needs before its loads, requested
+  // in one batch (left to the compiler: three or four dependent scalar-load
+  // round trips).
+  asm volatile("" ::"s"(nb), "s"(in.x), "s"(in.sx), "s"(w), "s"(rows), "s"(n), "s"(a.q), "s"(a.k), "s"(a.sqt),
+               "s"(a.sqh), "s"(a.skt), "s"(a.skh), "s"(a.wq), "s"(a.wk), "s"(a.cosb), "s"(a.sinb), "s"(a.scs),
+               "s"(a.qo), "s"(a.ko), "s"(a.T), "s"(a.HQ), "s"(a.HK), "s"(a.D), "s"(a.eps), "s"(y), "s"(sy), "s"(eps));
   if ((int)blockIdx.x < nb) {
     if constexpr (NK <= 1) {
       constexpr int TPR = NK == 0 ? 16 : 64;
