@@ -86,6 +86,15 @@ struct RowIn {
   uint16_t* xo; int64_t sxo;
 };
 
+// The arguments a row kernel needs before its loads, requested in one batch
+// (left to the compiler they come in two or three dependent scalar-load round
+// trips, each in front of the loads that use them).
+__device__ __forceinline__ void pin_row_args(const RowIn& in, const uint16_t* w, const uint16_t* y, int64_t sy,
+                                             int n, float eps) {
+  asm volatile("" ::"s"(in.x), "s"(in.sx), "s"(in.h), "s"(in.sh), "s"(in.hp), "s"(in.shp), "s"(in.sps), "s"(in.S),
+               "s"(in.xo), "s"(in.sxo), "s"(w), "s"(y), "s"(sy), "s"(n), "s"(eps));
+}
+
 template <int MODE, int SC>
 __device__ __forceinline__ void load_row_vec(const RowIn& in, int row, int c, float* v) {
   unpack8(*reinterpret_cast<const u32x4*>(in.x + row * in.sx + c), v);
@@ -160,6 +169,7 @@ __device__ __forceinline__ void rms_row_wave(const RowIn& in, int row, const uin
 template <int TPR, int VPL, int MODE, int SC>
 __global__ __launch_bounds__(256) void rmsnorm_small_kernel(RowIn in, const uint16_t* w, uint16_t* y, int64_t sy,
                                                             int rows, int n, float eps) {
+  pin_row_args(in, w, y, sy, n, eps);
   const int lane = __lane_id();
   const int row = (blockIdx.x * 256 + threadIdx.x) / TPR;
   const int sub = lane % TPR;
@@ -219,6 +229,7 @@ __device__ __forceinline__ void rms_row_block(const RowIn& in, const uint16_t* w
 template <int VPL, int MODE, int SC, int TH = 256>
 __global__ __launch_bounds__(TH) void rmsnorm_row_kernel(RowIn in, const uint16_t* w, uint16_t* y, int64_t sy, int n,
                                                          float eps) {
+  pin_row_args(in, w, y, sy, n, eps);
   rms_row_block<VPL, MODE, SC, TH>(in, w, y, sy, blockIdx.x, n, eps);
 }
 

@@ -32,6 +32,8 @@ template <bool PAIR>
 __global__ __launch_bounds__(kSwigluThreads) void silu_mul_kernel(const uint16_t* g, int64_t sg, const uint16_t* u,
                                                                   int64_t su, uint16_t* y, int64_t sy, int row0,
                                                                   int units) {
+  // Every argument in one scalar-load batch, ahead of the index arithmetic.
+  asm volatile("" ::"s"(g), "s"(sg), "s"(u), "s"(su), "s"(y), "s"(sy), "s"(row0), "s"(units));
   const int unit = blockIdx.x * kSwigluThreads + threadIdx.x;
   if (unit >= units) return;
   const int c = unit * (PAIR ? 2 : 1);
