@@ -62,12 +62,12 @@ def time_launches(launchers, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
-CPU_SHARE = 16   # host CPUs a one-GPU box allots to the GPU's job (its OMP_NUM_THREADS)
+CPU_SHARE = 16   # host CPUs allotted to one GPU's job on a shared multi-GPU host (its OMP_NUM_THREADS)
 
 
 def cpu_counts() -> dict:
     """The host's logical CPU count, how many this process may run on (affinity) and
-    the thread count the CPU baseline uses: the affinity count, at most the box's
+    the thread count the CPU baseline uses: the affinity count, at most the host's
     CPU share per GPU (CPU_SHARE; the rest of the host belongs to other GPUs' jobs)."""
     total = os.cpu_count() or 1
     try:

@@ -1,7 +1,7 @@
 """Writes tests/golden/mfma_16x16x32_bf16.npz: inputs and MI355X outputs of
 v_mfma_f32_16x16x32_bf16 (tests/golden/mfma_probe.hip, one MFMA per wave) on operands
 shaped like the attention kernel's -- scores (q, k ~ N(0,1) bf16, a running fp32 sum)
-and PV (v ~ N(0,1), p = 2^U(-25, 8) in bf16, a running fp32 sum).  Run on a GPU box:
+and PV (v ~ N(0,1), p = 2^U(-25, 8) in bf16, a running fp32 sum).  Run on an MI355X:
 
     hipcc --offload-arch=gfx950 -O2 -shared -fPIC -o /tmp/mfma_probe.so tests/golden/mfma_probe.hip
     python tests/golden/make_mfma_fixture.py /tmp/mfma_probe.so
