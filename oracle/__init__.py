@@ -2,8 +2,8 @@
 
 This package restates, on the CPU with numpy, the arithmetic of the reference
 implementation (soonhong99/respect) for the trie-verification hot path, plus
-float64 closed forms used to pin it.  It is the checker, never the thing that
-is measured or shipped: only ``tests/``, ``__graft_entry__.smoke()`` and the
+float64 closed forms used to pin it.  It checks results; it is never the thing
+that is measured or shipped: only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import it.  The product path
 (``respect_amd``) never imports it and has no CPU fallback.
 
