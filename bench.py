@@ -712,7 +712,8 @@ def phase_trace(args) -> int:
     L.rspx_trie_attn_phase_trace.argtypes = [ctypes.c_void_p, ctypes.c_int64]
     from respect_amd.kernels.attention import make_launcher
     from respect_amd.workloads import AttnWorkload
-    wl = AttnWorkload(sets=args.sets, seed=0)
+    committed = args.trace_committed
+    wl = AttnWorkload(sets=args.sets, seed=committed, base=committed) if committed else AttnWorkload(sets=args.sets, seed=0)
     launchers = [make_launcher(*st, wl.msk, wl.sm_scale)[0] for st in wl.sets]
     for i in range(40):
         launchers[i % len(launchers)]()
@@ -733,7 +734,9 @@ def phase_trace(args) -> int:
         rows.append({"phase": PHASES[k - 1], "median_us": round(float(np.median(d)), 2),
                      "max_us": round(float(d.max()), 2), "ends_at_us": round(float(np.median(ends[:, k])) / 100, 2)})
         prev = ends[:, k]
-    out = {"workload": "8B-shape attention, 64-node trie, KV 3072: the last of 40 back-to-back calls",
+    out = {"workload": "8B-shape attention, 64-node trie, KV 3072"
+                       + (f", after {committed} committed node slots" if committed else "")
+                       + ": the last of 40 back-to-back calls",
            "workgroups": nwg, "start_spread_us": round(float(starts.max() - starts.min()) / 100, 2),
            "first_start_to_last_end_us": round(float(span), 2),
            "wg_length_median_us": round(float(np.median(ends[:, 15] - starts)) / 100, 2), "phases": rows}
@@ -759,6 +762,8 @@ def main() -> int:
     ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--phase-trace", action="store_true",
                     help="phase timeline of the headline call from the trace build (librespect_amd_trace.so)")
+    ap.add_argument("--trace-committed", type=int, default=0,
+                    help="with --phase-trace: that many committed node slots before the trie (extra.attn_committed)")
     ap.add_argument("--counter-probe", action="store_true",
                     help="a few attention and linear-layer dispatches for rocprofv3 --pmc (MFMA counters)")
     args = ap.parse_args()
