@@ -1,7 +1,8 @@
 """Calls with more rows than one grid's y dimension holds (65,535).
 
-The element-wise kernels, the split-K reduction of the linear layer and the
-vision RoPE take a row from `blockIdx.y` and run one launch per 65,535 rows.
+The element-wise kernels, the split-K reduction of the linear layer, the vision
+RoPE and the decoder's q/k/v epilogue take a row (token) from `blockIdx.y` and
+run one launch per 65,535 rows.
 Every row of a 66,000-row call must match the oracle (bitwise where the kernel
 is bitwise), and the rows on either side of the launch boundary must equal the
 same rows computed in a small call.
@@ -80,3 +81,37 @@ def test_linear_split_k_reduction_past_grid_rows():
     bound = G.linear_error_bound(x[rows], w)
     o = _np(out[torch.from_numpy(rows).cuda()])
     assert np.all(np.abs(o - ex) <= bound + bf16.ulp(np.abs(ex) + bound))
+
+
+def test_qkv_rope_cache_past_grid_tokens():
+    """The decoder's q/k/v epilogue (grid: head rows x tokens) over 66,000 tokens: q, K and
+    V rows bitwise those of rspx_qk_norm_rope (a flat grid) and of the packed projection."""
+    from respect_amd import _lib
+    from respect_amd.system.fused import qk_norm_rope
+    T, HQ, HK, D = ROWS, 1, 1, 128
+    print(f"[qkv_rope_cache] T={T}", flush=True)
+    rng = np.random.default_rng(17)
+    q = gen.bf16_normal(rng, (T, HQ, D))
+    k = gen.bf16_normal(rng, (T, HK, D))
+    v = gen.bf16_normal(rng, (T, HK, D))
+    wq = bf16.round_bf16(1 + 0.02 * rng.standard_normal(D).astype(np.float32))
+    wk = bf16.round_bf16(1 + 0.02 * rng.standard_normal(D).astype(np.float32))
+    cos, sin = N.rope_tables(rng.integers(0, 8192, T), head_dim=D)
+    wqd, wkd, cosd, sind = _dev(wq), _dev(wk), _dev(cos), _dev(sin)
+    qo, ko = qk_norm_rope(_dev(q), _dev(k), wqd, wkd, 1e-6, cosd, sind)
+    L = _lib.lib()
+    s = _lib.stream_ptr(torch.device("cuda"))
+    qkv = _dev(np.concatenate([q.reshape(T, -1), k.reshape(T, -1), v.reshape(T, -1)], axis=1))
+    n = (HQ + 2 * HK) * D
+    P = T + 5
+    slots = torch.arange(2, 2 + T, dtype=torch.int32, device="cuda")
+    ck = torch.zeros(HK, P, D, device="cuda", dtype=torch.bfloat16)
+    cv = torch.zeros_like(ck)
+    q2 = torch.empty(T, HQ, D, device="cuda", dtype=torch.bfloat16)
+    _lib.check("rspx_qkv_rope_cache", L.rspx_qkv_rope_cache(
+        qkv.data_ptr(), n, wqd.data_ptr(), wkd.data_ptr(), cosd.data_ptr(), sind.data_ptr(), D,
+        slots.data_ptr(), P, ck.data_ptr(), P * D, D, cv.data_ptr(), P * D, D, q2.data_ptr(), T, HQ, HK, D, 1e-6, s))
+    torch.cuda.synchronize()
+    assert torch.equal(q2, qo)
+    assert torch.equal(ck[:, 2:2 + T].transpose(0, 1), ko)
+    assert torch.equal(cv[:, 2:2 + T].transpose(0, 1), _dev(v))
