@@ -326,7 +326,9 @@ struct PromptLds {
   static constexpr int QBYTES = 2 * kRT * G::DQ * 1024;
   static constexpr int RINGBYTES = G::RING * G::ROUND;
   static constexpr int BYTES = RINGBYTES + QBYTES;
-  static_assert(BYTES <= 160 * 1024, "LDS budget");
+  // The quarters' (m, l) of the combine, past the Q fragments (KEEP_Q).
+  static constexpr int MLBYTES = 8 * kRT * 16 * 8;
+  static_assert(BYTES + MLBYTES <= 160 * 1024, "LDS budget");
 };
 
 // The prompt work of workgroup (g, rb, q) -- kv head g, rows [32 kRT rb,
@@ -334,7 +336,9 @@ struct PromptLds {
 // memory.  Wave w: row half h = w / 4 (kRT tiles of 16 rows), key quarter
 // k = w % 4 (steps 4 i + k of the group).  ATOMIC: the partial is stored with
 // agent-scope atomic stores (write-through) for a merge inside the same launch.
-template <int D, int kRT, bool ATOMIC, bool EARLY_STORES = false, class Hook>
+// KEEP_Q: the combine's (m, l) go past the Q fragments (PromptLds::MLBYTES more
+// LDS), which stay in place for the hook and after it.
+template <int D, int kRT, bool ATOMIC, bool EARLY_STORES = false, bool KEEP_Q = false, class Hook>
 __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, int g, int rb, int q,
                                              const Hook& before_stores) {
   using G = StepGeom<D>;
@@ -571,8 +575,8 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
   typedef __attribute__((address_space(3))) f32x2 lds_f32x2;
   constexpr int BR = 32 * kRT;  // rows of the block
   static_assert(4 * BR * D * 4 <= RINGBYTES, "the four scaled quarters fit the ring");
-  static_assert(8 * kRT * 16 * 8 <= L::QBYTES, "quarter (m, l) fit the Q area");
-  lds_float* qml = (lds_float*)qreg;    // [h][k][t][16 rows] (m, l)
+  static_assert(L::MLBYTES <= L::QBYTES, "quarter (m, l) fit the Q area");
+  lds_float* qml = (lds_float*)(KEEP_Q ? qreg + L::QBYTES : qreg);    // [h][k][t][16 rows] (m, l)
   lds_float* qacc = (lds_float*)ring;   // [k][BR rows][D], 16-byte units swizzled by row
   lds_barrier();
   if (g4 == 0) {
@@ -859,6 +863,41 @@ __device__ __forceinline__ void node_q(const TrieAttnArgs& A, int g, int p0, int
   const uint16_t* qp = A.q + (R.hd * A.sqh + R.mq * A.sqm + 8 * (lane >> 4));
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) qf[i] = *reinterpret_cast<const bf16x8*>(qp + 32 * i);
+}
+
+// node_q's fragment from a prompt workgroup's Q fragments in LDS (prompt_block
+// with KEEP_Q: chunk (tile T, i) at qreg + 1 KB (T DQ + i), lane (n16, g4)
+// holding row 16 T + n16 of the block from row0, head_dim [32 i + 8 g4, +8)),
+// for rows p0 .. rend - 1 of that block.  The asm read and its own lgkmcnt
+// wait keep the compiler from fencing it behind the direct-to-LDS loads in
+// flight.
+template <int D>
+__device__ __forceinline__ void node_q_lds(const lds_char* qreg, int row0, int p0, int rend, bf16x8 (&qf)[D / 32]) {
+  constexpr int DQ = D / 32;
+  const int lane = __lane_id();
+  const int r = p0 + (lane & 15);
+  const int br = (r < rend ? r : p0) - row0;
+  const lds_char* src = qreg + (br >> 4) * DQ * 1024 + 16 * ((br & 15) + 16 * (lane >> 4));
+  if constexpr (DQ == 4) {
+    u32x4 v0, v1, v2, v3;
+    asm volatile(
+        "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:1024\n\t"
+        "ds_read_b128 %2, %4 offset:2048\n\tds_read_b128 %3, %4 offset:3072\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3)
+        : "v"(src)
+        : "memory");
+    qf[0] = __builtin_bit_cast(bf16x8, v0);
+    qf[1] = __builtin_bit_cast(bf16x8, v1);
+    qf[2] = __builtin_bit_cast(bf16x8, v2);
+    qf[3] = __builtin_bit_cast(bf16x8, v3);
+  } else {
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) {
+      u32x4 v;
+      asm volatile("ds_read_b128 %0, %1 offset:%2\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(src), "i"(1024 * i) : "memory");
+      qf[i] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
 }
 
 // Mask byte of row r (below R) for slot c0 + lane; 0 past NN.
@@ -1358,9 +1397,11 @@ __device__ __forceinline__ const lds_float* node_rows(const TrieAttnArgs& A, int
 
 // Issues node_rows' loads of a resident segment (0 < NN <= RES kChunk,
 // p0 < rend): chunk c into buffer c, the mask bytes and the score fragment.
+// qreg (not null): the score fragment from prompt_block's Q fragments in LDS
+// (KEEP_Q), rows from row0, instead of from memory.
 template <int D>
 __device__ __forceinline__ void node_prefetch(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv, int w,
-                                              NodePre<D>& pre) {
+                                              NodePre<D>& pre, const lds_char* qreg = nullptr, int row0 = 0) {
   constexpr int nw = kWavesA;
   const int nrd = (rend - p0 - w + nw - 1) / nw;
   for (int b = 0; b < NodeLds<D>::RES && b * kChunk < A.NN; ++b) node_issue<D>(A, g, b * kChunk, kv, b, w);
@@ -1381,7 +1422,8 @@ __device__ __forceinline__ void node_prefetch(const TrieAttnArgs& A, int g, int 
     pre.m20 = raw(2, 0);
     pre.m21 = raw(2, 1);
   }
-  node_q<D>(A, g, p0, rend, pre.qf);
+  if (qreg) node_q_lds<D>(qreg, row0, p0, rend, pre.qf);
+  else node_q<D>(A, g, p0, rend, pre.qf);
 }
 
 
@@ -1685,9 +1727,10 @@ __device__ __forceinline__ int counter_before(const TrieAttnArgs& A, int g, int 
 template <int D, int kRT>
 __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   using LY = NodeLds<D>;
+  using PL = PromptLds<D, kRT>;
   constexpr int NB = node_area_bytes<D>() + 16;
-  constexpr int LB = PromptLds<D, kRT>::BYTES > NB ? PromptLds<D, kRT>::BYTES : NB;
-  static_assert(NB <= PromptLds<D, kRT>::RINGBYTES, "node LDS and the wait flag inside the ring");
+  constexpr int LB = PL::BYTES + PL::MLBYTES > NB ? PL::BYTES + PL::MLBYTES : NB;
+  static_assert(NB <= PL::RINGBYTES, "node LDS and the wait flag inside the ring (the Q fragments stay)");
   __shared__ __attribute__((aligned(16))) char lds[LB];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = blockIdx.x, rb = blockIdx.y, q = blockIdx.z;
@@ -1706,8 +1749,8 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   // batch) is loaded while the group partial is being stored.
   const bool pf = A.NN > 0 && A.NN <= LY::RES * kChunk && r0 < rend;
   NodePre<D> pre;
-  prompt_block<D, kRT, true>(A, lds, g, rb, q, [&] {
-    if (pf) node_prefetch<D>(A, g, r0, rend0, (lds_char*)lds, w, pre);
+  prompt_block<D, kRT, true, false, true>(A, lds, g, rb, q, [&] {
+    if (pf) node_prefetch<D>(A, g, r0, rend0, (lds_char*)lds, w, pre, (const lds_char*)lds + PL::RINGBYTES, rb * 32 * kRT);
   });
   count_partial(A, g, rb, q);
   block_tail<D, kRT>(A, lds, g, rb, q, pre, pf, old);
