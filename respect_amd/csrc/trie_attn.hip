@@ -338,9 +338,10 @@ struct PromptLds {
 // agent-scope atomic stores (write-through) for a merge inside the same launch.
 // KEEP_Q: the combine's (m, l) go past the Q fragments (PromptLds::MLBYTES more
 // LDS), which stay in place for the hook and after it.
-template <int D, int kRT, bool ATOMIC, bool EARLY_STORES = false, bool KEEP_Q = false, class Hook>
+// after_loop runs once every wave is past its last step, before the combine.
+template <int D, int kRT, bool ATOMIC, bool EARLY_STORES = false, bool KEEP_Q = false, class Hook, class Hook0>
 __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, int g, int rb, int q,
-                                             const Hook& before_stores) {
+                                             const Hook& before_stores, const Hook0& after_loop) {
   using G = StepGeom<D>;
   using L = PromptLds<D, kRT>;
   constexpr int DQ = G::DQ, DT = G::DT;
@@ -563,6 +564,7 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
     }
   }
 
+  after_loop();
   // Quarter partials combined in one step (the ring and the Q area are free
   // once every wave is past its last step).  Each wave writes (m, l) of its
   // rows, then scales its accumulators by s_k = exp2(m_k - M), M the row's
@@ -634,24 +636,24 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
     const f32x4 a3 = *(const lds_f32x4*)(src + 3 * BR * D);
     sv[jj] = (a0 + a1) + (a2 + a3);
   }
-  if (has_rows && k == 0 && g4 == 0) {
+  const __amdgpu_buffer_rsrc_t racc = buffer_rsrc(A.gp_acc, 0x7fffffff);
+  auto store_partial = [&] {
+    if (has_rows && k == 0 && g4 == 0) {
 #pragma unroll
-    for (int t = 0; t < kRT; ++t) {
-      const int r = trow + 16 * t + n16;
-      if (r < A.R) {
-        float* ml = A.gp_ml + (((size_t)g * A.R + r) * A.NG + q) * 2;
-        if constexpr (ATOMIC) {
-          __hip_atomic_store(ml, Mr[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(ml + 1, Lr[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-          ml[0] = Mr[t];
-          ml[1] = Lr[t];
+      for (int t = 0; t < kRT; ++t) {
+        const int r = trow + 16 * t + n16;
+        if (r < A.R) {
+          float* ml = A.gp_ml + (((size_t)g * A.R + r) * A.NG + q) * 2;
+          if constexpr (ATOMIC) {
+            __hip_atomic_store(ml, Mr[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(ml + 1, Lr[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          } else {
+            ml[0] = Mr[t];
+            ml[1] = Lr[t];
+          }
         }
       }
     }
-  }
-  const __amdgpu_buffer_rsrc_t racc = buffer_rsrc(A.gp_acc, 0x7fffffff);
-  auto store_partial = [&] {
 #pragma unroll
     for (int jj = 0; jj < NSW; ++jj) {
       const int r = row0 + (w + kWavesA * jj) * RPI + lane / (D / 4);
@@ -679,7 +681,7 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
 template <int D, int kRT>
 __global__ __launch_bounds__(512) void prompt_kernel(TrieAttnArgs A) {
   __shared__ __attribute__((aligned(16))) char lds[PromptLds<D, kRT>::BYTES];
-  prompt_block<D, kRT, false, true>(A, lds, blockIdx.x, blockIdx.y, blockIdx.z, [] {});
+  prompt_block<D, kRT, false, true>(A, lds, blockIdx.x, blockIdx.y, blockIdx.z, [] {}, [] {});
 }
 
 // ------------------------------------------------------------------ node partials and merge
@@ -820,8 +822,15 @@ __device__ __forceinline__ uint32_t pre_masks(const TrieAttnArgs& A, int nrd, in
 // multiple of the swizzle's 8-row period), so each wave computes its first K
 // and V offsets once and steps them: straight-line issue, no per-piece
 // divisions.
-template <int D>
-__device__ __forceinline__ void node_issue(const TrieAttnArgs& A, int g, int c0, lds_char* kv, int b, int w) {
+// Pieces of node_issue per wave.
+template <int D> constexpr int node_pieces() {
+  constexpr int KX = NodeLds<D>::CB / 1024;
+  return KX % kWavesA == 0 ? 2 * KX / kWavesA : 1;
+}
+
+// f(j, rsrc, byte offset, LDS offset from kv) for piece j of this wave.
+template <int D, class F>
+__device__ __forceinline__ void node_each_piece(const TrieAttnArgs& A, int g, int c0, int b, int w, const F& f) {
   using LY = NodeLds<D>;
   constexpr int DQ = D / 32, RB = 2 * D;
   constexpr int KX = LY::CB / 1024;        // K pieces (and V pieces) of a chunk
@@ -844,13 +853,37 @@ __device__ __forceinline__ void node_issue(const TrieAttnArgs& A, int g, int c0,
   if constexpr (KX % kWavesA == 0) {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      if (j < KX / kWavesA) bdma16(rk, koff + j * kstep, LY::kbuf(kv, b) + (w + kWavesA * j) * 1024);
-      else bdma16(rv, voff + (j - KX / kWavesA) * vstep, LY::vbuf(kv, b) + (w + kWavesA * (j - KX / kWavesA)) * 1024);
+      if (j < KX / kWavesA) f(j, rk, koff + j * kstep, LY::KOFF + b * LY::CB + (w + kWavesA * j) * 1024);
+      else f(j, rv, voff + (j - KX / kWavesA) * vstep, LY::VOFF + b * LY::CB + (w + kWavesA * (j - KX / kWavesA)) * 1024);
     }
   } else {
     const bool isk = w < KX;
-    bdma16(isk ? rk : rv, isk ? koff : voff, isk ? LY::kbuf(kv, b) + w * 1024 : LY::vbuf(kv, b) + y0 * 1024);
+    f(0, isk ? rk : rv, isk ? koff : voff, isk ? LY::KOFF + b * LY::CB + w * 1024 : LY::VOFF + b * LY::CB + y0 * 1024);
   }
+}
+
+template <int D>
+__device__ __forceinline__ void node_issue(const TrieAttnArgs& A, int g, int c0, lds_char* kv, int b, int w) {
+  node_each_piece<D>(A, g, c0, b, w, [&](int, __amdgpu_buffer_rsrc_t r, int off, int lo) { bdma16(r, off, kv + lo); });
+}
+
+// node_issue's pieces of chunk c0 into registers (lane i: the 16 bytes its
+// direct-to-LDS load would have written at the piece's LDS offset + 16 i), and
+// their LDS stores into buffer b: the loads can then be in flight while the
+// LDS is still in other use, with no LDS-DMA fence on the LDS accesses between.
+template <int D>
+__device__ __forceinline__ void node_load(const TrieAttnArgs& A, int g, int c0, u32x4 (&pc)[node_pieces<D>()], int w) {
+  node_each_piece<D>(A, g, c0, 0, w, [&](int j, __amdgpu_buffer_rsrc_t r, int off, int) {
+    pc[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  });
+}
+template <int D>
+__device__ __forceinline__ void node_put(const TrieAttnArgs& A, int g, int c0, lds_char* kv, int b,
+                                         const u32x4 (&pc)[node_pieces<D>()], int w) {
+  const int lane = __lane_id();
+  node_each_piece<D>(A, g, c0, b, w, [&](int j, __amdgpu_buffer_rsrc_t, int, int lo) {
+    *(lds_u32x4*)(kv + lo + 16 * lane) = pc[j];
+  });
 }
 
 // Score fragment of the rows starting at p0: lane (n16, g4) holds head_dim
@@ -1399,12 +1432,11 @@ __device__ __forceinline__ const lds_float* node_rows(const TrieAttnArgs& A, int
 // p0 < rend): chunk c into buffer c, the mask bytes and the score fragment.
 // qreg (not null): the score fragment from prompt_block's Q fragments in LDS
 // (KEEP_Q), rows from row0, instead of from memory.
+// The mask bytes of node_prefetch.
 template <int D>
-__device__ __forceinline__ void node_prefetch(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv, int w,
-                                              NodePre<D>& pre, const lds_char* qreg = nullptr, int row0 = 0) {
+__device__ __forceinline__ void node_prefetch_masks(const TrieAttnArgs& A, int p0, int rend, int w, NodePre<D>& pre) {
   constexpr int nw = kWavesA;
   const int nrd = (rend - p0 - w + nw - 1) / nw;
-  for (int b = 0; b < NodeLds<D>::RES && b * kChunk < A.NN; ++b) node_issue<D>(A, g, b * kChunk, kv, b, w);
   // Mask byte of round i, chunk c: row p0 + w + 8 i (p0 past the wave's rows),
   // slot c kChunk + lane clamped into [0, NN); node_rows zeroes what is out of range.
   auto raw = [&](int c, int i) -> uint32_t {
@@ -1422,6 +1454,13 @@ __device__ __forceinline__ void node_prefetch(const TrieAttnArgs& A, int g, int 
     pre.m20 = raw(2, 0);
     pre.m21 = raw(2, 1);
   }
+}
+
+template <int D>
+__device__ __forceinline__ void node_prefetch(const TrieAttnArgs& A, int g, int p0, int rend, lds_char* kv, int w,
+                                              NodePre<D>& pre, const lds_char* qreg = nullptr, int row0 = 0) {
+  for (int b = 0; b < NodeLds<D>::RES && b * kChunk < A.NN; ++b) node_issue<D>(A, g, b * kChunk, kv, b, w);
+  node_prefetch_masks<D>(A, p0, rend, w, pre);
   if (qreg) node_q_lds<D>(qreg, row0, p0, rend, pre.qf);
   else node_q<D>(A, g, p0, rend, pre.qf);
 }
@@ -1746,12 +1785,37 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
   const int old = counter_before(A, g, rb);
 
   // A resident node segment (K/V, score fragment, mask bytes of the first
-  // batch) is loaded while the group partial is being stored.
+  // batch) is loaded while the group partial is being stored.  Up to
+  // D = 128 the first chunk's K/V and the mask bytes are requested into
+  // registers before the quarter combine (whose LDS traffic they then
+  // overlap) and written into the ring after it.
   const bool pf = A.NN > 0 && A.NN <= LY::RES * kChunk && r0 < rend;
+  constexpr bool kEarly = D <= 128;
   NodePre<D> pre;
-  prompt_block<D, kRT, true, false, true>(A, lds, g, rb, q, [&] {
-    if (pf) node_prefetch<D>(A, g, r0, rend0, (lds_char*)lds, w, pre, (const lds_char*)lds + PL::RINGBYTES, rb * 32 * kRT);
-  });
+  u32x4 pc[node_pieces<D>()];
+  const lds_char* qreg = (const lds_char*)lds + PL::RINGBYTES;
+  prompt_block<D, kRT, true, false, true>(
+      A, lds, g, rb, q,
+      [&] {
+        if constexpr (kEarly) {
+          // Unconditional, so that no path leaves the register loads pending
+          // (without a prefetch the node phase overwrites these bytes).
+          node_put<D>(A, g, 0, (lds_char*)lds, 0, pc, w);
+          if (!pf) return;
+          for (int b = 1; b < LY::RES && b * kChunk < A.NN; ++b) node_issue<D>(A, g, b * kChunk, (lds_char*)lds, b, w);
+          node_q_lds<D>(qreg, rb * 32 * kRT, r0, rend0, pre.qf);
+        } else {
+          if (pf) node_prefetch<D>(A, g, r0, rend0, (lds_char*)lds, w, pre, qreg, rb * 32 * kRT);
+        }
+      },
+      [&] {
+        if constexpr (kEarly) {
+          if (pf) {
+            node_load<D>(A, g, 0, pc, w);
+            node_prefetch_masks<D>(A, r0, rend0, w, pre);
+          }
+        }
+      });
   count_partial(A, g, rb, q);
   block_tail<D, kRT>(A, lds, g, rb, q, pre, pf, old);
 }
@@ -1779,7 +1843,7 @@ __global__ __launch_bounds__(512) void fused2_kernel(TrieAttnArgs A) {
   for (int b = 0; b < 2; ++b) {
     if (b < nb) {
       const int rb = rbw + NRBW * b;
-      prompt_block<D, kRT, true, true>(A, lds, g, rb, q, [] {});
+      prompt_block<D, kRT, true, true>(A, lds, g, rb, q, [] {}, [] {});
       count_partial(A, g, rb, q);
     }
   }
