@@ -1830,26 +1830,69 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
 template <int D, int kRT>
 __global__ __launch_bounds__(512) void fused2_kernel(TrieAttnArgs A) {
   using LY = NodeLds<D>;
+  using PL = PromptLds<D, kRT>;
   constexpr int NB = node_area_bytes<D>() + 16;
-  constexpr int LB = PromptLds<D, kRT>::BYTES > NB ? PromptLds<D, kRT>::BYTES : NB;
+  constexpr int LB = PL::BYTES + PL::MLBYTES > NB ? PL::BYTES + PL::MLBYTES : NB;
+  static_assert(NB <= PL::RINGBYTES, "node LDS and the wait flag inside the ring (the Q fragments stay)");
   __shared__ __attribute__((aligned(16))) char lds[LB];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = blockIdx.x, rbw = blockIdx.y, q = blockIdx.z;
   // Every argument the prologue needs, requested in one batch.
   asm volatile("" ::"s"(A.q), "s"(A.kp), "s"(A.vp), "s"(A.sync), "s"(A.sqh), "s"(A.sqm), "s"(A.skph), "s"(A.skpn),
                "s"(A.svph), "s"(A.svpn), "s"(A.P), "s"(A.NRB), "s"(A.NG), "s"(A.S), "s"(A.R), "s"(A.GQS));
   const int NRBW = (A.NRB + 1) / 2;
   const int nb = rbw + NRBW < A.NRB ? 2 : 1;
-  const int old[2] = {counter_before(A, g, rbw), counter_before(A, g, nb > 1 ? rbw + NRBW : rbw)};
-  for (int b = 0; b < 2; ++b) {
-    if (b < nb) {
-      const int rb = rbw + NRBW * b;
-      prompt_block<D, kRT, true, true>(A, lds, g, rb, q, [] {}, [] {});
-      count_partial(A, g, rb, q);
-    }
+  const int rb1 = nb > 1 ? rbw + NRBW : rbw;
+  const int old[2] = {counter_before(A, g, rbw), counter_before(A, g, rb1)};
+  // With two blocks and a resident node segment (up to D = 128), the node
+  // data both tails share is requested during the second block's prompt
+  // part: the first chunk's K/V into registers before its quarter combine
+  // (written into the ring after it, further chunks as direct-to-LDS loads),
+  // with both blocks' mask bytes and the first block's score fragment; the
+  // second block's score fragment comes from its Q fragments in LDS.  The node
+  // phases leave the K/V chunks in place, so the second tail reuses them.
+  constexpr bool kEarly = D <= 128;
+  int r0[2], rend[2], rend0[2];
+  merge_share<kRT>(A, rbw, q, r0[0], rend[0]);
+  merge_share<kRT>(A, rb1, q, r0[1], rend[1]);
+  rend0[0] = min(rend[0], r0[0] + kNodeRows);
+  rend0[1] = min(rend[1], r0[1] + kNodeRows);
+  const bool seg = kEarly && nb > 1 && A.NN > 0 && A.NN <= LY::RES * kChunk;
+  const bool pf0 = seg && r0[0] < rend[0], pf1 = seg && r0[1] < rend[1];
+  NodePre<D> pre0, pre1;
+  u32x4 pc[node_pieces<D>()];
+  const lds_char* qreg = (const lds_char*)lds + PL::RINGBYTES;
+  prompt_block<D, kRT, true, true>(A, lds, g, rbw, q, [] {}, [] {});
+  count_partial(A, g, rbw, q);
+  if (nb > 1) {
+    prompt_block<D, kRT, true, false, true>(
+        A, lds, g, rb1, q,
+        [&] {
+          if constexpr (kEarly) {
+            // Unconditional, so that no path leaves the register loads pending.
+            node_put<D>(A, g, 0, (lds_char*)lds, 0, pc, w);
+            if (!seg) return;
+            for (int b = 1; b < LY::RES && b * kChunk < A.NN; ++b) node_issue<D>(A, g, b * kChunk, (lds_char*)lds, b, w);
+          }
+        },
+        [&] {
+          if constexpr (kEarly) {
+            if (seg) {
+              node_load<D>(A, g, 0, pc, w);
+              if (pf0) {
+                node_prefetch_masks<D>(A, r0[0], rend0[0], w, pre0);
+                node_q<D>(A, g, r0[0], rend0[0], pre0.qf);
+              }
+              if (pf1) node_prefetch_masks<D>(A, r0[1], rend0[1], w, pre1);
+            }
+          }
+        });
+    count_partial(A, g, rb1, q);
+    if constexpr (kEarly)
+      if (pf1) node_q_lds<D>(qreg, rb1 * 32 * kRT, r0[1], rend0[1], pre1.qf);
   }
-  NodePre<D> none;
-  for (int b = 0; b < 2; ++b)
-    if (b < nb) block_tail<D, kRT>(A, lds, g, rbw + NRBW * b, q, none, false, old[b]);
+  block_tail<D, kRT>(A, lds, g, rbw, q, pre0, pf0, old[0]);
+  if (nb > 1) block_tail<D, kRT>(A, lds, g, rb1, q, pre1, pf1, old[1]);
 }
 
 // ------------------------------------------------------------------ host side
