@@ -338,10 +338,14 @@ struct PromptLds {
 // agent-scope atomic stores (write-through) for a merge inside the same launch.
 // KEEP_Q: the combine's (m, l) go past the Q fragments (PromptLds::MLBYTES more
 // LDS), which stay in place for the hook and after it.
-// after_loop runs once every wave is past its last step, before the combine.
-template <int D, int kRT, bool ATOMIC, bool EARLY_STORES = false, bool KEEP_Q = false, class Hook, class Hook0>
+// after_loop runs once every wave is past its last step, before the combine;
+// first_round once every wave's round 0 (and every memory operation the
+// workgroup issued before it) is complete.
+template <int D, int kRT, bool ATOMIC, bool EARLY_STORES = false, bool KEEP_Q = false, class Hook, class Hook0,
+          class Hook1>
 __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, int g, int rb, int q,
-                                             const Hook& before_stores, const Hook0& after_loop) {
+                                             const Hook& before_stores, const Hook0& after_loop,
+                                             const Hook1& first_round) {
   using G = StepGeom<D>;
   using L = PromptLds<D, kRT>;
   constexpr int DQ = G::DQ, DT = G::DT;
@@ -446,9 +450,11 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
     // Own chunks of round r (and the Q chunks, issued first) have landed.
     wait_rounds<G::OWN, G::RING>(r == 0 ? 0 : min(nr - 1 - r, G::RING - 1));
     lds_barrier();   // every wave's chunks of round r are in LDS
-    if (r == 0)
+    if (r == 0) {
+      first_round();
       for (int rr = 1; rr < min(nr, G::RING); ++rr)
         issue_round<D>(rk, rv, kstep, vstep, kQuarters * rr, voff, ring + rr * G::ROUND, w);
+    }
     if (r < 3) RSPX_MARK(1 + 2 * r);
     if (r == 0 && has_rows) {
 #pragma unroll
@@ -681,7 +687,7 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
 template <int D, int kRT>
 __global__ __launch_bounds__(512) void prompt_kernel(TrieAttnArgs A) {
   __shared__ __attribute__((aligned(16))) char lds[PromptLds<D, kRT>::BYTES];
-  prompt_block<D, kRT, false, true>(A, lds, blockIdx.x, blockIdx.y, blockIdx.z, [] {}, [] {});
+  prompt_block<D, kRT, false, true>(A, lds, blockIdx.x, blockIdx.y, blockIdx.z, [] {}, [] {}, [] {});
 }
 
 // ------------------------------------------------------------------ node partials and merge
@@ -1739,6 +1745,17 @@ __device__ __forceinline__ void block_tail(const TrieAttnArgs& A, char* lds, int
   RSPX_MARK(15);
 }
 
+// Adds workgroup q's share of kCountUnit to row block rb's counter, from the
+// last wave (waves 0-3 score the node slots next, and a wave with the add in
+// flight would wait for it at its first vmcnt wait).  Every wave's stores of
+// the group partial must be complete (each wave's vmcnt(0), then a barrier).
+__device__ __forceinline__ void count_add(const TrieAttnArgs& A, int g, int rb, int q) {
+  if (threadIdx.x == 64 * (kWavesA - 1)) {
+    const int share = (int)kCountUnit / A.NG + (q < (int)kCountUnit % A.NG ? 1 : 0);
+    __hip_atomic_fetch_add(A.sync + 1 + 2 * (g * A.NRB + rb), share, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // The group partial is complete in memory (each wave waited for its own
 // stores): add workgroup q's share of kCountUnit to the row block's counter.
 __device__ __forceinline__ void count_partial(const TrieAttnArgs& A, int g, int rb, int q) {
@@ -1746,12 +1763,7 @@ __device__ __forceinline__ void count_partial(const TrieAttnArgs& A, int g, int 
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are complete
   lds_barrier();
   RSPX_MARK(11);
-  // The add from the last wave: waves 0-3 score the node slots next, and a
-  // wave with the add in flight would wait for it at its first vmcnt wait.
-  if (threadIdx.x == 64 * (kWavesA - 1)) {
-    const int share = (int)kCountUnit / A.NG + (q < (int)kCountUnit % A.NG ? 1 : 0);
-    __hip_atomic_fetch_add(A.sync + 1 + 2 * (g * A.NRB + rb), share, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  count_add(A, g, rb, q);
 }
 
 // The row block's counter as this workgroup finds it before adding its own
@@ -1815,7 +1827,8 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
             node_prefetch_masks<D>(A, r0, rend0, w, pre);
           }
         }
-      });
+      },
+      [] {});
   count_partial(A, g, rb, q);
   block_tail<D, kRT>(A, lds, g, rb, q, pre, pf, old);
 }
@@ -1862,8 +1875,11 @@ __global__ __launch_bounds__(512) void fused2_kernel(TrieAttnArgs A) {
   NodePre<D> pre0, pre1;
   u32x4 pc[node_pieces<D>()];
   const lds_char* qreg = (const lds_char*)lds + PL::RINGBYTES;
-  prompt_block<D, kRT, true, true>(A, lds, g, rbw, q, [] {}, [] {});
-  count_partial(A, g, rbw, q);
+  prompt_block<D, kRT, true, true>(A, lds, g, rbw, q, [] {}, [] {}, [] {});
+  // With a second block the first block's count waits for nothing: it is added
+  // once the second block's round 0 has landed, by when the first block's
+  // stores (issued before that round's loads) are complete in every wave.
+  if (nb == 1) count_partial(A, g, rbw, q);
   if (nb > 1) {
     prompt_block<D, kRT, true, false, true>(
         A, lds, g, rb1, q,
@@ -1886,7 +1902,8 @@ __global__ __launch_bounds__(512) void fused2_kernel(TrieAttnArgs A) {
               if (pf1) node_prefetch_masks<D>(A, r0[1], rend0[1], w, pre1);
             }
           }
-        });
+        },
+        [&] { count_add(A, g, rbw, q); });
     count_partial(A, g, rb1, q);
     if constexpr (kEarly)
       if (pf1) node_q_lds<D>(qreg, rb1 * 32 * kRT, r0[1], rend0[1], pre1.qf);
