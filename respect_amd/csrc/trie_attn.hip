@@ -671,9 +671,11 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
     }
   };
   // EARLY_STORES (callers with no hook): the stores go out before the
-  // barrier (128-node tries at 8B heads: 33.1 -> 32.7 us).  With a node
-  // prefetch in the hook, the prefetch goes first so that its data lands
-  // while the stores drain.
+  // barrier (128-node tries at 8B heads: 33.1 -> 32.7 us).  A hook that
+  // writes node data into the ring goes first: issued after the stores, the
+  // compiler's wait for the registers it writes from would also wait for
+  // the stores' write-through, and further chunks' loads land while the
+  // stores drain.
   if constexpr (EARLY_STORES) store_partial();
   // Every wave's ring reads are complete: `before_stores` may issue
   // direct-to-LDS loads into the ring.
