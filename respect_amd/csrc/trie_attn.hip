@@ -1690,21 +1690,19 @@ __device__ __forceinline__ void merge_share(const TrieAttnArgs& A, int rb, int q
 }
 
 // After workgroup (g, rb, q) has counted its group partial of row block rb:
-// the node partials of its merge rows in batches of at most kNodeRows (the
-// first batch while the block's other workgroups finish, then the bounded
-// wait), then the merge.  pre / pf: node_rows' first batch.  old: the
-// counter before this workgroup's share (counter_before), so the block is
-// complete once the counter has moved kCountUnit past the multiple of
-// kCountUnit below it.
+// the node partials of its merge rows [r0, rend) of that block in batches of
+// at most kNodeRows (the first batch while the block's other workgroups
+// finish, then the bounded wait), then the merge.  pre / pf: node_rows'
+// first batch.  old: the counter before this workgroup's share
+// (counter_before), so the block is complete once the counter has moved
+// kCountUnit past the multiple of kCountUnit below it.
 template <int D, int kRT>
-__device__ __forceinline__ void block_tail(const TrieAttnArgs& A, char* lds, int g, int rb, int q,
+__device__ __forceinline__ void block_tail(const TrieAttnArgs& A, char* lds, int g, int rb, int q, int r0, int rend,
                                            const NodePre<D>& pre, bool pf, int old) {
   using LY = NodeLds<D>;
   const int lane = __lane_id();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int* cnt = A.sync + 1 + 2 * (g * A.NRB + rb);
-  int r0, rend;
-  merge_share<kRT>(A, rb, q, r0, rend);
   const int rend0 = min(rend, r0 + kNodeRows);
   int* gave_up = reinterpret_cast<int*>(lds + node_area_bytes<D>());  // one LDS word past the node areas
   if (r0 < rend) {
@@ -1832,16 +1830,17 @@ __global__ __launch_bounds__(512) void fused_kernel(TrieAttnArgs A) {
       },
       [] {});
   count_partial(A, g, rb, q);
-  block_tail<D, kRT>(A, lds, g, rb, q, pre, pf, old);
+  block_tail<D, kRT>(A, lds, g, rb, q, r0, rend, pre, pf, old);
 }
 
 // The same work as fused_kernel for grids twice as large as the device holds
 // at once (e.g. 128-node tries at 8B heads: 512 rows per kv head): workgroup
 // (g, rbw, q) runs the prompt groups of row blocks rbw and rbw + NRBW
 // (NRBW = ceil(NRB / 2)) one after the other, counting each, then the node
-// partials and merges of both.  Every count precedes every wait, so the waits
-// end as in fused_kernel; the arithmetic of every row is the same: the same
-// bits.
+// partials and merges of its merge rows (its shares of both blocks, or with
+// NG = 2, 4 or 8 twice a share of one block).  Every count precedes every
+// wait, so the waits end as in fused_kernel; the arithmetic of every row is
+// the same: the same bits.
 template <int D, int kRT>
 __global__ __launch_bounds__(512) void fused2_kernel(TrieAttnArgs A) {
   using LY = NodeLds<D>;
@@ -1859,22 +1858,30 @@ __global__ __launch_bounds__(512) void fused2_kernel(TrieAttnArgs A) {
   const int nb = rbw + NRBW < A.NRB ? 2 : 1;
   const int rb1 = nb > 1 ? rbw + NRBW : rbw;
   const int old[2] = {counter_before(A, g, rbw), counter_before(A, g, rb1)};
-  // With two blocks and a resident node segment (up to D = 128), the node
-  // data both tails share is requested during the second block's prompt
-  // part: the first chunk's K/V into registers before its quarter combine
-  // (written into the ring after it, further chunks as direct-to-LDS loads),
-  // with both blocks' mask bytes and the first block's score fragment; the
-  // second block's score fragment comes from its Q fragments in LDS.  The node
-  // phases leave the K/V chunks in place, so the second tail reuses them.
+  // With two blocks and NG = 2, 4 or 8 the merges are split by workgroup, not
+  // by block: workgroup q merges 2 (32 kRT) / NG consecutive rows of one block
+  // (block rbw for q < NG / 2, block rb1 above), so it has one node phase, one
+  // wait and one merge for twice the rows of a block's share.  With a resident
+  // node segment (up to D = 128) its node data is requested during the second
+  // block's prompt part: the first chunk's K/V into registers before that
+  // block's quarter combine (written into the ring after it, further chunks as
+  // direct-to-LDS loads) with the rows' mask bytes, and the score fragment from
+  // memory (rows of block rbw) or from the second block's Q fragments, kept in
+  // LDS (rows of block rb1).
   constexpr bool kEarly = D <= 128;
-  int r0[2], rend[2], rend0[2];
-  merge_share<kRT>(A, rbw, q, r0[0], rend[0]);
-  merge_share<kRT>(A, rb1, q, r0[1], rend[1]);
-  rend0[0] = min(rend[0], r0[0] + kNodeRows);
-  rend0[1] = min(rend[1], r0[1] + kNodeRows);
-  const bool seg = kEarly && nb > 1 && A.NN > 0 && A.NN <= LY::RES * kChunk;
-  const bool pf0 = seg && r0[0] < rend[0], pf1 = seg && r0[1] < rend[1];
-  NodePre<D> pre0, pre1;
+  const int rows_blk = 32 * kRT;
+  const bool pairs = nb > 1 && (A.NG == 2 || A.NG == 4 || A.NG == 8);
+  const bool second = pairs && q >= (A.NG >> 1);
+  const int mrb = second ? rb1 : rbw;            // the block whose rows this workgroup merges (pairs)
+  int m0 = 0, mend = 0;
+  if (pairs) {
+    const int rpw2 = 2 * rows_blk / A.NG;        // 16 .. 64 rows, a multiple of 4 dividing the block
+    m0 = mrb * rows_blk + (second ? q - (A.NG >> 1) : q) * rpw2;
+    mend = min(m0 + rpw2, A.R);
+  }
+  const int mend0 = min(mend, m0 + kNodeRows);
+  const bool pf = kEarly && pairs && A.NN > 0 && A.NN <= LY::RES * kChunk && m0 < mend;
+  NodePre<D> pre;
   u32x4 pc[node_pieces<D>()];
   const lds_char* qreg = (const lds_char*)lds + PL::RINGBYTES;
   prompt_block<D, kRT, true, true>(A, lds, g, rbw, q, [] {}, [] {}, [] {});
@@ -1889,29 +1896,36 @@ __global__ __launch_bounds__(512) void fused2_kernel(TrieAttnArgs A) {
           if constexpr (kEarly) {
             // Unconditional, so that no path leaves the register loads pending.
             node_put<D>(A, g, 0, (lds_char*)lds, 0, pc, w);
-            if (!seg) return;
+            if (!pf) return;
             for (int b = 1; b < LY::RES && b * kChunk < A.NN; ++b) node_issue<D>(A, g, b * kChunk, (lds_char*)lds, b, w);
           }
         },
         [&] {
           if constexpr (kEarly) {
-            if (seg) {
+            if (pf) {
               node_load<D>(A, g, 0, pc, w);
-              if (pf0) {
-                node_prefetch_masks<D>(A, r0[0], rend0[0], w, pre0);
-                node_q<D>(A, g, r0[0], rend0[0], pre0.qf);
-              }
-              if (pf1) node_prefetch_masks<D>(A, r0[1], rend0[1], w, pre1);
+              node_prefetch_masks<D>(A, m0, mend0, w, pre);
+              if (!second) node_q<D>(A, g, m0, mend0, pre.qf);
             }
           }
         },
         [&] { count_add(A, g, rbw, q); });
     count_partial(A, g, rb1, q);
     if constexpr (kEarly)
-      if (pf1) node_q_lds<D>(qreg, rb1 * 32 * kRT, r0[1], rend0[1], pre1.qf);
+      if (pf && second) node_q_lds<D>(qreg, rb1 * rows_blk, m0, mend0, pre.qf);
   }
-  block_tail<D, kRT>(A, lds, g, rbw, q, pre0, pf0, old[0]);
-  if (nb > 1) block_tail<D, kRT>(A, lds, g, rb1, q, pre1, pf1, old[1]);
+  if (pairs) {
+    block_tail<D, kRT>(A, lds, g, mrb, q, m0, mend, pre, pf, second ? old[1] : old[0]);
+  } else {
+    NodePre<D> none;
+    int r0, rend;
+    merge_share<kRT>(A, rbw, q, r0, rend);
+    block_tail<D, kRT>(A, lds, g, rbw, q, r0, rend, none, false, old[0]);
+    if (nb > 1) {
+      merge_share<kRT>(A, rb1, q, r0, rend);
+      block_tail<D, kRT>(A, lds, g, rb1, q, r0, rend, none, false, old[1]);
+    }
+  }
 }
 
 // ------------------------------------------------------------------ host side
