@@ -348,7 +348,7 @@ def _status(case, ws):
 
 
 @pytest.mark.parametrize("which", ["cfg1", "cfg2", "base37", "base100", "n64b40", "long", "gqa2", "d64",
-                                   "d64b90", "n128b70", "n72", "n100b30"])
+                                   "d64b90", "n128b70", "n72", "n100b30", "n192p512", "n256p512", "n512p256"])
 def test_one_and_two_launches_equal(which):
     """The one-kernel path (prompt groups, node partials and merge with workgroups
     waiting on per-row-block counters) and the two-kernel path give the same
@@ -357,7 +357,10 @@ def test_one_and_two_launches_equal(which):
     65-128 slots in the node segment (two chunks, loaded whole by both paths); long /
     n128b70 have 512 rows per kv head, two row blocks per workgroup in one launch;
     n72 / n100b30 (288 / 400 rows, 5 / 7 row blocks) leave the last workgroups of
-    that launch a single block."""
+    that launch a single block.  n192p512 / n256p512 / n512p256 take the two-block
+    launch with 4 / 4 / 2 key groups, where each workgroup merges 2 x 64 / NG
+    consecutive rows of one block (a resident, a V-resident and a streamed node
+    segment; 32 and 64 merge rows need two and four node batches)."""
     from respect_amd import _lib
     c = {"cfg1": gen.cfg1, "cfg2": gen.cfg2, "base37": lambda: gen.cfg2(seed=4, base=37),
          "base100": lambda: gen.cfg2(seed=4, base=100),
@@ -370,7 +373,10 @@ def test_one_and_two_launches_equal(which):
                                           base=70),
          "n72": lambda: gen.attn_case(14, 32, 8, 128, 3072, 4, 24, 0, 16, 72, kv_scale=128 ** -0.5),
          "n100b30": lambda: gen.attn_case(13, 32, 8, 128, 3072, 6, 24, 0, 16, 100, kv_scale=128 ** -0.5,
-                                          base=30)}[which]()
+                                          base=30),
+         "n192p512": lambda: gen.attn_case(16, 32, 8, 128, 512, 12, 16, 0, 0, 192, kv_scale=128 ** -0.5),
+         "n256p512": lambda: gen.attn_case(17, 32, 8, 128, 512, 16, 16, 0, 0, 256, kv_scale=128 ** -0.5),
+         "n512p256": lambda: gen.attn_case(18, 32, 8, 128, 256, 16, 32, 0, 0, 512, kv_scale=128 ** -0.5)}[which]()
     print(f"[one/two launches] {which} NN={c.kn.shape[1]}", flush=True)
     H, M, D = c.q.shape
     HK, P, _ = c.kp.shape
