@@ -651,8 +651,10 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
         if (r < A.R) {
           float* ml = A.gp_ml + (((size_t)g * A.R + r) * A.NG + q) * 2;
           if constexpr (ATOMIC) {
-            __hip_atomic_store(ml, Mr[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(ml + 1, Lr[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // One 8-byte store with the coherence of an agent-scope atomic store
+            // (sc1), instead of two 4-byte atomic stores.
+            __builtin_amdgcn_raw_buffer_store_b64(f32x2{Mr[t], Lr[t]}, buffer_rsrc(A.gp_ml, 0x7fffffff),
+                                                  (int)((((size_t)g * A.R + r) * A.NG + q) * 8), 0, 16);
           } else {
             ml[0] = Mr[t];
             ml[1] = Lr[t];
