@@ -684,9 +684,9 @@ def bench_copy(args) -> dict:
 
 
 PHASES = ("round 0 landed", "round 0 computed", "round 1 landed", "round 1 computed", "round 2 landed",
-          "round 2 computed", "quarter (m, l) exchanged", "scaled quarters written", "quarter sums stored",
-          "node data issued", "partial stored and counted", "node partials", "counter wait", "merge",
-          "merge rows stored (end)")
+          "round 2 computed", "node loads issued, quarter (m, l) exchanged", "scaled quarters written",
+          "quarter sums read", "node chunk into LDS", "partial stored and counted", "node partials",
+          "counter wait", "merge", "merge rows stored (end)")
 
 
 def phase_trace(args) -> int:

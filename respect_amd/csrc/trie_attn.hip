@@ -109,10 +109,10 @@ __device__ __forceinline__ int wg_index(const TrieAttnArgs& A, int g, int rb, in
 // records the device's real-time counter (s_memrealtime, 100 MHz) at mark k
 // of the one-launch kernel into g_phase[(b 8 + w) kPhaseMarks + k], read back
 // with rspx_trie_attn_phase_trace.  Marks: 0 start; 1 + 2 r / 2 + 2 r round
-// r (r < 3) landed / computed; 7 quarter (m, l) exchanged; 8 scaled quarters
-// written; 9 quarter sums and (m, l) stores done; 10 node data issued; 11
-// group partial stored and counted; 12 node partials done; 13 wait over; 14
-// merged; 15 end.
+// r (r < 3) landed / computed; 7 node loads issued and quarter (m, l)
+// exchanged; 8 scaled quarters written; 9 quarter sums read; 10 node chunk
+// written into LDS (the hook); 11 group partial stored and counted; 12 node
+// partials done; 13 wait over; 14 merged; 15 end.
 constexpr int kPhaseMarks = 16;
 constexpr int kPhaseWgs = 1024;
 // Dispatch-order index of workgroup (g, rb, q) of the one-launch grid
