@@ -12,7 +12,10 @@ Each workgroup (g, rb, q) of a row block of NG workgroups:
      its rows become NaN and the status word is set);
   3. merges, reading the NG partials of its block.
 Counters are never reset.  fused2_kernel runs step 1 for both of its row
-blocks before any step 2.
+blocks before any step 2 (the first block's add comes once the second block's
+first loads have landed); with NG = 2, 4 or 8 each of its workgroups then
+runs steps 2-3 for one of the two blocks only (workgroups q < NG / 2 the
+first), otherwise for both.
 
 The scheduler holds at most `slots` workgroups resident (dispatch in
 workgroup order, a slot freed when a workgroup ends) and interleaves the
@@ -53,12 +56,21 @@ def run(cnt, NRB, NG, slots, two=False, deadline=200, seed=0):
     events = {"gave_up": 0, "merged": 0}
 
     def program(wg):
-        olds = [cnt[rb] for rb in wg["blocks"]]      # counter_before, at the kernel's start
-        for rb in wg["blocks"]:                      # prompt groups, then counts
-            yield
-            stored[rb].add(wg["q"])                  # partial complete (vmcnt 0, barrier)
-            cnt[rb] += share(wg["q"], NG)            # count_partial
-        for rb, old in zip(wg["blocks"], olds):      # block_tail
+        blocks = wg["blocks"]
+        olds = [cnt[rb] for rb in blocks]            # counter_before, at the kernel's start
+        if len(blocks) == 1:
+            yield                                    # prompt groups
+            stored[blocks[0]].add(wg["q"])           # partial complete (vmcnt 0, barrier)
+            cnt[blocks[0]] += share(wg["q"], NG)     # count_partial
+        else:
+            yield                                    # first block's prompt groups
+            stored[blocks[0]].add(wg["q"])           # its stores issued ...
+            yield                                    # ... second block's round 0 landed (vmcnt 0)
+            cnt[blocks[0]] += share(wg["q"], NG)     # first block's count
+            yield                                    # rest of the second block
+            stored[blocks[1]].add(wg["q"])
+            cnt[blocks[1]] += share(wg["q"], NG)     # count_partial
+        for rb, old in merge_plan(wg, olds):         # block_tail
             base = old - old % UNIT
             polls = 0
             while True:
@@ -74,6 +86,14 @@ def run(cnt, NRB, NG, slots, two=False, deadline=200, seed=0):
                 events["gave_up"] += 1
             yield
 
+    def merge_plan(wg, olds):
+        blocks = wg["blocks"]
+        if len(blocks) == 2 and NG in (2, 4, 8):     # one block's rows per workgroup
+            i = 0 if wg["q"] < NG // 2 else 1
+            return [(blocks[i], olds[i])]
+        return list(zip(blocks, olds))
+
+    events["expected"] = sum(len(merge_plan(wg, [0, 0])) for wg in wgs)
     pending = list(wgs)
     resident = []
     while pending or resident:
@@ -93,14 +113,15 @@ def n_wgs(NRB, NG, two):
 
 
 @pytest.mark.parametrize("NRB,NG,two", [(1, 8, False), (2, 8, False), (4, 8, False), (4, 8, True), (3, 6, True),
-                                        (4, 3, False), (2, 5, False), (1, 1, False), (2, 7, True)])
+                                        (4, 3, False), (2, 5, False), (1, 1, False), (2, 7, True), (8, 4, True),
+                                        (5, 2, True), (16, 8, True)])
 def test_resident_grid_never_gives_up(NRB, NG, two):
     """Grids of every NG (the 8B shape: 4 row blocks x 8 groups per kv head) all resident."""
     for seed in range(30):
         cnt = [0] * NRB
         for call in range(3):
             ev = run(cnt, NRB, NG, slots=n_wgs(NRB, NG, two), two=two, seed=seed * 7 + call)
-            assert ev["gave_up"] == 0 and ev["merged"] == NRB * NG
+            assert ev["gave_up"] == 0 and ev["merged"] == ev["expected"]
 
 
 def test_calls_of_different_shapes_share_the_counters():
@@ -115,7 +136,7 @@ def test_calls_of_different_shapes_share_the_counters():
         sub = cnt[:NRB]
         ev = run(sub, NRB, NG, slots=n_wgs(NRB, NG, two), two=two, seed=call)
         cnt[:NRB] = sub
-        assert ev["gave_up"] == 0 and ev["merged"] == NRB * NG
+        assert ev["gave_up"] == 0 and ev["merged"] == ev["expected"]
     assert all(c % UNIT == 0 for c in cnt)
 
 
@@ -128,7 +149,7 @@ def test_partial_residency_drains_by_the_deadline(NRB, NG, two):
     for seed in range(30):
         cnt = [0] * NRB
         ev = run(cnt, NRB, NG, slots=max(1, n_wgs(NRB, NG, two) // 2), two=two, seed=seed)
-        assert ev["gave_up"] + ev["merged"] == NRB * NG
+        assert ev["gave_up"] + ev["merged"] == ev["expected"]
         gave += ev["gave_up"]
         ev = run(cnt, NRB, NG, slots=n_wgs(NRB, NG, two), two=two, seed=seed + 100)
         assert ev["gave_up"] == 0
