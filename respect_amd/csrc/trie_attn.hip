@@ -649,15 +649,15 @@ __device__ __forceinline__ void prompt_block(const TrieAttnArgs& A, char* lds, i
       for (int t = 0; t < kRT; ++t) {
         const int r = trow + 16 * t + n16;
         if (r < A.R) {
-          float* ml = A.gp_ml + (((size_t)g * A.R + r) * A.NG + q) * 2;
+          const size_t mo = ((size_t)g * A.R + r) * A.NG + q;   // (m, l) pair index
           if constexpr (ATOMIC) {
             // One 8-byte store with the coherence of an agent-scope atomic store
             // (sc1), instead of two 4-byte atomic stores.
             __builtin_amdgcn_raw_buffer_store_b64(f32x2{Mr[t], Lr[t]}, buffer_rsrc(A.gp_ml, 0x7fffffff),
-                                                  (int)((((size_t)g * A.R + r) * A.NG + q) * 8), 0, 16);
+                                                  (int)(mo * 8), 0, 16);
           } else {
-            ml[0] = Mr[t];
-            ml[1] = Lr[t];
+            A.gp_ml[2 * mo] = Mr[t];
+            A.gp_ml[2 * mo + 1] = Lr[t];
           }
         }
       }
@@ -1701,7 +1701,6 @@ __device__ __forceinline__ void merge_share(const TrieAttnArgs& A, int rb, int q
 template <int D, int kRT>
 __device__ __forceinline__ void block_tail(const TrieAttnArgs& A, char* lds, int g, int rb, int q, int r0, int rend,
                                            const NodePre<D>& pre, bool pf, int old) {
-  using LY = NodeLds<D>;
   const int lane = __lane_id();
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int* cnt = A.sync + 1 + 2 * (g * A.NRB + rb);
